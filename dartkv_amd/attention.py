@@ -1,0 +1,146 @@
+"""Attention over DartKV caches (reference src/dart/attention.py:1-90).
+
+* ``dense_attention``: eager fp32 attention on dense tensors (a plain
+  reference for tests and the materialized path).
+* ``streamed_dart_attention``: attention over the packed cache without
+  materializing it.  One query token runs the HIP split-K decode kernel;
+  several query tokens dequantize one segment at a time with the HIP
+  dequantize kernels and keep an online softmax on the GPU.
+* ``decode_attention``: the single-token kernel entry used by both
+  ``streamed_dart_attention`` and ``fused_dart_attention``.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .cache import DartKVCache, tail_segment
+
+
+def dense_attention(query: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, *,
+                    scale: Optional[float] = None) -> torch.Tensor:
+    """Eager attention for [B, H, Q/T, D] tensors (reference attention.py:14-29)."""
+    if query.ndim != 4 or keys.ndim != 4 or values.ndim != 4:
+        raise ValueError("query, keys, and values must have shape [B, H, T, D]")
+    if keys.shape != values.shape or query.shape[0] != keys.shape[0] or query.shape[-1] != keys.shape[-1]:
+        raise ValueError("query/key/value batch, head_dim, and key/value shapes must be compatible")
+    factor = scale if scale is not None else 1.0 / math.sqrt(query.shape[-1])
+    logits = torch.matmul(query.float(), keys.float().transpose(-1, -2)) * factor
+    return torch.matmul(torch.softmax(logits, dim=-1), values.float()).to(query.dtype)
+
+
+def _check_query(query: torch.Tensor, cache: DartKVCache):
+    if cache.get_seq_length() == 0 or cache.shape is None:
+        raise ValueError("cache is empty")
+    batch, kv_heads, _, head_dim = cache.shape
+    if query.shape[0] != batch or query.shape[-1] != head_dim:
+        raise ValueError("query batch and head_dim must match the cache")
+    if query.shape[1] % kv_heads:
+        raise ValueError("query heads must be divisible by cache KV heads")
+    return batch, kv_heads, head_dim
+
+
+def default_splits(batch: int, kv_heads: int, n_segments: int) -> int:
+    """Split count that gives the 256-CU device a few thousand workgroups."""
+    target = 4096
+    return max(1, min(n_segments, -(-target // max(1, batch * kv_heads))))
+
+
+def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,
+                     n_splits: Optional[int] = None, out_f32: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Single-token decode over the packed cache with the HIP split-K kernel.
+
+    ``query`` is [B, Hq, 1, D] (or [B, Hq, D]) on the cache's device.  Returns
+    [B, Hq, 1, D] in ``query.dtype``.  If ``out_f32`` ([B, Hq, D] fp32) is
+    given it receives the result before the final cast.
+    """
+    _lib.require_device(query)
+    batch, kv_heads, head_dim = _check_query(query, cache)
+    q3 = query.reshape(query.shape[0], query.shape[1], query.shape[-1]) if query.ndim == 4 else query
+    if q3.stride(-1) != 1:
+        q3 = q3.contiguous()
+    if query.device != cache.device:
+        raise ValueError("query and cache must be on the same device")
+    factor = scale if scale is not None else 1.0 / math.sqrt(head_dim)
+    plan = cache.decode_plan(query.device)
+    tail = tail_segment(cache) if plan.tail_is_pending else _lib.Segment()
+    total = plan.count + (1 if tail.tokens > 0 else 0)
+    splits = n_splits or default_splits(batch, kv_heads, total)
+    splits = max(1, min(splits, max(1, total)))
+    Hq = q3.shape[1]
+    out = torch.empty(batch, Hq, 1, head_dim, dtype=query.dtype, device=query.device)
+    lib = _lib.load()
+    ws_bytes = lib.dkv_decode_workspace_bytes(batch, Hq, head_dim, splits)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+    a = _lib.DecodeArgs()
+    a.query = q3.data_ptr()
+    a.q_dtype = _lib.dtype_code(q3.dtype)
+    a.q_sb, a.q_sh = q3.stride(0), q3.stride(1)
+    a.out = out.data_ptr()
+    a.out_sb, a.out_sh = out.stride(0), out.stride(1)
+    if out_f32 is not None:
+        if out_f32.shape != (batch, Hq, head_dim) or out_f32.dtype != torch.float32 or not out_f32.is_contiguous():
+            raise ValueError("out_f32 must be a contiguous float32 [B, Hq, D] tensor")
+        a.out_f32 = out_f32.data_ptr()
+    a.segments = 0 if plan.table is None else plan.table.data_ptr()
+    a.n_segments = plan.count
+    a.tail = tail
+    a.B, a.Hq, a.Hkv, a.D = batch, Hq, kv_heads, head_dim
+    a.cache_dtype = _lib.dtype_code(cache.dtype)
+    meta = cache.config.metadata_dtype
+    a.meta_dtype = _lib.dtype_code(meta)
+    a.scale = float(factor)
+    a.n_splits = splits
+    a.workspace = workspace.data_ptr()
+    a.workspace_bytes = ws_bytes
+    _lib.check(lib.dkv_decode_attention(a, _lib.stream_ptr(query.device)), "dkv_decode_attention")
+    return out
+
+
+def streamed_dart_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None) -> torch.Tensor:
+    """Attend to packed pages without materializing the cache (reference attention.py:32-87).
+
+    GQA maps query head h to KV head h // (Hq / Hkv).
+    """
+    if query.ndim != 4:
+        raise ValueError("query must have shape [B, Hq, Q, D]")
+    if cache.get_seq_length() == 0:
+        raise ValueError("cache is empty")
+    batch, kv_heads, head_dim = _check_query(query, cache)
+    _lib.require_device(query)
+    if query.shape[-2] == 1:
+        return decode_attention(query, cache, scale=scale)
+    return _multi_token_attention(query, cache, scale=scale)
+
+
+def _multi_token_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None) -> torch.Tensor:
+    """Several query tokens: per-segment HIP dequantization + fp32 online softmax on the GPU."""
+    batch, kv_heads, head_dim = cache.shape[0], cache.shape[1], cache.shape[3]
+    Hq = query.shape[1]
+    groups = Hq // kv_heads
+    factor = scale if scale is not None else 1.0 / math.sqrt(head_dim)
+    q = query.float().reshape(batch, kv_heads, groups, query.shape[-2], head_dim)
+    m = torch.full(q.shape[:-1], -torch.inf, dtype=torch.float32, device=query.device)
+    l = torch.zeros_like(m)
+    acc = torch.zeros_like(q)
+    for kseg, vseg in cache.iter_segments():
+        keys = kseg if isinstance(kseg, torch.Tensor) else kseg.dequantize()
+        values = vseg if isinstance(vseg, torch.Tensor) else vseg.dequantize()
+        keys = keys.float().unsqueeze(2).contiguous()      # [B, Hkv, 1, T, D]
+        values = values.float().unsqueeze(2).contiguous()
+        logits = torch.matmul(q, keys.transpose(-1, -2).contiguous()) * factor
+        new_m = torch.maximum(m, logits.amax(dim=-1))
+        old_w = torch.exp(m - new_m)
+        w = torch.exp(logits - new_m.unsqueeze(-1))
+        acc = acc * old_w.unsqueeze(-1) + torch.matmul(w, values)
+        l = l * old_w + w.sum(dim=-1)
+        m = new_m
+    out = acc / l.clamp_min(1e-20).unsqueeze(-1)
+    return out.reshape(batch, Hq, query.shape[-2], head_dim).to(query.dtype)
+
+
+__all__ = ["dense_attention", "streamed_dart_attention", "decode_attention"]

@@ -1,0 +1,254 @@
+// Single-token GQA decode attention over packed DartKV segments (gfx950).
+//
+// Split-K over segments: workgroup (split, kv_head, batch) streams its
+// contiguous range of segments, keeps an online-softmax state (max, sum,
+// acc[D]) for each of the query heads that share the KV head, and writes the
+// partial state to the workspace.  A merge pass combines the splits with the
+// log-sum-exp rule and applies the reference's final normalisation
+// `acc / max(sum, 1e-20)` (reference src/dart/attention.py:86,
+// src/dart/fused_attention.py:742).
+//
+// K/V elements are dequantized with the reference's rounding chain
+// (code*scale and +zero rounded in the metadata dtype, then the cache dtype),
+// so the values attended to are exactly those the reference's streamed
+// attention sees (attention.py:74-77).
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "dkv_capi_util.h"
+#include "dkv_device.h"
+
+using namespace dkv;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxGroup = 16;   // query heads per KV head
+constexpr int kMaxDim = 512;    // head_dim
+constexpr int kChanPerThread = kMaxDim / kThreads;
+
+struct DecodeParams {
+  dkv_decode_args a;
+  int group;        // query heads per KV head
+  int n_total;      // segments including the tail
+};
+
+__device__ __forceinline__ float key_value(const dkv_segment& s, int64_t bh, int c, int t, int D, const int32_t* inv,
+                                           int cache_dt, int meta) {
+  if (s.key_kind == DKV_KEY_DENSE) {
+    return dev_load((const void*)s.key[0], bh * s.key_bh[0] + (int64_t)t * D + c, cache_dt);
+  }
+  const int kg = s.key_group;
+  const int G = (s.tokens + kg - 1) / kg;
+  const int g = t / kg;
+  uint32_t code;
+  if (s.key_kind == DKV_KEY_UNIFORM) {
+    const int per_byte = 8 / s.key_bits;
+    const int pk = (G * kg + per_byte - 1) / per_byte;
+    const uint8_t byte = ((const uint8_t*)s.key[0])[bh * s.key_bh[0] + (int64_t)c * pk + t / per_byte];
+    code = (byte >> ((t % per_byte) * s.key_bits)) & ((1u << s.key_bits) - 1u);
+  } else {
+    const int nb = (kg + 3) / 4;
+    const int w = t % kg;
+    const uint8_t lo = ((const uint8_t*)s.key[0])[bh * s.key_bh[0] + ((int64_t)c * G + g) * nb + w / 4];
+    code = (lo >> ((w % 4) * 2)) & 3u;
+    const int slot = inv[c];
+    if (slot >= 0) {
+      const uint8_t hi = ((const uint8_t*)s.key[1])[bh * s.key_bh[1] + ((int64_t)slot * G + g) * nb + w / 4];
+      code |= ((hi >> ((w % 4) * 2)) & 3u) << 2;
+    }
+  }
+  const int64_t mi = (int64_t)c * G + g;
+  return dev_dequant(code, dev_load_meta((const void*)s.key[3], bh * s.key_bh[3] + mi, meta),
+                     dev_load_meta((const void*)s.key[4], bh * s.key_bh[4] + mi, meta), meta, cache_dt);
+}
+
+__device__ __forceinline__ float value_value(const dkv_segment& s, int64_t bh, int t, int c, int D, int cache_dt,
+                                             int meta) {
+  if (s.value_kind == DKV_VALUE_DENSE) {
+    return dev_load((const void*)s.value[0], bh * s.value_bh[0] + (int64_t)t * D + c, cache_dt);
+  }
+  const int vg = s.value_group;
+  const int Gv = (D + vg - 1) / vg;
+  const int per_byte = 8 / s.value_bits;
+  const int pv = (Gv * vg + per_byte - 1) / per_byte;
+  const uint8_t byte = ((const uint8_t*)s.value[0])[bh * s.value_bh[0] + (int64_t)t * pv + c / per_byte];
+  const uint32_t code = (byte >> ((c % per_byte) * s.value_bits)) & ((1u << s.value_bits) - 1u);
+  const int64_t mi = (int64_t)t * Gv + c / vg;
+  return dev_dequant(code, dev_load_meta((const void*)s.value[1], bh * s.value_bh[1] + mi, meta),
+                     dev_load_meta((const void*)s.value[2], bh * s.value_bh[2] + mi, meta), meta, cache_dt);
+}
+
+__global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p) {
+  const dkv_decode_args& a = p.a;
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int D = (int)a.D, G = p.group, Hq = (int)a.Hq;
+  const int cache_dt = (int)a.cache_dtype, meta = (int)a.meta_dtype;
+  const int64_t bh = (int64_t)b * a.Hkv + kvh;
+  const float scale = (float)a.scale;
+
+  __shared__ float q_s[kMaxGroup * kMaxDim];
+  __shared__ float w_s[kMaxGroup * kThreads];
+  __shared__ float red_s[kMaxGroup * (kThreads / 64)];
+  __shared__ int32_t inv_s[kMaxDim];
+
+  for (int i = threadIdx.x; i < G * D; i += kThreads) {
+    const int h = i / D, c = i % D;
+    q_s[i] = dev_load(a.query, (int64_t)b * a.q_sb + (int64_t)(kvh * G + h) * a.q_sh + c, (int)a.q_dtype);
+  }
+
+  float m[kMaxGroup], l[kMaxGroup], acc[kMaxGroup][kChanPerThread];
+  for (int h = 0; h < kMaxGroup; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+    for (int j = 0; j < kChanPerThread; ++j) acc[h][j] = 0.f;
+  }
+
+  const int s0 = (int)(((int64_t)split * p.n_total) / a.n_splits);
+  const int s1 = (int)(((int64_t)(split + 1) * p.n_total) / a.n_splits);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+
+  for (int si = s0; si < s1; ++si) {
+    const dkv_segment seg = si < a.n_segments ? a.segments[si] : a.tail;
+    __syncthreads();
+    if (seg.key_kind == DKV_KEY_MIXED) {
+      for (int c = threadIdx.x; c < D; c += kThreads) inv_s[c] = -1;
+      __syncthreads();
+      const int32_t* idx = (const int32_t*)seg.key[2] + bh * seg.key_bh[2];
+      for (int j = threadIdx.x; j < seg.promoted; j += kThreads) {
+        const int32_t ch = idx[j];
+        if (ch >= 0 && ch < D) inv_s[ch] = j;
+      }
+    }
+    __syncthreads();
+    for (int t0 = 0; t0 < seg.tokens; t0 += kThreads) {
+      const int nt = min(kThreads, seg.tokens - t0);
+      // ---- logits for this tile: thread = token ----
+      float logit[kMaxGroup];
+      for (int h = 0; h < G; ++h) logit[h] = 0.f;
+      if ((int)threadIdx.x < nt) {
+        const int t = t0 + threadIdx.x;
+        for (int c = 0; c < D; ++c) {
+          const float kv = key_value(seg, bh, c, t, D, inv_s, cache_dt, meta);
+          for (int h = 0; h < G; ++h) logit[h] = fmaf(q_s[h * D + c], kv, logit[h]);
+        }
+        for (int h = 0; h < G; ++h) logit[h] = logit[h] * scale;
+      } else {
+        for (int h = 0; h < G; ++h) logit[h] = -INFINITY;
+      }
+      // ---- tile max per head ----
+      for (int h = 0; h < G; ++h) {
+        const float wm = wave_max(logit[h]);
+        if (lane == 0) red_s[h * (kThreads / 64) + wave] = wm;
+      }
+      __syncthreads();
+      float new_m[kMaxGroup], old_w[kMaxGroup];
+      for (int h = 0; h < G; ++h) {
+        float tm = red_s[h * (kThreads / 64)];
+        for (int w = 1; w < kThreads / 64; ++w) tm = fmaxf(tm, red_s[h * (kThreads / 64) + w]);
+        new_m[h] = fmaxf(m[h], tm);
+        old_w[h] = expf(m[h] - new_m[h]);
+      }
+      __syncthreads();
+      for (int h = 0; h < G; ++h) {
+        const float w = (int)threadIdx.x < nt ? expf(logit[h] - new_m[h]) : 0.f;
+        w_s[h * kThreads + threadIdx.x] = w;
+        const float ws = wave_sum(w);
+        if (lane == 0) red_s[h * (kThreads / 64) + wave] = ws;
+      }
+      __syncthreads();
+      for (int h = 0; h < G; ++h) {
+        float ts = 0.f;
+        for (int w = 0; w < kThreads / 64; ++w) ts += red_s[h * (kThreads / 64) + w];
+        l[h] = l[h] * old_w[h] + ts;
+        m[h] = new_m[h];
+      }
+      // ---- weighted values: thread = channel ----
+      for (int j = 0; j < kChanPerThread; ++j) {
+        const int c = threadIdx.x + j * kThreads;
+        if (c >= D) break;
+        float pv[kMaxGroup];
+        for (int h = 0; h < G; ++h) pv[h] = 0.f;
+        for (int t = 0; t < nt; ++t) {
+          const float vv = value_value(seg, bh, t0 + t, c, D, cache_dt, meta);
+          for (int h = 0; h < G; ++h) pv[h] = fmaf(w_s[h * kThreads + t], vv, pv[h]);
+        }
+        for (int h = 0; h < G; ++h) acc[h][j] = acc[h][j] * old_w[h] + pv[h];
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- partial state: ws[(b, hq, split)] = {max, sum, acc[D]} ----
+  float* ws = (float*)a.workspace;
+  for (int h = 0; h < G; ++h) {
+    const int hq = kvh * G + h;
+    float* rec = ws + (((int64_t)b * Hq + hq) * a.n_splits + split) * (D + 2);
+    if (threadIdx.x == 0) {
+      rec[0] = m[h];
+      rec[1] = l[h];
+    }
+    for (int j = 0; j < kChanPerThread; ++j) {
+      const int c = threadIdx.x + j * kThreads;
+      if (c < D) rec[2 + c] = acc[h][j];
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) decode_merge(DecodeParams p) {
+  const dkv_decode_args& a = p.a;
+  const int bq = blockIdx.x;  // b * Hq + hq
+  const int b = bq / (int)a.Hq, hq = bq % (int)a.Hq;
+  const int D = (int)a.D, S = (int)a.n_splits;
+  const float* ws = (const float*)a.workspace + (int64_t)bq * S * (D + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, ws[s * (D + 2)]);
+  float L = 0.f;
+  for (int s = 0; s < S; ++s) {
+    const float ms = ws[s * (D + 2)];
+    if (ms != -INFINITY) L += ws[s * (D + 2) + 1] * expf(ms - M);
+  }
+  const float denom = fmaxf(L, 1e-20f);
+  for (int c = threadIdx.x; c < D; c += kThreads) {
+    float o = 0.f;
+    for (int s = 0; s < S; ++s) {
+      const float ms = ws[s * (D + 2)];
+      if (ms != -INFINITY) o += ws[s * (D + 2) + 2 + c] * expf(ms - M);
+    }
+    o = o / denom;
+    dev_store(a.out, (int64_t)b * a.out_sb + (int64_t)hq * a.out_sh + c, o, (int)a.q_dtype);
+    if (a.out_f32) a.out_f32[(int64_t)bq * D + c] = o;
+  }
+}
+
+}  // namespace
+
+extern "C" int64_t dkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t n_splits) {
+  return B * Hq * n_splits * (D + 2) * (int64_t)sizeof(float);
+}
+
+extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
+  DKV_CHECK(args != nullptr, DKV_ERR_INVALID, "args is NULL");
+  const dkv_decode_args& a = *args;
+  DKV_CHECK(a.B > 0 && a.Hq > 0 && a.Hkv > 0 && a.D > 0, DKV_ERR_INVALID, "bad decode shape");
+  DKV_CHECK(a.Hq % a.Hkv == 0, DKV_ERR_INVALID, "query heads must be divisible by cache KV heads");
+  DKV_CHECK(a.Hq / a.Hkv <= kMaxGroup, DKV_ERR_UNSUPPORTED, "at most %d query heads per KV head", kMaxGroup);
+  DKV_CHECK(a.D <= kMaxDim, DKV_ERR_UNSUPPORTED, "head_dim %lld > %d", (long long)a.D, kMaxDim);
+  DKV_CHECK(a.n_splits >= 1 && a.n_splits <= 65535, DKV_ERR_INVALID, "n_splits out of range");
+  DKV_CHECK(a.n_segments >= 0 && (a.n_segments == 0 || a.segments != nullptr), DKV_ERR_INVALID, "segments missing");
+  DKV_CHECK(a.n_segments + (a.tail.tokens > 0 ? 1 : 0) > 0, DKV_ERR_INVALID, "cache is empty");
+  DKV_CHECK(a.workspace_bytes >= dkv_decode_workspace_bytes(a.B, a.Hq, a.D, a.n_splits), DKV_ERR_INVALID,
+            "workspace too small");
+  DKV_CHECK(a.B <= 65535 && a.Hkv <= 65535, DKV_ERR_UNSUPPORTED, "batch or KV heads too large");
+  DecodeParams p;
+  p.a = a;
+  p.group = (int)(a.Hq / a.Hkv);
+  p.n_total = (int)(a.n_segments + (a.tail.tokens > 0 ? 1 : 0));
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(decode_split_general, dim3((unsigned)a.n_splits, (unsigned)a.Hkv, (unsigned)a.B), dim3(kThreads),
+                     0, s, p);
+  int rc = dkv_check_launch("dkv_decode_attention(split)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(decode_merge, dim3((unsigned)(a.B * a.Hq)), dim3(kThreads), 0, s, p);
+  return dkv_check_launch("dkv_decode_attention(merge)");
+}

@@ -1,0 +1,92 @@
+// Device-side helpers shared by the DartKV HIP kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dkv_numeric.h"
+
+namespace dkv {
+
+// Hardware conversions that give the same results as the software ones in
+// dkv_numeric.h (IEEE round-to-nearest-even, fp16 subnormals preserved).
+__device__ __forceinline__ float dev_round_f16(float x) { return (float)(_Float16)x; }
+
+__device__ __forceinline__ float dev_round_to(float x, int dt) {
+  if (dt == kBF16) return round_bf16(x);
+  if (dt == kF16) return dev_round_f16(x);
+  return x;
+}
+
+__device__ __forceinline__ float dev_load(const void* base, int64_t index, int dt) {
+  if (dt == kBF16) return bf16_to_f32(((const uint16_t*)base)[index]);
+  if (dt == kF16) return (float)(((const _Float16*)base)[index]);
+  return ((const float*)base)[index];
+}
+
+__device__ __forceinline__ void dev_store(void* base, int64_t index, float v, int dt) {
+  if (dt == kBF16) {
+    ((uint16_t*)base)[index] = bf16_bits_rne(v);
+  } else if (dt == kF16) {
+    ((_Float16*)base)[index] = (_Float16)v;
+  } else {
+    ((float*)base)[index] = v;
+  }
+}
+
+__device__ __forceinline__ void dev_store_meta(void* base, int64_t index, float v, int meta) {
+  if (meta == kF16) {
+    ((_Float16*)base)[index] = (_Float16)v;
+  } else if (meta == kBF16) {
+    ((uint16_t*)base)[index] = bf16_bits_rne(v);
+  } else if (meta == kF32) {
+    ((float*)base)[index] = v;
+  } else {
+    ((double*)base)[index] = (double)v;
+  }
+}
+
+__device__ __forceinline__ double dev_load_meta(const void* base, int64_t index, int meta) {
+  if (meta == kF16) return (double)(float)(((const _Float16*)base)[index]);
+  if (meta == kBF16) return (double)bf16_to_f32(((const uint16_t*)base)[index]);
+  if (meta == kF32) return (double)((const float*)base)[index];
+  return ((const double*)base)[index];
+}
+
+// Reference dequantization chain (quantization.py:103-106): meta-dtype
+// multiply, meta-dtype add, cast to the cache dtype; returned as fp32.
+__device__ __forceinline__ float dev_dequant(uint32_t code, double scale, double zero, int meta, int out_dt) {
+  if (meta == kF64) {
+    const double w = __dadd_rn(__dmul_rn((double)code, scale), zero);
+    return dev_round_to((float)w, out_dt);
+  }
+  const float s = (float)scale, z = (float)zero;
+  const float prod = dev_round_to(__fmul_rn((float)code, s), meta);
+  const float sum = dev_round_to(__fadd_rn(prod, z), meta);
+  return dev_round_to(sum, out_dt);
+}
+
+__device__ __forceinline__ float dev_group_scale(float mn, float mx, float qmax, int dt) {
+  float range = dev_round_to(__fsub_rn(mx, mn), dt);
+  const float eps = quant_eps(dt);
+  if (!(range >= eps)) range = eps;
+  return dev_round_to(__fdiv_rn(range, qmax), dt);
+}
+
+__device__ __forceinline__ uint32_t dev_group_code(float x, float mn, float scale, float qmax, int dt) {
+  const float diff = dev_round_to(__fsub_rn(x, mn), dt);
+  float q = __builtin_rintf(dev_round_to(__fdiv_rn(diff, scale), dt));
+  q = q < 0.0f ? 0.0f : q;
+  q = q > qmax ? qmax : q;
+  return (uint32_t)q;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace dkv

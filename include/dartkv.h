@@ -1,0 +1,205 @@
+/*
+ * dartkv.h — C ABI of the MI355X-native DartKV compressed-KV path.
+ *
+ * libdartkv_hip.so exports these functions.  Every pointer is a device pointer
+ * unless stated otherwise.  Every call enqueues work on the given HIP stream
+ * (a hipStream_t passed as void*, NULL = default stream), returns immediately,
+ * and returns DKV_OK (0) or an error code.  On error, dkv_last_error() returns a
+ * thread-local message.  Nothing here allocates device memory: callers pass
+ * outputs and workspace.
+ *
+ * Element types (the *_dtype arguments) use DKV_DTYPE_*.
+ *
+ * Layouts are the reference's tensor layouts (reference src/dart/quantization.py,
+ * src/dart/mixed.py), so a reference-side binding can hand over the storage
+ * of its QuantizedTensor / MixedQuantizedKey fields unchanged.
+ */
+#ifndef DARTKV_H
+#define DARTKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DKV_DTYPE_F32 0
+#define DKV_DTYPE_F16 1
+#define DKV_DTYPE_BF16 2
+#define DKV_DTYPE_F64 3
+
+#define DKV_OK 0
+#define DKV_ERR_INVALID 1     /* bad shape / argument (Python: ValueError)     */
+#define DKV_ERR_UNSUPPORTED 2 /* valid but not implemented here (ValueError)   */
+#define DKV_ERR_DTYPE 3       /* bad element type (Python: TypeError)          */
+#define DKV_ERR_HIP 4         /* HIP runtime failure (Python: RuntimeError)     */
+
+#define DKV_KEY_DENSE 0
+#define DKV_KEY_UNIFORM 1
+#define DKV_KEY_MIXED 2
+#define DKV_VALUE_DENSE 0
+#define DKV_VALUE_UNIFORM 1
+
+#define DKV_SELECT_MAGNITUDE 0
+#define DKV_SELECT_VARIANCE 1
+#define DKV_SELECT_GIVEN 2 /* caller supplies per-head indices ("random" strategy) */
+
+/* Thread-local description of the last error on this thread. */
+const char* dkv_last_error(void);
+
+/* ABI version; bumps when a struct below changes. */
+int dkv_abi_version(void);
+
+/*
+ * Uniform group quantization of `rows` rows of `n` elements each, groups of
+ * `group` consecutive elements, last group padded by repeating the row's last
+ * element.  Element (r, i) of the source is at src[r * row_stride + i * elem_stride].
+ *
+ * Outputs (contiguous): values[rows][packed_bytes] with element i of a row at
+ * byte i / (8/bits), bits [(i % (8/bits)) * bits, ...) (LSB first);
+ * scale[rows][groups], zero[rows][groups] in meta_dtype.
+ *
+ * Replaces reference src/dart/quantization.py:134-204 (`quantize`, after its
+ * movedim to the last axis) and :213-223 (`quantize_axis`); the cache calls it
+ * for value pages (src/dart/cache.py:505-512).
+ */
+int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, int64_t n,
+                      int64_t row_stride, int64_t elem_stride, int bits, int64_t group,
+                      uint8_t* values, void* scale, void* zero, int meta_dtype, void* stream);
+
+/*
+ * Key quantization along tokens for `n_pages` pages of `page_tokens` tokens.
+ * Source keys are [B, H, T, D]; page p covers tokens
+ * [p * page_tokens, (p + 1) * page_tokens) of `src`, element (b, h, t, d) at
+ * src[b*sb + h*sh + t*st + d*sd].
+ *
+ * key_mode DKV_KEY_MIXED (Dart promotion, reference src/dart/mixed.py:166-244,
+ * channel choice :119-163): per page, fields laid out as the reference's
+ *   low   [B][H][D][G][nb]  uint8, nb = ceil(group/4)
+ *   high  [B][H][K][G][nb]  uint8 (upper 2 bits of promoted channels, top-k order)
+ *   idx   [B][H][K]         int32
+ *   scale [B][H][D][G], zero [B][H][D][G] in meta_dtype
+ * with G = ceil(page_tokens / group) and K = `promoted`.  `selection` picks the
+ * channel score (DKV_SELECT_*); DKV_SELECT_GIVEN reads given_idx[H][K].
+ *
+ * key_mode DKV_KEY_UNIFORM (reference src/dart/quantization.py:213-223 with
+ * axis=-2, as src/dart/cache.py:497-502 calls it):
+ *   low   [B][H][D][pk]     uint8 codes of the padded token axis, pk = ceil(G*group / (8/bits))
+ *   scale [B][H][D][G], zero [B][H][D][G]
+ * (high and idx unused).
+ *
+ * Page p's fields start at field + p * field_page_stride (strides in bytes).
+ * Replaces reference src/dart/cache.py:481-503 (`_quantize_key_pages`).
+ */
+typedef struct dkv_key_pages_args {
+  const void* src;
+  int64_t src_dtype;
+  int64_t B, H, D, page_tokens, n_pages;
+  int64_t sb, sh, st, sd; /* element strides of the source */
+  int64_t key_mode, bits, group, promoted, selection;
+  const int32_t* given_idx;
+  int64_t meta_dtype;
+  uint8_t* low;
+  int64_t low_page_stride;
+  uint8_t* high;
+  int64_t high_page_stride;
+  int32_t* idx;
+  int64_t idx_page_stride;
+  void* scale;
+  int64_t scale_page_stride;
+  void* zero;
+  int64_t zero_page_stride;
+} dkv_key_pages_args;
+
+int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stream);
+
+/*
+ * Dequantize `rows` rows produced by dkv_quantize_rows (same layout) into
+ * out[r * out_row_stride + i] (i < n) in out_dtype, with the reference's
+ * rounding chain: out = to_out(meta(meta(code * scale) + zero)).
+ * Replaces reference src/dart/quantization.py:96-109 and the uniform kernels of
+ * src/dart/triton_ops.py:32-110.
+ */
+int dkv_dequantize_rows(const uint8_t* values, const void* scale, const void* zero, int meta_dtype,
+                        int64_t rows, int64_t n, int bits, int64_t group, void* out, int out_dtype,
+                        int64_t out_row_stride, void* stream);
+
+/*
+ * Dequantize mixed keys (layout of dkv_quantize_key_pages, one page of
+ * `tokens` tokens) to out[B][H][tokens][D] in out_dtype.
+ * Replaces reference src/dart/mixed.py:72-94 and src/dart/triton_ops.py:113-201.
+ */
+int dkv_dequantize_mixed(const uint8_t* low, const uint8_t* high, const int32_t* idx, const void* scale,
+                         const void* zero, int meta_dtype, int64_t B, int64_t H, int64_t D, int64_t tokens,
+                         int64_t group, int64_t promoted, void* out, int out_dtype, void* stream);
+
+/*
+ * One cache segment (a page, a dense sink piece, the dense pending tail) as
+ * the decode kernel sees it.  Field addresses are device addresses; *_bh are
+ * strides, in elements of that field, between consecutive (batch, kv-head)
+ * blocks.  Inside a block the layouts are those of dkv_quantize_key_pages /
+ * dkv_quantize_rows, and a dense block is [tokens][D] with row stride D.
+ *   key[0]: dense values | uniform codes | mixed low codes
+ *   key[1]: mixed high codes      key[2]: mixed channel indices (int32)
+ *   key[3]: scale                 key[4]: zero
+ *   value[0]: dense values | codes   value[1]: scale   value[2]: zero
+ */
+typedef struct dkv_segment {
+  int32_t tokens;
+  int32_t key_kind;   /* DKV_KEY_*   */
+  int32_t value_kind; /* DKV_VALUE_* */
+  int32_t key_bits;
+  int32_t key_group;
+  int32_t promoted;
+  int32_t value_bits;
+  int32_t value_group;
+  uint64_t key[5];
+  int64_t key_bh[5];
+  uint64_t value[3];
+  int64_t value_bh[3];
+} dkv_segment;
+
+/*
+ * Single-token GQA decode attention over a packed cache: query [B][Hq][D]
+ * (element (b,h,d) at query[b*q_sb + h*q_sh + d]) attends to every token of
+ * segments[0..n_segments) (device array, in sequence order) and, when
+ * tail.tokens > 0, to `tail` (passed by value, last in sequence).  Query head h
+ * uses KV head h / (Hq/Hkv).  Logits are (q . k) * scale in fp32 with an online
+ * softmax; K and V are dequantized with the reference's rounding chain.
+ *
+ * Work is split over `n_splits` contiguous segment ranges per (batch, kv head);
+ * partial (max, sum, acc[D]) go to `workspace` (dkv_decode_workspace_bytes
+ * bytes) and a merge pass writes out[b][h][d] (out_sb, out_sh strides, q dtype)
+ * and, if out_f32 != NULL, the fp32 result before the final cast to
+ * out_f32[(b*Hq + h)*D + d].
+ *
+ * Replaces reference src/dart/fused_attention.py:654-771
+ * (`fused_dart_attention`, one query token) and, for one query token,
+ * src/dart/attention.py:32-87 (`streamed_dart_attention`).
+ */
+typedef struct dkv_decode_args {
+  const void* query;
+  int64_t q_dtype, q_sb, q_sh;
+  void* out;
+  int64_t out_sb, out_sh;
+  float* out_f32;
+  const dkv_segment* segments;
+  int64_t n_segments;
+  dkv_segment tail;
+  int64_t B, Hq, Hkv, D;
+  int64_t cache_dtype, meta_dtype;
+  double scale;
+  int64_t n_splits;
+  void* workspace;
+  int64_t workspace_bytes;
+} dkv_decode_args;
+
+int64_t dkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t n_splits);
+
+int dkv_decode_attention(const dkv_decode_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DARTKV_H */

@@ -1,0 +1,41 @@
+"""The C-ABI library builds, loads without a GPU and exports every declared symbol (CPU)."""
+
+from __future__ import annotations
+
+import os
+import re
+import subprocess
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "dartkv.h")
+LIB = os.path.join(REPO, "dartkv_amd", "libdartkv_hip.so")
+
+
+def declared_functions() -> set:
+    text = open(HEADER).read()
+    return set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]*?\b(dkv_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    assert {"dkv_quantize_rows", "dkv_quantize_key_pages", "dkv_dequantize_rows", "dkv_dequantize_mixed",
+            "dkv_decode_attention", "dkv_decode_workspace_bytes", "dkv_last_error", "dkv_abi_version"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    assert os.path.exists(LIB), "build the library first: python -m dartkv_amd.build"
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (dkv_\w+)", out))
+    missing = declared_functions() - exported
+    assert not missing, missing
+
+
+def test_library_loads_and_reports_errors_without_gpu():
+    from dartkv_amd import _lib
+    lib = _lib.load()
+    assert lib.dkv_abi_version() == 1
+    # argument validation runs on the host before any launch
+    rc = lib.dkv_quantize_rows(None, 0, 1, 4, 4, 1, 3, 4, None, None, None, 0, None)
+    assert rc == _lib.DKV_ERR_INVALID
+    assert b"bits" in lib.dkv_last_error()
+    assert lib.dkv_decode_workspace_bytes(2, 4, 8, 3) == 2 * 4 * 3 * 10 * 4

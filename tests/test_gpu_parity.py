@@ -1,0 +1,150 @@
+"""HIP kernels vs the reference's golden vectors and the CPU oracle (GPU).
+
+Bar: packed codes, channel indices, scales and zero points bit-exact;
+attention within max|a-b| / max|b| per (batch, head) of 2e-3 for bf16/fp16
+caches and 1e-5 for fp32 caches, on the fp32 output before the final cast.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from tests.golden_util import DTYPES, bits_equal
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _dkv():
+    import dartkv_amd
+    from dartkv_amd import _lib
+    _lib.load()
+    return dartkv_amd
+
+
+def rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
+    """max over (batch, head) of max|a-b| / max|b| on [B, H, ..., D] tensors."""
+    a = actual.detach().float().cpu().flatten(2)
+    b = expected.detach().float().cpu().flatten(2)
+    num = (a - b).abs().amax(dim=-1)
+    den = b.abs().amax(dim=-1).clamp_min(1e-30)
+    return float((num / den).max())
+
+
+def tolerance(dtype: torch.dtype) -> float:
+    return 1e-5 if dtype == torch.float32 else 2e-3
+
+
+def test_uniform_quantize_bit_exact_vs_golden(golden):
+    dart = _dkv()
+    for e in golden.manifest["uniform"]:
+        data = golden.get(e["input"]).to(DEV)
+        print("case", e["tag"], tuple(data.shape), data.dtype, e["bits"], e["group"], e["axis"], flush=True)
+        q = dart.quantize(data, bits=e["bits"], group_size=e["group"], metadata_dtype=DTYPES[e["meta"]], axis=e["axis"])
+        torch.cuda.synchronize()
+        assert golden.matches(e["values"], q.values.cpu()), e["tag"]
+        assert golden.matches(e["scale"], q.scale.cpu()), e["tag"]
+        assert golden.matches(e["zero"], q.zero_point.cpu()), e["tag"]
+        assert golden.matches(e["deq"], q.dequantize().cpu().contiguous()), e["tag"]
+
+
+def test_mixed_key_bit_exact_vs_golden_including_tie_order(golden):
+    dart = _dkv()
+    from tests.test_oracle_golden import _input
+    for e in golden.manifest["mixed"]:
+        keys = _input(golden, e, DTYPES[e["dtype"]]).to(DEV)
+        print("case", e["tag"], tuple(keys.shape), keys.dtype, e["group"], e["ratio"], e["strategy"], flush=True)
+        mk = dart.quantize_key_mixed(keys, group_size=e["group"], promote_ratio=e["ratio"], strategy=e["strategy"],
+                                     metadata_dtype=torch.float16)
+        torch.cuda.synchronize()
+        for field, actual in (("low", mk.low_values), ("high", mk.high_values), ("idx", mk.channel_indices),
+                              ("scale", mk.scale), ("zero", mk.zero_point), ("deq", mk.dequantize())):
+            assert golden.matches(e[field], actual.cpu()), (e["tag"], field)
+
+
+def _config(cfg: dict):
+    import dartkv_amd
+    kw = dict(cfg)
+    if "metadata_dtype" in kw:
+        kw["metadata_dtype"] = DTYPES[kw["metadata_dtype"]]
+    return dartkv_amd.DartKVCacheConfig(**kw)
+
+
+def _seg_fields(seg):
+    if isinstance(seg, torch.Tensor):
+        return {"dense": seg}
+    if hasattr(seg, "low_values"):
+        return {"low": seg.low_values, "high": seg.high_values, "idx": seg.channel_indices,
+                "scale": seg.scale, "zero": seg.zero_point}
+    return {"values": seg.values, "scale": seg.scale, "zero": seg.zero_point}
+
+
+@pytest.mark.parametrize("name", ["c2", "c1", "nonheld", "held_mixed", "kitty_local", "kitty_value_local",
+                                  "uniform_mix_bits"])
+def test_cache_pages_and_decode_vs_golden(golden, name):
+    dart = _dkv()
+    from tests.test_oracle_golden import _lifecycle_inputs
+    e = next(x for x in golden.manifest["cache"] if x["name"] == name)
+    keys, values, query = _lifecycle_inputs(golden, e)
+    print("lifecycle", name, tuple(keys.shape), keys.dtype, e["updates"], flush=True)
+    cache = dart.DartKVCache(_config(e["config"]))
+    start = 0
+    kd, vd = keys.to(DEV), values.to(DEV)
+    for n in e["updates"]:
+        cache.update(kd[..., start:start + n, :], vd[..., start:start + n, :])
+        start += n
+    table = cache.page_table().validate()
+    assert table.sequence_ranges().tolist() == e["ranges"]
+    assert table.key_modes.tolist() == e["key_modes"]
+    assert table.value_modes.tolist() == e["value_modes"]
+    assert cache.storage_bytes == e["storage_bytes"]
+    segs = cache.iter_segments()
+    assert len(segs) == len(e["segments"])
+    for i, ((kseg, vseg), rec) in enumerate(zip(segs, e["segments"])):
+        for side, seg in (("key", kseg), ("value", vseg)):
+            fields = _seg_fields(seg)
+            assert set(fields) == set(rec[side]), (name, i, side)
+            for field, ref in rec[side].items():
+                assert golden.matches(ref, fields[field].cpu().contiguous()), (name, i, side, field)
+    ref32 = golden.get(e["attn_out_f32"])
+    qd = query.to(DEV)
+    if qd.shape[-2] == 1:
+        out32 = torch.empty(qd.shape[0], qd.shape[1], qd.shape[-1], dtype=torch.float32, device=DEV)
+        out = dart.decode_attention(qd, cache, out_f32=out32)
+        torch.cuda.synchronize()
+        err = rel_err(out32.unsqueeze(2), ref32)
+        print("decode rel err", name, err, flush=True)
+        assert err <= tolerance(keys.dtype), (name, err)
+        fused = dart.fused_dart_attention(qd, cache, fallback=False)
+        assert bits_equal(fused.cpu(), out.cpu())
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_config2_decode_vs_oracle(seed, dtype):
+    """Config 2 (B1, T1024, Hkv 8, Hq 32, D 128, page 128, kg 128, vg 64, 2-bit + 25 %, sink 32, held tail)."""
+    dart = _dkv()
+    from oracle import dart_oracle as O
+    from dartkv_amd import synthetic
+    k, v, q = synthetic.outlier_kv(1, 8, 1024, 128, query_heads=32, dtype=dtype, seed=100 + seed)
+    cfg = dict(bits=2, page_size=128, key_group_size=128, value_group_size=64, promote_ratio=0.25, sink_tokens=32,
+               hold_partial_pages=True, metadata_dtype=torch.float16)
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    oc.append(k, v)
+    _, ref32 = O.streamed_attention(q, oc, return_fp32=True)
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    cache.append(k.to(DEV), v.to(DEV))
+    out32 = torch.empty(1, 32, 128, dtype=torch.float32, device=DEV)
+    dart.decode_attention(q.to(DEV), cache, out_f32=out32)
+    torch.cuda.synchronize()
+    err = rel_err(out32.unsqueeze(2), ref32)
+    print("config2", seed, dtype, "rel err", err, flush=True)
+    assert err <= 2e-3
+    # every packed page matches the oracle bit for bit
+    for (ks, vs), (oks, ovs) in zip(cache.iter_segments(), oc.segments()):
+        for a, b in zip(_seg_fields(ks).values(), _seg_fields(oks).values()):
+            assert bits_equal(a.cpu(), b)
+        for a, b in zip(_seg_fields(vs).values(), _seg_fields(ovs).values()):
+            assert bits_equal(a.cpu(), b)
