@@ -1,0 +1,252 @@
+"""Benchmark: packed-KV single-token decode attention on a Qwen3-8B-shaped cache.
+
+Workload: batch 64, 32768-token context per
+sequence, 8 KV heads, 32 query heads, head_dim 128, bf16 K/V with 8 outlier
+channels per KV head, page 128, key group 128, value group 64, 2-bit codes
+with 25 % key-channel promotion, 32 sink tokens, held tail; 36 layers of
+packed cache resident in HBM, each layer a separate cache.
+
+One step = one decode token for all 64 sequences through all 36 layers:
+36 launches of the fused decode attention (split-K + merge).  ``value`` is
+the algorithmic bytes those launches must read and write (packed pages,
+dense sink and tail, query, output) per second.
+
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3]
+
+Prints one JSON line.  Only one GPU is supported (``--gpus`` > 1 exits).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def config_for(bits_mode: str) -> dict:
+    cfg = dict(page_size=128, key_group_size=128, value_group_size=64, sink_tokens=32, hold_partial_pages=True,
+               metadata_dtype=None)
+    if bits_mode == "2b25":
+        cfg.update(bits=2, promote_ratio=0.25)
+    elif bits_mode == "4b":
+        cfg.update(bits=4, promote_ratio=0.0)
+    else:
+        raise ValueError(bits_mode)
+    return cfg
+
+
+def algorithmic_bytes(batch: int, kv_heads: int, q_heads: int, context: int, head_dim: int, cfg: dict,
+                      elem: int = 2, meta_bytes: int = 2) -> int:
+    """Bytes one decode launch must move: packed pages + dense sink/tail + query + output."""
+    page = cfg["page_size"]
+    sink = min(cfg["sink_tokens"], context)
+    pages = (context - sink) // page
+    tail = context - sink - pages * page
+    kg, vg = cfg["key_group_size"], cfg["value_group_size"]
+    if cfg.get("promote_ratio", 0.0) > 0:
+        K = min(head_dim, int(head_dim * cfg["promote_ratio"] + 1e-6))
+        G = (page + kg - 1) // kg
+        nb = (kg + 3) // 4
+        kbytes = head_dim * G * nb + K * G * nb + 4 * K + 2 * head_dim * G * meta_bytes
+    else:
+        per = 8 // cfg["bits"]
+        G = (page + kg - 1) // kg
+        kbytes = head_dim * ((G * kg + per - 1) // per) + 2 * head_dim * G * meta_bytes
+    per = 8 // cfg["bits"]
+    gv = (head_dim + vg - 1) // vg
+    vbytes = page * ((gv * vg + per - 1) // per) + 2 * page * gv * meta_bytes
+    per_bh = pages * (kbytes + vbytes) + (sink + tail) * head_dim * elem * 2
+    return batch * kv_heads * per_bh + 2 * batch * q_heads * head_dim * elem
+
+
+def build_caches(args, torch, dart, synthetic):
+    cfg = config_for(args.bits)
+    cfg["metadata_dtype"] = torch.float16
+    dev = torch.device("cuda:0")
+    log(f"building {args.layers} layer caches: B={args.batch} T={args.context} Hkv={args.kv_heads} D={args.head_dim}")
+    t0 = time.time()
+    keys, values, _ = synthetic.outlier_kv(args.batch, args.kv_heads, args.context, args.head_dim,
+                                           query_heads=args.q_heads, dtype=torch.bfloat16, device=dev)
+    caches = []
+    for layer in range(args.layers):
+        cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+        cache.append(keys, values)
+        caches.append(cache)
+        if layer == 0:
+            torch.cuda.synchronize()
+            log(f"  layer 0 quantized in {time.time() - t0:.2f}s")
+    torch.cuda.synchronize()
+    del keys, values
+    torch.cuda.empty_cache()
+    gen = torch.Generator(device=dev).manual_seed(1)
+    queries = [torch.randn(args.batch, args.q_heads, 1, args.head_dim, generator=gen, device=dev).to(torch.bfloat16)
+               for _ in range(args.layers)]
+    log(f"caches ready in {time.time() - t0:.1f}s; storage {sum(c.storage_bytes for c in caches) / 1e9:.2f} GB")
+    return cfg, caches, queries
+
+
+def cpu_baseline(args, cfg, budget_s: float = 20.0) -> dict:
+    """Oracle (CPU PyTorch restatement of the reference) on a bounded sample of the same workload."""
+    import torch
+
+    from dartkv_amd import synthetic
+    from oracle import dart_oracle as O
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    ocfg = dict(cfg)
+    ocfg["metadata_dtype"] = torch.float16
+    k, v, q = synthetic.outlier_kv(1, args.kv_heads, args.context, args.head_dim, query_heads=args.q_heads,
+                                   dtype=torch.bfloat16)
+    oc = O.OracleCache(O.OracleConfig(**ocfg))
+    oc.append(k, v)
+    bytes_one = algorithmic_bytes(1, args.kv_heads, args.q_heads, args.context, args.head_dim, cfg)
+    O.streamed_attention(q, oc)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.streamed_attention(q, oc)
+        reps += 1
+        if time.perf_counter() - t0 > budget_s or reps >= 50:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    return {"value": round(bytes_one / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle streamed_attention, 1 sequence x 1 layer of the same workload "
+                       f"({args.context} tokens, {bytes_one} algorithmic bytes), {reps} reps, {dt * 1e3:.1f} ms each"),
+            "tok_s": round(1.0 / (dt * args.layers), 4)}
+
+
+def main() -> int:
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--layers", type=int, default=36)
+    p.add_argument("--batch", type=int, default=64)
+    p.add_argument("--context", type=int, default=32768)
+    p.add_argument("--kv-heads", type=int, default=8)
+    p.add_argument("--q-heads", type=int, default=32)
+    p.add_argument("--head-dim", type=int, default=128)
+    p.add_argument("--bits", choices=["2b25", "4b"], default="2b25")
+    p.add_argument("--splits", type=int, default=0, help="split-K count (0 = heuristic)")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    args = p.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the decode path shards by "
+              "(batch, kv-head) with no collective, so per-GPU throughput is the N=1 number.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import dartkv_amd as dart
+    from dartkv_amd import synthetic
+
+    cfg, caches, queries = build_caches(args, torch, dart, synthetic)
+    nbytes = algorithmic_bytes(args.batch, args.kv_heads, args.q_heads, args.context, args.head_dim, cfg)
+    splits = args.splits or None
+    stream = torch.cuda.current_stream()
+
+    def step():
+        for cache, q in zip(caches, queries):
+            dart.decode_attention(q, cache, n_splits=splits)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    n = args.layers * args.steps
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    t_begin = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_begin.record(stream)
+    i = 0
+    for _ in range(args.steps):
+        for cache, q in zip(caches, queries):
+            starts[i].record(stream)
+            dart.decode_attention(q, cache, n_splits=splits)
+            ends[i].record(stream)
+            i += 1
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t_begin.elapsed_time(t_end)
+    launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    avg_launch_ms = sum(launch_ms) / len(launch_ms)
+    ms_per_step = total_ms / args.steps
+    gbs = nbytes * args.layers / (ms_per_step * 1e-3) / 1e9
+    achieved = nbytes / (avg_launch_ms * 1e-3) / 1e9
+    tok_s = args.batch / (ms_per_step * 1e-3)
+
+    # config-2 latency (single layer, B1, T1024): the reference's published shape
+    k2, v2, q2 = synthetic.outlier_kv(1, 8, 1024, 128, query_heads=32, dtype=torch.bfloat16, device="cuda:0")
+    c2cfg = config_for("2b25")
+    c2cfg["metadata_dtype"] = torch.float16
+    c2 = dart.DartKVCache(dart.DartKVCacheConfig(**c2cfg))
+    c2.append(k2, v2)
+    for _ in range(5):
+        dart.decode_attention(q2, c2)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(50):
+        dart.decode_attention(q2, c2)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    c2_us = e0.elapsed_time(e1) / 50 * 1e3
+
+    result = {
+        "metric": "packed-KV decode-attn GB/s (% HBM peak); decode tok/s, Qwen3-8B-shape",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V with 8 x10 outlier key channels per KV head; random bf16 query)",
+        "config": {
+            "workload": (f"C5 long-context decode: batch {args.batch}, {args.context}-token context, "
+                         f"{args.kv_heads} KV / {args.q_heads} query heads, head_dim {args.head_dim}, "
+                         f"{args.layers} layers resident, {'2-bit + 25% key promotion' if args.bits == '2b25' else '4-bit uniform'}, "
+                         "page 128, kg 128, vg 64, sink 32, fp16 metadata"),
+            "batch": args.batch, "context": args.context, "layers": args.layers, "bits": args.bits,
+            "algorithmic_bytes_per_layer": nbytes, "splits": splits or "heuristic",
+        },
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "decode_tok_s": round(tok_s, 2),
+        "c2_latency_us": round(c2_us, 2),
+        "wall_s_timed": round(wall, 3),
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "decode_split_general + decode_merge (one dkv_decode_attention call)",
+            "avg_launch_us": round(avg_launch_ms * 1e3, 2),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle baseline ...")
+        result["cpu_baseline"] = cpu_baseline(args, cfg)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -26,6 +26,8 @@ KEY_DENSE, KEY_UNIFORM, KEY_MIXED = 0, 1, 2
 VALUE_DENSE, VALUE_UNIFORM = 0, 1
 SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 
+ABI_VERSION = 2
+
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
 
@@ -75,6 +77,8 @@ class DecodeArgs(ctypes.Structure):
         ("scale", ctypes.c_double),
         ("n_splits", ctypes.c_int64),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+        ("fast_first", ctypes.c_int64), ("fast_count", ctypes.c_int64), ("fast_promoted", ctypes.c_int64),
+        ("fast_value_group", ctypes.c_int64), ("fast_splits", ctypes.c_int64),
     ]
 
 
@@ -116,7 +120,7 @@ def load() -> ctypes.CDLL:
         for name in ("dkv_quantize_rows", "dkv_quantize_key_pages", "dkv_dequantize_rows", "dkv_dequantize_mixed",
                      "dkv_decode_attention"):
             getattr(lib, name).restype = ctypes.c_int
-        if lib.dkv_abi_version() != 1:
+        if lib.dkv_abi_version() != ABI_VERSION:
             raise RuntimeError("libdartkv_hip.so ABI version mismatch; rebuild it")
         _lib = lib
     return _lib

@@ -13,6 +13,7 @@
 from __future__ import annotations
 
 import math
+import os
 from typing import Optional
 
 import torch
@@ -44,19 +45,26 @@ def _check_query(query: torch.Tensor, cache: DartKVCache):
     return batch, kv_heads, head_dim
 
 
-def default_splits(batch: int, kv_heads: int, n_segments: int) -> int:
-    """Split count that gives the 256-CU device a few thousand workgroups."""
-    target = 4096
+def default_splits(batch: int, kv_heads: int, n_segments: int, target: int = 4096) -> int:
+    """Split count that gives the 256-CU device a few thousand workers."""
     return max(1, min(n_segments, -(-target // max(1, batch * kv_heads))))
 
 
+def _fast_enabled() -> bool:
+    return os.environ.get("DKV_FORCE_GENERAL", "0") in ("", "0")
+
+
 def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,
-                     n_splits: Optional[int] = None, out_f32: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     n_splits: Optional[int] = None, out_f32: Optional[torch.Tensor] = None,
+                     fast: Optional[bool] = None) -> torch.Tensor:
     """Single-token decode over the packed cache with the HIP split-K kernel.
 
     ``query`` is [B, Hq, 1, D] (or [B, Hq, D]) on the cache's device.  Returns
     [B, Hq, 1, D] in ``query.dtype``.  If ``out_f32`` ([B, Hq, D] fp32) is
-    given it receives the result before the final cast.
+    given it receives the result before the final cast.  ``fast`` selects
+    the MFMA page kernel for the pages it supports (default: on unless the
+    environment sets DKV_FORCE_GENERAL=1); ``n_splits`` overrides the split
+    count of the page kernel (or of the general kernel when it does all work).
     """
     _lib.require_device(query)
     batch, kv_heads, head_dim = _check_query(query, cache)
@@ -68,13 +76,22 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     factor = scale if scale is not None else 1.0 / math.sqrt(head_dim)
     plan = cache.decode_plan(query.device)
     tail = tail_segment(cache) if plan.tail_is_pending else _lib.Segment()
-    total = plan.count + (1 if tail.tokens > 0 else 0)
-    splits = n_splits or default_splits(batch, kv_heads, total)
-    splits = max(1, min(splits, max(1, total)))
+    use_fast = (_fast_enabled() if fast is None else fast) and plan.fast_count > 0 \
+        and q3.shape[1] // kv_heads in (1, 2, 4)
+    fast_count = plan.fast_count if use_fast else 0
+    rest = plan.count - fast_count + (1 if tail.tokens > 0 else 0)
+    if fast_count:
+        fast_splits = n_splits or default_splits(batch, kv_heads, fast_count, target=8192)
+        fast_splits = max(1, min(fast_splits, fast_count))
+        splits = max(1, min(rest, 4)) if rest else 0
+    else:
+        fast_splits = 0
+        splits = n_splits or default_splits(batch, kv_heads, rest)
+        splits = max(1, min(splits, max(1, rest)))
     Hq = q3.shape[1]
     out = torch.empty(batch, Hq, 1, head_dim, dtype=query.dtype, device=query.device)
     lib = _lib.load()
-    ws_bytes = lib.dkv_decode_workspace_bytes(batch, Hq, head_dim, splits)
+    ws_bytes = lib.dkv_decode_workspace_bytes(batch, Hq, head_dim, splits + fast_splits)
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
     a = _lib.DecodeArgs()
     a.query = q3.data_ptr()
@@ -97,6 +114,9 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     a.n_splits = splits
     a.workspace = workspace.data_ptr()
     a.workspace_bytes = ws_bytes
+    if fast_count:
+        a.fast_first, a.fast_count = plan.fast_first, fast_count
+        a.fast_promoted, a.fast_value_group, a.fast_splits = plan.fast_promoted, plan.fast_value_group, fast_splits
     _lib.check(lib.dkv_decode_attention(a, _lib.stream_ptr(query.device)), "dkv_decode_attention")
     return out
 

@@ -121,10 +121,16 @@ class DartKVCacheConfig:
 
 
 class _DecodePlan:
-    """Device table of sealed segment descriptors plus the tensors it points into."""
+    """Device table of sealed segment descriptors plus the tensors it points into.
+
+    ``fast_first``/``fast_count`` mark the run of table entries the MFMA page
+    kernel may take (full 128-token Dart pages in its layout); ``fast_promoted``
+    and ``fast_value_group`` are that run's promoted-channel count and value
+    group size.
+    """
 
     def __init__(self, version: int, device: torch.device, table: Optional[torch.Tensor], count: int,
-                 keepalive: list, tail_is_pending: bool, n_tokens: int) -> None:
+                 keepalive: list, tail_is_pending: bool, n_tokens: int, fast: Tuple[int, int, int, int]) -> None:
         self.version = version
         self.device = device
         self.table = table
@@ -132,6 +138,7 @@ class _DecodePlan:
         self.keepalive = keepalive
         self.tail_is_pending = tail_is_pending
         self.n_tokens = n_tokens
+        self.fast_first, self.fast_count, self.fast_promoted, self.fast_value_group = fast
 
 
 class DartKVCache:
@@ -632,7 +639,9 @@ class DartKVCache:
         if sealed:
             raw = torch.frombuffer(bytearray(bytes(descs)), dtype=torch.uint8)
             table = raw.to(device)
-        plan = _DecodePlan(self._sealed_version, device, table, len(sealed), keepalive, tail_is_pending, n_tokens)
+        fast = _fast_run(self, descs, len(sealed))
+        plan = _DecodePlan(self._sealed_version, device, table, len(sealed), keepalive, tail_is_pending, n_tokens,
+                           fast)
         self._decode_plan_cache = plan
         return plan
 
@@ -798,6 +807,47 @@ def _dense_block(t: torch.Tensor, keepalive: list) -> Tuple[int, int]:
     c = t.contiguous()
     keepalive.append(c)
     return c.data_ptr(), T * D
+
+
+def _fast_run(cache: DartKVCache, descs, count: int) -> Tuple[int, int, int, int]:
+    """Longest run of descriptors the MFMA page kernel handles: (first, count, promoted, value group)."""
+    if cache.shape is None or cache.dtype not in (torch.bfloat16, torch.float16):
+        return (0, 0, 0, 0)
+    c = cache.config
+    if (cache.shape[-1] != 128 or c.page_size != 128 or c.metadata_dtype != torch.float16
+            or c.promote_ratio <= 0.0 or c.resolved_key_group_size != 128 or c.resolved_value_bits != 2):
+        return (0, 0, 0, 0)
+    vg = c.resolved_value_group_size
+    K = promoted_count(128, c.promote_ratio)
+    if vg % 8 or 128 % vg or K % 16 or K > 64:
+        return (0, 0, 0, 0)
+
+    def ok(d) -> bool:
+        if not (d.tokens == 128 and d.key_kind == _lib.KEY_MIXED and d.value_kind == _lib.VALUE_UNIFORM
+                and d.promoted == K and d.key_group == 128 and d.value_bits == 2 and d.value_group == vg):
+            return False
+        sizes = (1, 1, 4, 2, 2)
+        for i in range(5):
+            if d.key[i] % 16 or (d.key_bh[i] * sizes[i]) % 16:
+                return False
+        for i, size in enumerate((1, 2, 2)):
+            if d.value[i] % 16 or (d.value_bh[i] * size) % 16:
+                return False
+        return True
+
+    best = (0, 0)
+    i = 0
+    while i < count:
+        if not ok(descs[i]):
+            i += 1
+            continue
+        j = i
+        while j < count and ok(descs[j]):
+            j += 1
+        if j - i > best[1]:
+            best = (i, j - i)
+        i = j
+    return (best[0], best[1], K, vg)
 
 
 def tail_segment(cache: DartKVCache):

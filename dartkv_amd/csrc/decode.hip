@@ -16,6 +16,7 @@
 #include <math.h>
 
 #include "dkv_capi_util.h"
+#include "dkv_decode.h"
 #include "dkv_device.h"
 
 using namespace dkv;
@@ -30,8 +31,21 @@ constexpr int kChanPerThread = kMaxDim / kThreads;
 struct DecodeParams {
   dkv_decode_args a;
   int group;        // query heads per KV head
-  int n_total;      // segments including the tail
+  int n_total;      // segments this kernel walks, including the tail
+  int splits;       // splits of this kernel
+  int split_offset; // first workspace split slot this kernel writes
+  int split_stride; // split slots per (batch, query head) record
+  int skip_first;   // descriptor entries [skip_first, skip_first + skip_count)
+  int skip_count;   // belong to the fast page kernel
 };
+
+// Segment v of the general kernel's sequence: descriptor entries outside the
+// fast range, then the tail.
+__device__ __forceinline__ dkv_segment general_segment(const DecodeParams& p, int v) {
+  const int rest = (int)p.a.n_segments - p.skip_count;
+  if (v >= rest) return p.a.tail;
+  return p.a.segments[v < p.skip_first ? v : v + p.skip_count];
+}
 
 __device__ __forceinline__ float key_value(const dkv_segment& s, int64_t bh, int c, int t, int D, const int32_t* inv,
                                            int cache_dt, int meta) {
@@ -104,12 +118,12 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
     for (int j = 0; j < kChanPerThread; ++j) acc[h][j] = 0.f;
   }
 
-  const int s0 = (int)(((int64_t)split * p.n_total) / a.n_splits);
-  const int s1 = (int)(((int64_t)(split + 1) * p.n_total) / a.n_splits);
+  const int s0 = (int)(((int64_t)split * p.n_total) / p.splits);
+  const int s1 = (int)(((int64_t)(split + 1) * p.n_total) / p.splits);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 
   for (int si = s0; si < s1; ++si) {
-    const dkv_segment seg = si < a.n_segments ? a.segments[si] : a.tail;
+    const dkv_segment seg = general_segment(p, si);
     __syncthreads();
     if (seg.key_kind == DKV_KEY_MIXED) {
       for (int c = threadIdx.x; c < D; c += kThreads) inv_s[c] = -1;
@@ -121,6 +135,8 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
       }
     }
     __syncthreads();
+    const bool dense16 = seg.key_kind == DKV_KEY_DENSE && cache_dt != kF32 && (D % 8) == 0 &&
+                         (seg.key[0] % 16) == 0 && ((seg.key_bh[0] * 2) % 16) == 0;
     for (int t0 = 0; t0 < seg.tokens; t0 += kThreads) {
       const int nt = min(kThreads, seg.tokens - t0);
       // ---- logits for this tile: thread = token ----
@@ -128,9 +144,31 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
       for (int h = 0; h < G; ++h) logit[h] = 0.f;
       if ((int)threadIdx.x < nt) {
         const int t = t0 + threadIdx.x;
-        for (int c = 0; c < D; ++c) {
-          const float kv = key_value(seg, bh, c, t, D, inv_s, cache_dt, meta);
-          for (int h = 0; h < G; ++h) logit[h] = fmaf(q_s[h * D + c], kv, logit[h]);
+        if (dense16) {
+          // dense 16-bit keys: 16-byte loads, 4 in flight, same channel order
+          const uint4* row = (const uint4*)((const uint16_t*)seg.key[0] + bh * seg.key_bh[0] + (int64_t)t * D);
+          for (int c0 = 0; c0 < D; c0 += 32) {
+            uint4 w4[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) w4[u] = (c0 + 8 * u < D) ? row[c0 / 8 + u] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              if (c0 + 8 * u >= D) break;
+              const uint32_t ww[4] = {w4[u].x, w4[u].y, w4[u].z, w4[u].w};
+#pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                const uint16_t bits = (uint16_t)(ww[i / 2] >> (16 * (i % 2)));
+                const float kv = cache_dt == kBF16 ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
+                const int c = c0 + 8 * u + i;
+                for (int h = 0; h < G; ++h) logit[h] = fmaf(q_s[h * D + c], kv, logit[h]);
+              }
+            }
+          }
+        } else {
+          for (int c = 0; c < D; ++c) {
+            const float kv = key_value(seg, bh, c, t, D, inv_s, cache_dt, meta);
+            for (int h = 0; h < G; ++h) logit[h] = fmaf(q_s[h * D + c], kv, logit[h]);
+          }
         }
         for (int h = 0; h < G; ++h) logit[h] = logit[h] * scale;
       } else {
@@ -169,9 +207,30 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
         if (c >= D) break;
         float pv[kMaxGroup];
         for (int h = 0; h < G; ++h) pv[h] = 0.f;
-        for (int t = 0; t < nt; ++t) {
-          const float vv = value_value(seg, bh, t0 + t, c, D, cache_dt, meta);
-          for (int h = 0; h < G; ++h) pv[h] = fmaf(w_s[h * kThreads + t], vv, pv[h]);
+        if (seg.value_kind == DKV_VALUE_DENSE && cache_dt != kF32) {
+          // dense 16-bit values: 8 loads in flight per thread, coalesced across channels
+          const uint16_t* vcol = (const uint16_t*)seg.value[0] + bh * seg.value_bh[0] + (int64_t)t0 * D + c;
+          int t = 0;
+          for (; t + 8 <= nt; t += 8) {
+            uint16_t vb[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vb[i] = vcol[(int64_t)(t + i) * D];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const float vv = cache_dt == kBF16 ? bf16_to_f32(vb[i]) : (float)__builtin_bit_cast(_Float16, vb[i]);
+              for (int h = 0; h < G; ++h) pv[h] = fmaf(w_s[h * kThreads + t + i], vv, pv[h]);
+            }
+          }
+          for (; t < nt; ++t) {
+            const uint16_t vb = vcol[(int64_t)t * D];
+            const float vv = cache_dt == kBF16 ? bf16_to_f32(vb) : (float)__builtin_bit_cast(_Float16, vb);
+            for (int h = 0; h < G; ++h) pv[h] = fmaf(w_s[h * kThreads + t], vv, pv[h]);
+          }
+        } else {
+          for (int t = 0; t < nt; ++t) {
+            const float vv = value_value(seg, bh, t0 + t, c, D, cache_dt, meta);
+            for (int h = 0; h < G; ++h) pv[h] = fmaf(w_s[h * kThreads + t], vv, pv[h]);
+          }
         }
         for (int h = 0; h < G; ++h) acc[h][j] = acc[h][j] * old_w[h] + pv[h];
       }
@@ -183,7 +242,7 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
   float* ws = (float*)a.workspace;
   for (int h = 0; h < G; ++h) {
     const int hq = kvh * G + h;
-    float* rec = ws + (((int64_t)b * Hq + hq) * a.n_splits + split) * (D + 2);
+    float* rec = ws + (((int64_t)b * Hq + hq) * p.split_stride + p.split_offset + split) * (D + 2);
     if (threadIdx.x == 0) {
       rec[0] = m[h];
       rec[1] = l[h];
@@ -195,27 +254,40 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
   }
 }
 
+// One block per (batch, query head): combine the split records with the
+// log-sum-exp rule, then out = acc / max(sum, 1e-20) (attention.py:86).
 __global__ void __launch_bounds__(kThreads) decode_merge(DecodeParams p) {
+  extern __shared__ float wsh[];  // [S] weights, [S] sums
   const dkv_decode_args& a = p.a;
   const int bq = blockIdx.x;  // b * Hq + hq
   const int b = bq / (int)a.Hq, hq = bq % (int)a.Hq;
-  const int D = (int)a.D, S = (int)a.n_splits;
+  const int D = (int)a.D, S = p.split_stride;
   const float* ws = (const float*)a.workspace + (int64_t)bq * S * (D + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, ws[s * (D + 2)]);
-  float L = 0.f;
-  for (int s = 0; s < S; ++s) {
-    const float ms = ws[s * (D + 2)];
-    if (ms != -INFINITY) L += ws[s * (D + 2) + 1] * expf(ms - M);
+  for (int s = threadIdx.x; s < S; s += blockDim.x) {
+    wsh[s] = ws[(int64_t)s * (D + 2)];
+    wsh[S + s] = ws[(int64_t)s * (D + 2) + 1];
   }
+  __syncthreads();
+  float M = -INFINITY;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, wsh[s]);
+  __syncthreads();
+  for (int s = threadIdx.x; s < S; s += blockDim.x) {
+    const float ms = wsh[s];
+    wsh[s] = ms == -INFINITY ? 0.f : expf(ms - M);
+  }
+  __syncthreads();
+  float L = 0.f;
+  for (int s = 0; s < S; ++s) L += wsh[S + s] * wsh[s];
   const float denom = fmaxf(L, 1e-20f);
-  for (int c = threadIdx.x; c < D; c += kThreads) {
-    float o = 0.f;
-    for (int s = 0; s < S; ++s) {
-      const float ms = ws[s * (D + 2)];
-      if (ms != -INFINITY) o += ws[s * (D + 2) + 2 + c] * expf(ms - M);
+  for (int c = threadIdx.x; c < D; c += blockDim.x) {
+    float o0 = 0.f, o1 = 0.f;
+    int s = 0;
+    for (; s + 1 < S; s += 2) {
+      o0 += ws[(int64_t)s * (D + 2) + 2 + c] * wsh[s];
+      o1 += ws[(int64_t)(s + 1) * (D + 2) + 2 + c] * wsh[s + 1];
     }
-    o = o / denom;
+    if (s < S) o0 += ws[(int64_t)s * (D + 2) + 2 + c] * wsh[s];
+    const float o = (o0 + o1) / denom;
     dev_store(a.out, (int64_t)b * a.out_sb + (int64_t)hq * a.out_sh + c, o, (int)a.q_dtype);
     if (a.out_f32) a.out_f32[(int64_t)bq * D + c] = o;
   }
@@ -234,21 +306,58 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
   DKV_CHECK(a.Hq % a.Hkv == 0, DKV_ERR_INVALID, "query heads must be divisible by cache KV heads");
   DKV_CHECK(a.Hq / a.Hkv <= kMaxGroup, DKV_ERR_UNSUPPORTED, "at most %d query heads per KV head", kMaxGroup);
   DKV_CHECK(a.D <= kMaxDim, DKV_ERR_UNSUPPORTED, "head_dim %lld > %d", (long long)a.D, kMaxDim);
-  DKV_CHECK(a.n_splits >= 1 && a.n_splits <= 65535, DKV_ERR_INVALID, "n_splits out of range");
   DKV_CHECK(a.n_segments >= 0 && (a.n_segments == 0 || a.segments != nullptr), DKV_ERR_INVALID, "segments missing");
   DKV_CHECK(a.n_segments + (a.tail.tokens > 0 ? 1 : 0) > 0, DKV_ERR_INVALID, "cache is empty");
-  DKV_CHECK(a.workspace_bytes >= dkv_decode_workspace_bytes(a.B, a.Hq, a.D, a.n_splits), DKV_ERR_INVALID,
-            "workspace too small");
   DKV_CHECK(a.B <= 65535 && a.Hkv <= 65535, DKV_ERR_UNSUPPORTED, "batch or KV heads too large");
+  const int64_t fast_count = a.fast_count;
+  if (fast_count > 0) {
+    DKV_CHECK(a.fast_first >= 0 && a.fast_first + fast_count <= a.n_segments, DKV_ERR_INVALID,
+              "fast page range outside the descriptor table");
+    DKV_CHECK(a.D == 128, DKV_ERR_UNSUPPORTED, "fast page path needs head_dim 128");
+    const int64_t gq = a.Hq / a.Hkv;
+    DKV_CHECK(gq == 1 || gq == 2 || gq == 4, DKV_ERR_UNSUPPORTED, "fast page path needs 1, 2 or 4 query heads per KV head");
+    DKV_CHECK(a.cache_dtype == dkv::kBF16 || a.cache_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED,
+              "fast page path needs a bf16 or fp16 cache");
+    DKV_CHECK(a.meta_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED, "fast page path needs fp16 metadata");
+    DKV_CHECK(a.fast_promoted % 16 == 0 && a.fast_promoted >= 0 && a.fast_promoted <= 64, DKV_ERR_UNSUPPORTED,
+              "fast page path needs a multiple of 16 (at most 64) promoted channels");
+    DKV_CHECK(a.fast_value_group % 8 == 0 && a.fast_value_group > 0 && 128 % a.fast_value_group == 0,
+              DKV_ERR_UNSUPPORTED, "fast page path needs a value group that is a multiple of 8 dividing 128");
+    DKV_CHECK(a.fast_splits >= 1 && a.fast_splits <= fast_count, DKV_ERR_INVALID, "fast_splits out of range");
+    DKV_CHECK(dkv::fast_decode_max_loads((int)a.fast_promoted, (int)(128 / a.fast_value_group)) < 16,
+              DKV_ERR_UNSUPPORTED, "fast page path: value group too small");
+  }
+  const int64_t rest = a.n_segments - (fast_count > 0 ? fast_count : 0) + (a.tail.tokens > 0 ? 1 : 0);
+  const int64_t general_splits = rest > 0 ? a.n_splits : 0;
+  DKV_CHECK(rest == 0 || (a.n_splits >= 1 && a.n_splits <= 65535), DKV_ERR_INVALID, "n_splits out of range");
+  const int64_t fast_splits = fast_count > 0 ? a.fast_splits : 0;
+  const int64_t stride = fast_splits + general_splits;
+  DKV_CHECK(stride <= 8192, DKV_ERR_UNSUPPORTED, "too many splits");
+  DKV_CHECK(a.workspace_bytes >= dkv_decode_workspace_bytes(a.B, a.Hq, a.D, stride), DKV_ERR_INVALID,
+            "workspace too small");
+  hipStream_t s = (hipStream_t)stream;
+  if (fast_count > 0) {
+    int rc = dkv::launch_fast_decode(a, (int)a.fast_first, (int)fast_count, (int)a.fast_promoted,
+                                     (int)a.fast_value_group, (int)fast_splits, (int)stride, s);
+    if (rc) return rc;
+  }
   DecodeParams p;
   p.a = a;
   p.group = (int)(a.Hq / a.Hkv);
-  p.n_total = (int)(a.n_segments + (a.tail.tokens > 0 ? 1 : 0));
-  hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(decode_split_general, dim3((unsigned)a.n_splits, (unsigned)a.Hkv, (unsigned)a.B), dim3(kThreads),
-                     0, s, p);
-  int rc = dkv_check_launch("dkv_decode_attention(split)");
-  if (rc) return rc;
-  hipLaunchKernelGGL(decode_merge, dim3((unsigned)(a.B * a.Hq)), dim3(kThreads), 0, s, p);
+  p.n_total = (int)rest;
+  p.splits = (int)general_splits;
+  p.split_offset = (int)fast_splits;
+  p.split_stride = (int)stride;
+  p.skip_first = fast_count > 0 ? (int)a.fast_first : 0;
+  p.skip_count = fast_count > 0 ? (int)fast_count : 0;
+  if (general_splits > 0) {
+    hipLaunchKernelGGL(decode_split_general, dim3((unsigned)general_splits, (unsigned)a.Hkv, (unsigned)a.B),
+                       dim3(kThreads), 0, s, p);
+    int rc = dkv_check_launch("dkv_decode_attention(split)");
+    if (rc) return rc;
+  }
+  const int merge_threads = (int)(a.D < 64 ? 64 : (a.D > kThreads ? kThreads : ((a.D + 63) / 64) * 64));
+  hipLaunchKernelGGL(decode_merge, dim3((unsigned)(a.B * a.Hq)), dim3(merge_threads),
+                     (size_t)2 * stride * sizeof(float), s, p);
   return dkv_check_launch("dkv_decode_attention(merge)");
 }

@@ -1,0 +1,21 @@
+// Internal interface between the decode entry point and the fast page kernel.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "../../include/dartkv.h"
+
+namespace dkv {
+
+// Loads in flight between a page's value codes and its PV (must be < 16).
+int fast_decode_max_loads(int np, int gv);
+
+// LDS bytes one fast-kernel workgroup needs.
+size_t fast_decode_lds_bytes(int np, int gv);
+
+// Launch the fast kernel over descriptor entries [first, first + count) of
+// a.segments (all full 128-token pages with the fast layout), writing splits
+// [0, splits) of a workspace whose records hold `split_stride` splits.
+int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, int vg, int splits,
+                       int split_stride, hipStream_t stream);
+
+}  // namespace dkv

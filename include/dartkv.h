@@ -167,11 +167,20 @@ typedef struct dkv_segment {
  * uses KV head h / (Hq/Hkv).  Logits are (q . k) * scale in fp32 with an online
  * softmax; K and V are dequantized with the reference's rounding chain.
  *
- * Work is split over `n_splits` contiguous segment ranges per (batch, kv head);
- * partial (max, sum, acc[D]) go to `workspace` (dkv_decode_workspace_bytes
- * bytes) and a merge pass writes out[b][h][d] (out_sb, out_sh strides, q dtype)
- * and, if out_f32 != NULL, the fp32 result before the final cast to
- * out_f32[(b*Hq + h)*D + d].
+ * Work is split over contiguous segment ranges per (batch, kv head); partial
+ * (max, sum, acc[D]) go to `workspace` (dkv_decode_workspace_bytes bytes for
+ * n_splits + fast_splits records) and a merge pass writes out[b][h][d]
+ * (out_sb, out_sh strides, q dtype) and, if out_f32 != NULL, the fp32 result
+ * before the final cast to out_f32[(b*Hq + h)*D + d].
+ *
+ * Fast page path: when fast_count > 0, descriptor entries
+ * [fast_first, fast_first + fast_count) must all be full 128-token pages with
+ * head_dim 128, Dart keys with fast_promoted promoted channels (a multiple of
+ * 16, at most 64, one key group per page), 2-bit values in groups of
+ * fast_value_group channels (a multiple of 8 dividing 128), fp16 metadata and a
+ * bf16 or fp16 cache, every field 16-byte aligned; the caller guarantees this.
+ * Those pages are processed by the MFMA page kernel over `fast_splits` splits;
+ * the other entries and the tail by the general kernel over `n_splits` splits.
  *
  * Replaces reference src/dart/fused_attention.py:654-771
  * (`fused_dart_attention`, one query token) and, for one query token,
@@ -192,6 +201,7 @@ typedef struct dkv_decode_args {
   int64_t n_splits;
   void* workspace;
   int64_t workspace_bytes;
+  int64_t fast_first, fast_count, fast_promoted, fast_value_group, fast_splits;
 } dkv_decode_args;
 
 int64_t dkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t n_splits);

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_library_loads_and_reports_errors_without_gpu():
     from dartkv_amd import _lib
     lib = _lib.load()
-    assert lib.dkv_abi_version() == 1
+    assert lib.dkv_abi_version() == _lib.ABI_VERSION
     # argument validation runs on the host before any launch
     rc = lib.dkv_quantize_rows(None, 0, 1, 4, 4, 1, 3, 4, None, None, None, 0, None)
     assert rc == _lib.DKV_ERR_INVALID

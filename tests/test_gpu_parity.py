@@ -148,3 +148,62 @@ def test_config2_decode_vs_oracle(seed, dtype):
             assert bits_equal(a.cpu(), b)
         for a, b in zip(_seg_fields(vs).values(), _seg_fields(ovs).values()):
             assert bits_equal(a.cpu(), b)
+
+
+def _oracle_and_cache(B, Hkv, Hq, T, dtype, seed, **over):
+    import dartkv_amd as dart
+    from dartkv_amd import synthetic
+    from oracle import dart_oracle as O
+    cfg = dict(bits=2, page_size=128, key_group_size=128, value_group_size=64, promote_ratio=0.25, sink_tokens=32,
+               hold_partial_pages=True, metadata_dtype=torch.float16)
+    cfg.update(over)
+    k, v, q = synthetic.outlier_kv(B, Hkv, T, 128, query_heads=Hq, dtype=dtype, seed=seed)
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    oc.append(k, v)
+    _, ref32 = O.streamed_attention(q, oc, return_fp32=True)
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    cache.append(k.to(DEV), v.to(DEV))
+    return cache, q.to(DEV), ref32
+
+
+@pytest.mark.parametrize("B,Hkv,Hq,T,dtype,vg", [
+    (1, 8, 32, 1024, torch.bfloat16, 64),    # config 2
+    (3, 4, 16, 2000, torch.bfloat16, 64),
+    (2, 2, 4, 1500, torch.float16, 32),      # GQA 2, fp16 cache, value group 32
+    (2, 4, 4, 700, torch.bfloat16, 128),     # GQA 1, value group 128
+])
+def test_fast_page_kernel_vs_oracle_and_general(B, Hkv, Hq, T, dtype, vg):
+    dart = _dkv()
+    cache, q, ref32 = _oracle_and_cache(B, Hkv, Hq, T, dtype, seed=7 + T, value_group_size=vg)
+    plan = cache.decode_plan(q.device)
+    print("case", B, Hkv, Hq, T, dtype, vg, "fast pages", plan.fast_count, "of", plan.count, flush=True)
+    assert plan.fast_count == (T - 32) // 128
+    out_fast = torch.empty(B, Hq, 128, dtype=torch.float32, device=DEV)
+    out_gen = torch.empty_like(out_fast)
+    dart.decode_attention(q, cache, out_f32=out_fast, fast=True)
+    dart.decode_attention(q, cache, out_f32=out_gen, fast=False)
+    torch.cuda.synchronize()
+    e_fast = rel_err(out_fast.unsqueeze(2), ref32)
+    e_gen = rel_err(out_gen.unsqueeze(2), ref32)
+    print("rel err fast", e_fast, "general", e_gen, flush=True)
+    assert e_gen <= 2e-3
+    assert e_fast <= 2e-3
+
+
+def test_fast_page_kernel_split_counts_agree():
+    """Every split count gives the same answer.
+
+    Splits normalise their softmax weights by their own running max before the
+    weights are rounded to fp16 for the PV product, so results differ by that
+    rounding (~1e-4), not by more.
+    """
+    dart = _dkv()
+    cache, q, ref32 = _oracle_and_cache(2, 8, 32, 3000, torch.bfloat16, seed=3)
+    outs = []
+    for splits in (1, 2, 5, 22):
+        o = torch.empty(2, 32, 128, dtype=torch.float32, device=DEV)
+        dart.decode_attention(q, cache, out_f32=o, n_splits=splits, fast=True)
+        outs.append(o.cpu())
+    for o in outs:
+        assert rel_err(o.unsqueeze(2), ref32) <= 2e-3
+        assert rel_err(o.unsqueeze(2), outs[0].unsqueeze(2)) <= 1e-3
