@@ -7,9 +7,11 @@ with 25 % key-channel promotion, 32 sink tokens, held tail; 36 layers of
 packed cache resident in HBM, each layer a separate cache.
 
 One step = one decode token for all 64 sequences through all 36 layers:
-36 launches of the fused decode attention (split-K + merge).  ``value`` is
-the algorithmic bytes those launches must read and write (packed pages,
-dense sink and tail, query, output) per second.
+36 calls of the decode attention (MFMA page kernel, dense sink/tail kernel,
+split merge).  ``value`` is the algorithmic bytes those calls must read and
+write (packed pages, dense sink and tail, query, output) per second of the
+whole step.  ``roofline`` is the page kernel alone: its pages' bytes over its
+mean duration, timed with HIP events recorded around its launch.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3]
 
@@ -48,13 +50,9 @@ def config_for(bits_mode: str) -> dict:
     return cfg
 
 
-def algorithmic_bytes(batch: int, kv_heads: int, q_heads: int, context: int, head_dim: int, cfg: dict,
-                      elem: int = 2, meta_bytes: int = 2) -> int:
-    """Bytes one decode launch must move: packed pages + dense sink/tail + query + output."""
+def page_bytes(head_dim: int, cfg: dict, meta_bytes: int = 2) -> int:
+    """Bytes of one packed page of one (batch, kv head): key and value codes plus metadata."""
     page = cfg["page_size"]
-    sink = min(cfg["sink_tokens"], context)
-    pages = (context - sink) // page
-    tail = context - sink - pages * page
     kg, vg = cfg["key_group_size"], cfg["value_group_size"]
     if cfg.get("promote_ratio", 0.0) > 0:
         K = min(head_dim, int(head_dim * cfg["promote_ratio"] + 1e-6))
@@ -68,8 +66,29 @@ def algorithmic_bytes(batch: int, kv_heads: int, q_heads: int, context: int, hea
     per = 8 // cfg["bits"]
     gv = (head_dim + vg - 1) // vg
     vbytes = page * ((gv * vg + per - 1) // per) + 2 * page * gv * meta_bytes
-    per_bh = pages * (kbytes + vbytes) + (sink + tail) * head_dim * elem * 2
+    return kbytes + vbytes
+
+
+def algorithmic_bytes(batch: int, kv_heads: int, q_heads: int, context: int, head_dim: int, cfg: dict,
+                      elem: int = 2, meta_bytes: int = 2) -> int:
+    """Bytes one decode launch must move: packed pages + dense sink/tail + query + output."""
+    page = cfg["page_size"]
+    sink = min(cfg["sink_tokens"], context)
+    pages = (context - sink) // page
+    tail = context - sink - pages * page
+    per_bh = pages * page_bytes(head_dim, cfg, meta_bytes) + (sink + tail) * head_dim * elem * 2
     return batch * kv_heads * per_bh + 2 * batch * q_heads * head_dim * elem
+
+
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` recorded in profiles/ (PMC FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
+    path = os.path.join(REPO, "profiles", f"{kernel}_{workload}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
 
 
 def build_caches(args, torch, dart, synthetic):
@@ -128,6 +147,25 @@ def cpu_baseline(args, cfg, budget_s: float = 20.0) -> dict:
             "tok_s": round(1.0 / (dt * args.layers), 4)}
 
 
+def config2_latency_us(torch, dart, synthetic, stream) -> float:
+    """Mean time of one decode call on config 2 (B1, T1024, 8/32 heads, 2-bit + 25 %)."""
+    k2, v2, q2 = synthetic.outlier_kv(1, 8, 1024, 128, query_heads=32, dtype=torch.bfloat16, device="cuda:0")
+    c2cfg = config_for("2b25")
+    c2cfg["metadata_dtype"] = torch.float16
+    c2 = dart.DartKVCache(dart.DartKVCacheConfig(**c2cfg))
+    c2.append(k2, v2)
+    for _ in range(5):
+        dart.decode_attention(q2, c2)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(50):
+        dart.decode_attention(q2, c2)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 50 * 1e3
+
+
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -142,6 +180,9 @@ def main() -> int:
     p.add_argument("--bits", choices=["2b25", "4b"], default="2b25")
     p.add_argument("--splits", type=int, default=0, help="split-K count (0 = heuristic)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-c2", action="store_true", help="skip the config-2 latency probe (clean profiles)")
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                   help="after timing, copy a MIB-MiB buffer 3 times (known bytes for PMC counter calibration)")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the decode path shards by "
@@ -165,9 +206,15 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # the page kernel (the dominant kernel) is timed by events the library
+    # records around its launch on the decode stream
+    plan = caches[0].decode_plan(torch.device("cuda:0"))
+    fast_bytes = args.batch * args.kv_heads * plan.fast_count * page_bytes(args.head_dim, cfg)
     n = args.layers * args.steps
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for e0, e1 in events:  # create the handles before they go to the library
+        e0.record(stream)
+        e1.record(stream)
     t_begin = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -176,37 +223,32 @@ def main() -> int:
     i = 0
     for _ in range(args.steps):
         for cache, q in zip(caches, queries):
-            starts[i].record(stream)
-            dart.decode_attention(q, cache, n_splits=splits)
-            ends[i].record(stream)
+            dart.decode_attention(q, cache, n_splits=splits, fast_events=events[i] if plan.fast_count else None)
             i += 1
     t_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_begin.elapsed_time(t_end)
-    launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    avg_launch_ms = sum(launch_ms) / len(launch_ms)
+    kernel_ms = [e0.elapsed_time(e1) for e0, e1 in events] if plan.fast_count else [float("nan")]
+    avg_kernel_ms = sum(kernel_ms) / len(kernel_ms)
     ms_per_step = total_ms / args.steps
     gbs = nbytes * args.layers / (ms_per_step * 1e-3) / 1e9
-    achieved = nbytes / (avg_launch_ms * 1e-3) / 1e9
+    achieved = fast_bytes / (avg_kernel_ms * 1e-3) / 1e9
     tok_s = args.batch / (ms_per_step * 1e-3)
 
+    if args.calibrate_copy:
+        src = torch.empty(args.calibrate_copy << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: 3 x {args.calibrate_copy} MiB read + written")
+        del src, dst
+
     # config-2 latency (single layer, B1, T1024): the reference's published shape
-    k2, v2, q2 = synthetic.outlier_kv(1, 8, 1024, 128, query_heads=32, dtype=torch.bfloat16, device="cuda:0")
-    c2cfg = config_for("2b25")
-    c2cfg["metadata_dtype"] = torch.float16
-    c2 = dart.DartKVCache(dart.DartKVCacheConfig(**c2cfg))
-    c2.append(k2, v2)
-    for _ in range(5):
-        dart.decode_attention(q2, c2)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(50):
-        dart.decode_attention(q2, c2)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    c2_us = e0.elapsed_time(e1) / 50 * 1e3
+    c2_us = None
+    if not args.no_c2:
+        c2_us = config2_latency_us(torch, dart, synthetic, stream)
 
     result = {
         "metric": "packed-KV decode-attn GB/s (% HBM peak); decode tok/s, Qwen3-8B-shape",
@@ -231,13 +273,15 @@ def main() -> int:
         },
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "decode_tok_s": round(tok_s, 2),
-        "c2_latency_us": round(c2_us, 2),
+        "c2_latency_us": None if c2_us is None else round(c2_us, 2),
         "wall_s_timed": round(wall, 3),
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "decode_split_general + decode_merge (one dkv_decode_attention call)",
-            "avg_launch_us": round(avg_launch_ms * 1e3, 2),
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic("decode_pages_fast", "c5") if args.bits == "2b25" else None,
+            "kernel": "decode_pages_fast (MFMA page kernel)",
+            "algorithmic_bytes_per_launch": fast_bytes,
+            "avg_kernel_us": round(avg_kernel_ms * 1e3, 2),
         },
         "cpu_baseline": None,
     }

@@ -26,7 +26,7 @@ KEY_DENSE, KEY_UNIFORM, KEY_MIXED = 0, 1, 2
 VALUE_DENSE, VALUE_UNIFORM = 0, 1
 SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
@@ -79,6 +79,8 @@ class DecodeArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
         ("fast_first", ctypes.c_int64), ("fast_count", ctypes.c_int64), ("fast_promoted", ctypes.c_int64),
         ("fast_value_group", ctypes.c_int64), ("fast_splits", ctypes.c_int64),
+        ("rest_dense_tokens", ctypes.c_int64),
+        ("fast_events", ctypes.c_void_p * 2),
     ]
 
 

@@ -19,7 +19,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from .cache import DartKVCache, tail_segment
+from .cache import DartKVCache, _dense16_ok, tail_segment
 
 
 def dense_attention(query: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, *,
@@ -56,7 +56,7 @@ def _fast_enabled() -> bool:
 
 def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,
                      n_splits: Optional[int] = None, out_f32: Optional[torch.Tensor] = None,
-                     fast: Optional[bool] = None) -> torch.Tensor:
+                     fast: Optional[bool] = None, fast_events=None) -> torch.Tensor:
     """Single-token decode over the packed cache with the HIP split-K kernel.
 
     ``query`` is [B, Hq, 1, D] (or [B, Hq, D]) on the cache's device.  Returns
@@ -65,6 +65,8 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     the MFMA page kernel for the pages it supports (default: on unless the
     environment sets DKV_FORCE_GENERAL=1); ``n_splits`` overrides the split
     count of the page kernel (or of the general kernel when it does all work).
+    ``fast_events`` (two recorded ``torch.cuda.Event`` objects) are recorded
+    again right before and after the page kernel, to time it alone.
     """
     _lib.require_device(query)
     batch, kv_heads, head_dim = _check_query(query, cache)
@@ -76,14 +78,19 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     factor = scale if scale is not None else 1.0 / math.sqrt(head_dim)
     plan = cache.decode_plan(query.device)
     tail = tail_segment(cache) if plan.tail_is_pending else _lib.Segment()
-    use_fast = (_fast_enabled() if fast is None else fast) and plan.fast_count > 0 \
-        and q3.shape[1] // kv_heads in (1, 2, 4)
+    group = q3.shape[1] // kv_heads
+    use_fast = (_fast_enabled() if fast is None else fast) and plan.fast_count > 0 and group in (1, 2, 4)
     fast_count = plan.fast_count if use_fast else 0
     rest = plan.count - fast_count + (1 if tail.tokens > 0 else 0)
+    # the dense kernel takes the non-page segments (sink, tail) when they are
+    # all dense: one record per 32-token chunk of each
+    dense_tokens = 0
+    if use_fast and rest and group <= 8 and plan.rest_dense >= 0 and (tail.tokens == 0 or _dense16_ok(tail)):
+        dense_tokens = max(plan.rest_dense, tail.tokens)
     if fast_count:
         fast_splits = n_splits or default_splits(batch, kv_heads, fast_count, target=8192)
         fast_splits = max(1, min(fast_splits, fast_count))
-        splits = max(1, min(rest, 4)) if rest else 0
+        splits = rest * -(-dense_tokens // 32) if dense_tokens else (max(1, min(rest, 4)) if rest else 0)
     else:
         fast_splits = 0
         splits = n_splits or default_splits(batch, kv_heads, rest)
@@ -117,6 +124,9 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     if fast_count:
         a.fast_first, a.fast_count = plan.fast_first, fast_count
         a.fast_promoted, a.fast_value_group, a.fast_splits = plan.fast_promoted, plan.fast_value_group, fast_splits
+    a.rest_dense_tokens = dense_tokens
+    if fast_events is not None:
+        a.fast_events[0], a.fast_events[1] = fast_events[0].cuda_event, fast_events[1].cuda_event
     _lib.check(lib.dkv_decode_attention(a, _lib.stream_ptr(query.device)), "dkv_decode_attention")
     return out
 

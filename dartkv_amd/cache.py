@@ -126,11 +126,13 @@ class _DecodePlan:
     ``fast_first``/``fast_count`` mark the run of table entries the MFMA page
     kernel may take (full 128-token Dart pages in its layout); ``fast_promoted``
     and ``fast_value_group`` are that run's promoted-channel count and value
-    group size.
+    group size.  ``rest_dense`` is the most tokens of any sealed entry outside
+    that run when the dense decode kernel can read all of them, else -1.
     """
 
     def __init__(self, version: int, device: torch.device, table: Optional[torch.Tensor], count: int,
-                 keepalive: list, tail_is_pending: bool, n_tokens: int, fast: Tuple[int, int, int, int]) -> None:
+                 keepalive: list, tail_is_pending: bool, n_tokens: int, fast: Tuple[int, int, int, int],
+                 rest_dense: int = -1) -> None:
         self.version = version
         self.device = device
         self.table = table
@@ -139,6 +141,7 @@ class _DecodePlan:
         self.tail_is_pending = tail_is_pending
         self.n_tokens = n_tokens
         self.fast_first, self.fast_count, self.fast_promoted, self.fast_value_group = fast
+        self.rest_dense = rest_dense
 
 
 class DartKVCache:
@@ -640,8 +643,9 @@ class DartKVCache:
             raw = torch.frombuffer(bytearray(bytes(descs)), dtype=torch.uint8)
             table = raw.to(device)
         fast = _fast_run(self, descs, len(sealed))
+        rest_dense = _rest_dense(self, descs, len(sealed), fast)
         plan = _DecodePlan(self._sealed_version, device, table, len(sealed), keepalive, tail_is_pending, n_tokens,
-                           fast)
+                           fast, rest_dense)
         self._decode_plan_cache = plan
         return plan
 
@@ -819,7 +823,7 @@ def _fast_run(cache: DartKVCache, descs, count: int) -> Tuple[int, int, int, int
         return (0, 0, 0, 0)
     vg = c.resolved_value_group_size
     K = promoted_count(128, c.promote_ratio)
-    if vg % 8 or 128 % vg or K % 16 or K > 64:
+    if vg % 16 or 128 % vg or K % 16 or K > 64:
         return (0, 0, 0, 0)
 
     def ok(d) -> bool:
@@ -848,6 +852,25 @@ def _fast_run(cache: DartKVCache, descs, count: int) -> Tuple[int, int, int, int
             best = (i, j - i)
         i = j
     return (best[0], best[1], K, vg)
+
+
+def _dense16_ok(d) -> bool:
+    """Dense segment whose K/V rows the dense decode kernel reads with 16-byte loads."""
+    return (d.key_kind == _lib.KEY_DENSE and d.value_kind == _lib.VALUE_DENSE and d.key[0] % 16 == 0
+            and d.value[0] % 16 == 0 and (d.key_bh[0] * 2) % 16 == 0 and (d.value_bh[0] * 2) % 16 == 0)
+
+
+def _rest_dense(cache: DartKVCache, descs, count: int, fast: Tuple[int, int, int, int]) -> int:
+    """Most tokens of any sealed entry outside the fast run when all of them are
+    dense 16-bit with aligned rows and head_dim is 128 (0 if there are none);
+    -1 when the dense decode kernel cannot take them."""
+    if cache.shape is None or cache.dtype not in (torch.bfloat16, torch.float16) or cache.shape[-1] != 128:
+        return -1
+    first, n = fast[0], fast[1]
+    rest = [descs[i] for i in range(count) if not first <= i < first + n]
+    if not all(_dense16_ok(d) for d in rest):
+        return -1
+    return max((d.tokens for d in rest), default=0)
 
 
 def tail_segment(cache: DartKVCache):

@@ -93,6 +93,11 @@ __device__ __forceinline__ float value_value(const dkv_segment& s, int64_t bh, i
                      dev_load_meta((const void*)s.value[2], bh * s.value_bh[2] + mi, meta), meta, cache_dt);
 }
 
+// MG is a compile-time bound on the query heads per KV head, so the per-head
+// state below stays in registers: DKV_FOR_HEAD unrolls over MG heads and skips
+// heads >= G.
+#define DKV_FOR_HEAD(h) _Pragma("unroll") for (int h = 0; h < MG; ++h) if (h < G)
+template <int MG>
 __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p) {
   const dkv_decode_args& a = p.a;
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -111,8 +116,9 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
     q_s[i] = dev_load(a.query, (int64_t)b * a.q_sb + (int64_t)(kvh * G + h) * a.q_sh + c, (int)a.q_dtype);
   }
 
-  float m[kMaxGroup], l[kMaxGroup], acc[kMaxGroup][kChanPerThread];
-  for (int h = 0; h < kMaxGroup; ++h) {
+  float m[MG], l[MG], acc[MG][kChanPerThread];
+#pragma unroll
+  for (int h = 0; h < MG; ++h) {
     m[h] = -INFINITY;
     l[h] = 0.f;
     for (int j = 0; j < kChanPerThread; ++j) acc[h][j] = 0.f;
@@ -140,8 +146,8 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
     for (int t0 = 0; t0 < seg.tokens; t0 += kThreads) {
       const int nt = min(kThreads, seg.tokens - t0);
       // ---- logits for this tile: thread = token ----
-      float logit[kMaxGroup];
-      for (int h = 0; h < G; ++h) logit[h] = 0.f;
+      float logit[MG];
+      DKV_FOR_HEAD(h) logit[h] = 0.f;
       if ((int)threadIdx.x < nt) {
         const int t = t0 + threadIdx.x;
         if (dense16) {
@@ -160,42 +166,42 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
                 const uint16_t bits = (uint16_t)(ww[i / 2] >> (16 * (i % 2)));
                 const float kv = cache_dt == kBF16 ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
                 const int c = c0 + 8 * u + i;
-                for (int h = 0; h < G; ++h) logit[h] = fmaf(q_s[h * D + c], kv, logit[h]);
+                DKV_FOR_HEAD(h) logit[h] = fmaf(q_s[h * D + c], kv, logit[h]);
               }
             }
           }
         } else {
           for (int c = 0; c < D; ++c) {
             const float kv = key_value(seg, bh, c, t, D, inv_s, cache_dt, meta);
-            for (int h = 0; h < G; ++h) logit[h] = fmaf(q_s[h * D + c], kv, logit[h]);
+            DKV_FOR_HEAD(h) logit[h] = fmaf(q_s[h * D + c], kv, logit[h]);
           }
         }
-        for (int h = 0; h < G; ++h) logit[h] = logit[h] * scale;
+        DKV_FOR_HEAD(h) logit[h] = logit[h] * scale;
       } else {
-        for (int h = 0; h < G; ++h) logit[h] = -INFINITY;
+        DKV_FOR_HEAD(h) logit[h] = -INFINITY;
       }
       // ---- tile max per head ----
-      for (int h = 0; h < G; ++h) {
+      DKV_FOR_HEAD(h) {
         const float wm = wave_max(logit[h]);
         if (lane == 0) red_s[h * (kThreads / 64) + wave] = wm;
       }
       __syncthreads();
-      float new_m[kMaxGroup], old_w[kMaxGroup];
-      for (int h = 0; h < G; ++h) {
+      float new_m[MG], old_w[MG];
+      DKV_FOR_HEAD(h) {
         float tm = red_s[h * (kThreads / 64)];
         for (int w = 1; w < kThreads / 64; ++w) tm = fmaxf(tm, red_s[h * (kThreads / 64) + w]);
         new_m[h] = fmaxf(m[h], tm);
         old_w[h] = expf(m[h] - new_m[h]);
       }
       __syncthreads();
-      for (int h = 0; h < G; ++h) {
+      DKV_FOR_HEAD(h) {
         const float w = (int)threadIdx.x < nt ? expf(logit[h] - new_m[h]) : 0.f;
         w_s[h * kThreads + threadIdx.x] = w;
         const float ws = wave_sum(w);
         if (lane == 0) red_s[h * (kThreads / 64) + wave] = ws;
       }
       __syncthreads();
-      for (int h = 0; h < G; ++h) {
+      DKV_FOR_HEAD(h) {
         float ts = 0.f;
         for (int w = 0; w < kThreads / 64; ++w) ts += red_s[h * (kThreads / 64) + w];
         l[h] = l[h] * old_w[h] + ts;
@@ -205,8 +211,8 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
       for (int j = 0; j < kChanPerThread; ++j) {
         const int c = threadIdx.x + j * kThreads;
         if (c >= D) break;
-        float pv[kMaxGroup];
-        for (int h = 0; h < G; ++h) pv[h] = 0.f;
+        float pv[MG];
+        DKV_FOR_HEAD(h) pv[h] = 0.f;
         if (seg.value_kind == DKV_VALUE_DENSE && cache_dt != kF32) {
           // dense 16-bit values: 8 loads in flight per thread, coalesced across channels
           const uint16_t* vcol = (const uint16_t*)seg.value[0] + bh * seg.value_bh[0] + (int64_t)t0 * D + c;
@@ -218,21 +224,21 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
               const float vv = cache_dt == kBF16 ? bf16_to_f32(vb[i]) : (float)__builtin_bit_cast(_Float16, vb[i]);
-              for (int h = 0; h < G; ++h) pv[h] = fmaf(w_s[h * kThreads + t + i], vv, pv[h]);
+              DKV_FOR_HEAD(h) pv[h] = fmaf(w_s[h * kThreads + t + i], vv, pv[h]);
             }
           }
           for (; t < nt; ++t) {
             const uint16_t vb = vcol[(int64_t)t * D];
             const float vv = cache_dt == kBF16 ? bf16_to_f32(vb) : (float)__builtin_bit_cast(_Float16, vb);
-            for (int h = 0; h < G; ++h) pv[h] = fmaf(w_s[h * kThreads + t], vv, pv[h]);
+            DKV_FOR_HEAD(h) pv[h] = fmaf(w_s[h * kThreads + t], vv, pv[h]);
           }
         } else {
           for (int t = 0; t < nt; ++t) {
             const float vv = value_value(seg, bh, t0 + t, c, D, cache_dt, meta);
-            for (int h = 0; h < G; ++h) pv[h] = fmaf(w_s[h * kThreads + t], vv, pv[h]);
+            DKV_FOR_HEAD(h) pv[h] = fmaf(w_s[h * kThreads + t], vv, pv[h]);
           }
         }
-        for (int h = 0; h < G; ++h) acc[h][j] = acc[h][j] * old_w[h] + pv[h];
+        DKV_FOR_HEAD(h) acc[h][j] = acc[h][j] * old_w[h] + pv[h];
       }
       __syncthreads();
     }
@@ -240,7 +246,7 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
 
   // ---- partial state: ws[(b, hq, split)] = {max, sum, acc[D]} ----
   float* ws = (float*)a.workspace;
-  for (int h = 0; h < G; ++h) {
+  DKV_FOR_HEAD(h) {
     const int hq = kvh * G + h;
     float* rec = ws + (((int64_t)b * Hq + hq) * p.split_stride + p.split_offset + split) * (D + 2);
     if (threadIdx.x == 0) {
@@ -251,6 +257,126 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
       const int c = threadIdx.x + j * kThreads;
       if (c < D) rec[2 + c] = acc[h][j];
     }
+  }
+}
+
+// Dense 16-bit segments (the sink and the held tail): one wave per (batch,
+// kv head, segment, 32-token chunk), fp32 dot products as the reference's
+// eager attention computes them.  Every global load of a wave is issued
+// before the first use (query, the chunk's K rows and V rows), so a wave costs
+// one memory round trip.  Q K: lane = (token, half of the channels), the two
+// halves combined across lanes l and l^32; P V: lane = channel pair.  The
+// wave writes one record at split slot split_offset + segment * chunks + chunk.
+constexpr int kDenseWaves = 4;
+constexpr int kDenseChunk = 32;
+constexpr int kDenseDim = 128;
+constexpr int kDenseMaxGroup = 8;
+
+template <int MG>
+__global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodeParams p, int chunks) {
+  __shared__ float qsh[kDenseWaves][kDenseDim * MG];      // [c][MG]
+  __shared__ float wsh[kDenseWaves][MG * kDenseChunk];    // [h][t] weights of the chunk
+  const dkv_decode_args& a = p.a;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int worker = blockIdx.x * kDenseWaves + wave;
+  const int per_bh = p.n_total * chunks;
+  if (worker >= (int)(a.B * a.Hkv) * per_bh) return;
+  const int v = (worker % per_bh) / chunks, chunk = worker % chunks;
+  const int bhi = worker / per_bh;
+  const int b = bhi / (int)a.Hkv, kvh = bhi % (int)a.Hkv;
+  const int64_t bh = (int64_t)bhi;
+  const int G = p.group;
+  const bool bf = a.cache_dtype == kBF16;
+  float* qs = qsh[wave];
+  float* ws = wsh[wave];
+
+  const dkv_segment seg = general_segment(p, v);
+  const bool ok = seg.key_kind == DKV_KEY_DENSE && seg.value_kind == DKV_VALUE_DENSE &&
+                  seg.tokens <= chunks * kDenseChunk;
+  const int t0 = chunk * kDenseChunk;
+  const int nt = ok ? max(0, min(kDenseChunk, seg.tokens - t0)) : 0;
+  const uint16_t* kbase = (const uint16_t*)seg.key[0] + bh * seg.key_bh[0];
+  const uint16_t* vbase = (const uint16_t*)seg.value[0] + bh * seg.value_bh[0];
+
+  // ---- all loads first ----
+  float qv[kDenseDim * MG / 64];
+#pragma unroll
+  for (int r = 0; r < kDenseDim * MG / 64; ++r) {
+    const int i = lane + 64 * r, c = i / MG, h = i % MG;
+    qv[r] = h < G ? dev_load(a.query, (int64_t)b * a.q_sb + (int64_t)(kvh * G + h) * a.q_sh + c, (int)a.q_dtype)
+                  : 0.f;
+  }
+  const int kt = lane & (kDenseChunk - 1), khalf = lane >> 5;  // token, channel half of the Q K lane
+  uint4 krow[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    krow[u] = kt < nt ? *((const uint4*)(kbase + (int64_t)(t0 + kt) * kDenseDim + 64 * khalf) + u)
+                      : make_uint4(0u, 0u, 0u, 0u);
+  uint32_t vpair[kDenseChunk];
+#pragma unroll
+  for (int u = 0; u < kDenseChunk; ++u)
+    vpair[u] = u < nt ? *(const uint32_t*)(vbase + (int64_t)(t0 + u) * kDenseDim + 2 * lane) : 0u;
+#pragma unroll
+  for (int r = 0; r < kDenseDim * MG / 64; ++r) qs[lane + 64 * r] = qv[r];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- logits ----
+  float logit[MG];
+  DKV_FOR_HEAD(h) logit[h] = 0.f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const uint32_t ww[4] = {krow[u].x, krow[u].y, krow[u].z, krow[u].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint16_t bits = (uint16_t)(ww[i / 2] >> (16 * (i % 2)));
+      const float kv = bf ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
+      const float* qc = qs + (64 * khalf + 8 * u + i) * MG;
+      DKV_FOR_HEAD(h) logit[h] = fmaf(qc[h], kv, logit[h]);
+    }
+  }
+  const float scale = (float)a.scale;
+  float m[MG], l[MG];
+  DKV_FOR_HEAD(h) {
+    const float lg = kt < nt ? (logit[h] + __shfl_xor(logit[h], 32, 64)) * scale : -INFINITY;
+    m[h] = wave_max(lg);
+    const float w = kt < nt ? expf(lg - m[h]) : 0.f;
+    if (khalf == 0) ws[h * kDenseChunk + kt] = w;
+    l[h] = wave_sum(w) * 0.5f;  // every weight appears in two lanes
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- weighted values: channels 2 lane, 2 lane + 1 ----
+  float pv0[MG], pv1[MG];
+  DKV_FOR_HEAD(h) pv0[h] = pv1[h] = 0.f;
+#pragma unroll
+  for (int u = 0; u < kDenseChunk; ++u) {
+    const float v0 = bf ? bf16_to_f32((uint16_t)vpair[u]) : (float)__builtin_bit_cast(_Float16, (uint16_t)vpair[u]);
+    const float v1 = bf ? bf16_to_f32((uint16_t)(vpair[u] >> 16))
+                        : (float)__builtin_bit_cast(_Float16, (uint16_t)(vpair[u] >> 16));
+    DKV_FOR_HEAD(h) {
+      const float w = ws[h * kDenseChunk + u];
+      pv0[h] = fmaf(w, v0, pv0[h]);
+      pv1[h] = fmaf(w, v1, pv1[h]);
+    }
+  }
+
+  float* wsp = (float*)a.workspace;
+  DKV_FOR_HEAD(h) {
+    const int hq = kvh * G + h;
+    float* rec =
+        wsp + (((int64_t)b * a.Hq + hq) * p.split_stride + p.split_offset + (int64_t)v * chunks + chunk) * (kDenseDim + 2);
+    if (lane == 0) {
+      // a segment this kernel cannot read poisons its record (NaN output)
+      rec[0] = ok ? (nt > 0 ? m[h] : -INFINITY) : NAN;
+      rec[1] = nt > 0 ? l[h] : 0.f;
+    }
+    rec[2 + 2 * lane] = pv0[h];
+    rec[3 + 2 * lane] = pv1[h];
   }
 }
 
@@ -295,6 +421,14 @@ __global__ void __launch_bounds__(kThreads) decode_merge(DecodeParams p) {
 
 }  // namespace
 
+// Record a caller's timing event (if any) on the stream.
+static int record_event(void* ev, hipStream_t s) {
+  if (ev == nullptr) return DKV_OK;
+  const hipError_t e = hipEventRecord((hipEvent_t)ev, s);
+  DKV_CHECK(e == hipSuccess, DKV_ERR_HIP, "dkv_decode_attention: hipEventRecord failed: %s", hipGetErrorString(e));
+  return DKV_OK;
+}
+
 extern "C" int64_t dkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t n_splits) {
   return B * Hq * n_splits * (D + 2) * (int64_t)sizeof(float);
 }
@@ -319,10 +453,10 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
     DKV_CHECK(a.cache_dtype == dkv::kBF16 || a.cache_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED,
               "fast page path needs a bf16 or fp16 cache");
     DKV_CHECK(a.meta_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED, "fast page path needs fp16 metadata");
-    DKV_CHECK(a.fast_promoted % 16 == 0 && a.fast_promoted >= 0 && a.fast_promoted <= 64, DKV_ERR_UNSUPPORTED,
-              "fast page path needs a multiple of 16 (at most 64) promoted channels");
-    DKV_CHECK(a.fast_value_group % 8 == 0 && a.fast_value_group > 0 && 128 % a.fast_value_group == 0,
-              DKV_ERR_UNSUPPORTED, "fast page path needs a value group that is a multiple of 8 dividing 128");
+    DKV_CHECK(a.fast_promoted % 16 == 0 && a.fast_promoted >= 16 && a.fast_promoted <= 64, DKV_ERR_UNSUPPORTED,
+              "fast page path needs 16, 32, 48 or 64 promoted channels");
+    DKV_CHECK(a.fast_value_group % 16 == 0 && a.fast_value_group > 0 && 128 % a.fast_value_group == 0,
+              DKV_ERR_UNSUPPORTED, "fast page path needs a value group that is a multiple of 16 dividing 128");
     DKV_CHECK(a.fast_splits >= 1 && a.fast_splits <= fast_count, DKV_ERR_INVALID, "fast_splits out of range");
     DKV_CHECK(dkv::fast_decode_max_loads((int)a.fast_promoted, (int)(128 / a.fast_value_group)) < 16,
               DKV_ERR_UNSUPPORTED, "fast page path: value group too small");
@@ -337,8 +471,12 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
             "workspace too small");
   hipStream_t s = (hipStream_t)stream;
   if (fast_count > 0) {
-    int rc = dkv::launch_fast_decode(a, (int)a.fast_first, (int)fast_count, (int)a.fast_promoted,
-                                     (int)a.fast_value_group, (int)fast_splits, (int)stride, s);
+    int rc = record_event(a.fast_events[0], s);
+    if (rc) return rc;
+    rc = dkv::launch_fast_decode(a, (int)a.fast_first, (int)fast_count, (int)a.fast_promoted,
+                                 (int)a.fast_value_group, (int)fast_splits, (int)stride, s);
+    if (rc) return rc;
+    rc = record_event(a.fast_events[1], s);
     if (rc) return rc;
   }
   DecodeParams p;
@@ -350,9 +488,32 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
   p.split_stride = (int)stride;
   p.skip_first = fast_count > 0 ? (int)a.fast_first : 0;
   p.skip_count = fast_count > 0 ? (int)fast_count : 0;
-  if (general_splits > 0) {
-    hipLaunchKernelGGL(decode_split_general, dim3((unsigned)general_splits, (unsigned)a.Hkv, (unsigned)a.B),
-                       dim3(kThreads), 0, s, p);
+  const bool dense_rest = rest > 0 && a.rest_dense_tokens > 0;
+  if (dense_rest) {
+    const int64_t chunks = (a.rest_dense_tokens + kDenseChunk - 1) / kDenseChunk;
+    DKV_CHECK(a.n_splits == rest * chunks, DKV_ERR_INVALID,
+              "rest_dense_tokens needs n_splits == non-page segments * ceil(rest_dense_tokens / %d)", kDenseChunk);
+    DKV_CHECK(a.cache_dtype == dkv::kBF16 || a.cache_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED,
+              "rest_dense_tokens needs a bf16 or fp16 cache");
+    DKV_CHECK(a.D == kDenseDim && p.group <= kDenseMaxGroup, DKV_ERR_UNSUPPORTED,
+              "rest_dense_tokens needs head_dim %d and at most %d query heads per KV head", kDenseDim, kDenseMaxGroup);
+    const int mg = p.group <= 1 ? 1 : p.group <= 2 ? 2 : p.group <= 4 ? 4 : 8;
+    const int64_t workers = a.B * a.Hkv * rest * chunks;
+    const dim3 grid((unsigned)((workers + kDenseWaves - 1) / kDenseWaves)), block(64 * kDenseWaves);
+    const int ch = (int)chunks;
+    if (mg == 1) hipLaunchKernelGGL(decode_dense_rest<1>, grid, block, 0, s, p, ch);
+    else if (mg == 2) hipLaunchKernelGGL(decode_dense_rest<2>, grid, block, 0, s, p, ch);
+    else if (mg == 4) hipLaunchKernelGGL(decode_dense_rest<4>, grid, block, 0, s, p, ch);
+    else hipLaunchKernelGGL(decode_dense_rest<8>, grid, block, 0, s, p, ch);
+    int rc = dkv_check_launch("dkv_decode_attention(dense)");
+    if (rc) return rc;
+  } else if (general_splits > 0) {
+    const dim3 grid((unsigned)general_splits, (unsigned)a.Hkv, (unsigned)a.B);
+    if (p.group <= 1) hipLaunchKernelGGL(decode_split_general<1>, grid, dim3(kThreads), 0, s, p);
+    else if (p.group <= 2) hipLaunchKernelGGL(decode_split_general<2>, grid, dim3(kThreads), 0, s, p);
+    else if (p.group <= 4) hipLaunchKernelGGL(decode_split_general<4>, grid, dim3(kThreads), 0, s, p);
+    else if (p.group <= 8) hipLaunchKernelGGL(decode_split_general<8>, grid, dim3(kThreads), 0, s, p);
+    else hipLaunchKernelGGL(decode_split_general<16>, grid, dim3(kThreads), 0, s, p);
     int rc = dkv_check_launch("dkv_decode_attention(split)");
     if (rc) return rc;
   }

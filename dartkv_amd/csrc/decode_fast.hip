@@ -2,28 +2,37 @@
 //
 // Scope: head_dim 128, 128-token pages, keys with Dart promotion (2-bit codes
 // for every channel plus the upper 2 bits of NP promoted channels, one key
-// group per page), 2-bit values with groups of vg (8 | vg, vg | 128) channels,
-// fp16 metadata, bf16 or fp16 cache, up to 4 query heads per KV head.
-// Everything else goes through the general kernel (decode.hip).
+// group per page), 2-bit values with groups of vg (16 | vg, vg | 128)
+// channels, fp16 metadata, bf16 or fp16 cache, up to 4 query heads per KV
+// head.  Everything else goes through the general kernel (decode.hip).
 //
 // One wave owns one split: a contiguous range of pages of one (batch, kv
 // head).  Per page the wave
 //   1. stages the packed page (10,880 bytes at the reference layout) in its
-//      private LDS region with 16-byte loads; the next page is prefetched into
-//      registers while the current one is processed;
+//      private LDS region with global_load_lds; the next page's parts are
+//      issued as soon as the current page no longer reads their region;
 //   2. builds exact-value tables: for every channel / (token, value group) the
 //      dequantized value of each code under the reference's rounding chain
 //      (fp16 code*scale, fp16 +zero, then the cache dtype), stored as fp16
-//      (bf16 values are exact in fp16 in its normal range);
-//   3. reorders channels so the NP promoted channels come first (the query is
-//      permuted the same way), turning the 4-bit / 2-bit split into whole
-//      16-channel blocks;
-//   4. computes logits S = Q K over the page and O += P V with
-//      v_mfma_f32_16x16x16f16 (query heads in the M rows, four of sixteen
-//      used); the B operands are assembled in registers by v_perm lookups of
-//      2-bit codes into byte-planar tables, so every K/V element is dequantized
-//      exactly once;
-//   5. keeps the online-softmax state (max, sum, O) across pages.
+//      (bf16 values are exact in fp16 in its normal range) in byte planes
+//      (low bytes of the entries in one dword, high bytes in another);
+//   3. orders channels so the NP promoted channels come first (the query is
+//      permuted the same way);
+//   4. computes S = Q K and O += P V with v_mfma_f32_16x16x16f16 in a "slot"
+//      layout: the 16 rows of a tile are 4 slots x 4 query heads.  For Q K the
+//      16 K values of one MFMA are 4 channels x 4 slots and a slot picks one
+//      of 4 tokens, so the B values a lane holds are 4 tokens of ONE channel
+//      (one table) and the A operand carries q at the lane's slot and zeros
+//      elsewhere.  For P V a slot picks one of 4 channels of one token (one
+//      table) and A carries p at the lane's slot.  A tile then holds 64
+//      tokens x 4 heads (Q K) or 64 channels x 4 heads (P V), and every lane
+//      holds useful results;
+//   5. B values come from v_perm lookups of the 2-bit codes in the byte-plane
+//      tables (a 16-entry table read as two 8-entry halves plus a blend for
+//      the 4-bit promoted codes), so every K/V element is dequantized once;
+//   6. keeps an online softmax in base 2 whose running max only moves when a
+//      logit exceeds it by more than 8 (so p <= 256 keeps fp16's relative
+//      precision); row sums stay per lane until the end.
 // The partial state goes to the workspace and the shared merge pass finishes.
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -42,35 +51,46 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 constexpr int kD = 128;
 constexpr int kPage = 128;
 constexpr int kWaves = 4;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kSlack = 8.f;  // log2 headroom before the running max moves
+constexpr int kQpStride = 264;     // bytes between promoted-query rows (8 banks + 2 apart)
+constexpr int kPtStride = 288;     // bytes between softmax-weight rows (8 banks apart)
+constexpr int kVlutStride = 1056;  // bytes between value-table groups (8 banks apart)
 
 // Byte offsets inside one wave's LDS region (16-byte aligned; sizes depend on
 // the promoted-channel count NP and value groups per token Gv).
 struct LdsMap {
-  int kl, vc, kh, ki, ks, kz, vs, vz, klut, klut16, vlut, pmap, qp, pt, q16, bytes;
+  int kl, vc, kh, ki, ks, kz, vs, vz, klut, klut16, vlut, pidx, q16, qp, pt, zero, bytes;
 };
 
 __host__ __device__ inline LdsMap lds_map(int np, int gv) {
   LdsMap m;
   int o = 0;
-  m.kl = o; o += 4096;            // key low codes   [128 ch][32 B]
-  m.vc = o; o += 4096;            // value codes     [128 tok][32 B]
-  m.kh = o; o += np * 32;         // key high codes  [NP][32 B]
-  m.ki = o; o += np * 4;          // channel indices [NP] int32
-  m.ks = o; o += 256;             // key scale  [128] fp16
-  m.kz = o; o += 256;             // key zero   [128] fp16
-  m.vs = o; o += 256 * gv;        // value scale [128 tok][Gv] fp16
-  m.vz = o; o += 256 * gv;        // value zero  [128 tok][Gv] fp16
-  m.klut = o; o += 1024;          // 2-bit key tables [128 pos][LO, HI]
-  m.klut16 = o; o += np * 32;     // 4-bit key tables [NP][16] fp16
-  m.vlut = o; o += 1024 * gv;     // value tables [Gv][128 tok][LO, HI]
-  m.pmap = o; o += 128;           // position -> channel uint8
-  m.qp = o; o += 1024;            // permuted query [4][128] fp16
-  m.pt = o; o += 1024;            // softmax weights [4][128] fp16 (channel flags before that)
-  m.q16 = o; o += 1024;           // query in channel order [4][128] fp16
-  m.bytes = o;
+  m.kl = o; o += 4096;                     // key low codes   [128 ch][32 B]
+  m.vc = o; o += 4096;                     // value codes     [128 tok][32 B]
+  m.kh = o; o += np * 32;                  // key high codes  [NP][32 B]
+  m.ki = o; o += (np * 4 + 15) / 16 * 16;  // channel indices [NP] int32
+  m.ks = o; o += 256;                      // key scale  [128] fp16
+  m.kz = o; o += 256;                      // key zero   [128] fp16
+  m.vs = o; o += 256 * gv;                 // value scale [128 tok][Gv] fp16
+  m.vz = o; o += 256 * gv;                 // value zero  [128 tok][Gv] fp16
+  m.klut = o; o += 1024;                   // 2-bit key tables [128 ch][LO, HI] (zero for promoted channels)
+  m.klut16 = o; o += np * 32;              // 4-bit key tables [NP][LO 16 B, HI 16 B]
+  m.vlut = o; o += kVlutStride * gv;       // value tables [Gv][128 tok][LO, HI], padded rows
+  m.pidx = o; o += 64;                     // promoted channels [NP] uint8 (a copy: ki is refilled early)
+  m.q16 = o; o += 1024;                    // query [4][128 ch] fp16
+  // A-operand sources; row strides put the rows one read touches in distinct
+  // banks, and the zero block 16 banks after an aligned row start.
+  o = (o + 127) / 128 * 128;
+  m.qp = o; o += 4 * kQpStride;            // query of the promoted channels [4][NP] fp16
+  o = (o + 127) / 128 * 128;
+  m.pt = o; o += 4 * kPtStride;            // softmax weights [4][128 tok] fp16 (channel flags before)
+  o = (o + 127) / 128 * 128 + 64;
+  m.zero = o; o += 256;                    // zeros read by A-operand lanes without data
+  m.bytes = (o + 15) / 16 * 16;
   return m;
 }
-
 
 __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
   return __builtin_amdgcn_perm(s0, s1, sel);
@@ -97,13 +117,31 @@ __device__ __forceinline__ uint32_t lut_pair(uint32_t codes_h2, uint32_t s_h2, u
   return bf16 ? round_pair_to_bf16_precision(r) : r;
 }
 
-// Byte-planar table of the 4 values for codes 0..3: LO = low bytes, HI = high bytes.
-__device__ __forceinline__ void build_lut4(uint16_t s, uint16_t z, bool bf16, uint32_t* lo, uint32_t* hi) {
-  const uint32_t s2 = (uint32_t)s * 0x10001u, z2 = (uint32_t)z * 0x10001u;
+// Byte-plane table of the 4 values for codes 0..3: x = low bytes, y = high bytes.
+__device__ __forceinline__ uint2 build_lut4(uint32_t s, uint32_t z, bool bf16) {
+  const uint32_t s2 = s * 0x10001u, z2 = z * 0x10001u;
   const uint32_t v01 = lut_pair(0x3c000000u, s2, z2, bf16);  // codes (0, 1)
   const uint32_t v23 = lut_pair(0x42004000u, s2, z2, bf16);  // codes (2, 3)
-  *lo = perm(v23, v01, 0x06040200u);
-  *hi = perm(v23, v01, 0x07050301u);
+  return make_uint2(perm(v23, v01, 0x06040200u), perm(v23, v01, 0x07050301u));
+}
+
+// B operand (4 fp16 = slots 0..3 of one table) from 4 codes e (one per byte,
+// values 0..3) and a byte-plane table (lo, hi).
+__device__ __forceinline__ half4 lookup4(uint32_t e, uint32_t lo, uint32_t hi) {
+  const uint32_t l4 = perm(hi, lo, e);  // selector bytes 0..3 pick from lo
+  const uint32_t h4 = perm(lo, hi, e);  // ... and here from hi
+  return __builtin_bit_cast(half4, make_uint2(perm(h4, l4, 0x05010400u), perm(h4, l4, 0x07030602u)));
+}
+
+// B operand from 4-bit codes: el = low 2 bits per byte (values 0..3), th =
+// high 2 bits in bits 0..1 of each byte (other bits ignored), L / H = low /
+// high bytes of table entries 0..15 (entry = low + 4 * high).
+__device__ __forceinline__ half4 lookup16(uint32_t el, uint32_t th, const uint4& L, const uint4& H) {
+  const uint32_t sel = el | ((th & 0x01010101u) << 2);              // entry within an 8-entry half
+  const uint32_t blend = ((th & 0x02020202u) << 1) | 0x03020100u;  // take the upper half's byte
+  const uint32_t l4 = perm(perm(L.w, L.z, sel), perm(L.y, L.x, sel), blend);
+  const uint32_t h4 = perm(perm(H.w, H.z, sel), perm(H.y, H.x, sel), blend);
+  return __builtin_bit_cast(half4, make_uint2(perm(h4, l4, 0x05010400u), perm(h4, l4, 0x07030602u)));
 }
 
 struct FastParams {
@@ -157,7 +195,7 @@ __device__ __forceinline__ void copy_to_lds(uint8_t* dst, const uint8_t* src, in
 // longer reads that LDS region.
 __device__ __forceinline__ void issue_small(const LdsMap& M, uint8_t* lds, const PageAddr& a, int np, int gv,
                                             int lane) {
-  copy_to_lds(lds + M.ki, (const uint8_t*)a.ki, np * 4, lane);
+  copy_to_lds(lds + M.ki, (const uint8_t*)a.ki, (np * 4 + 15) / 16 * 16, lane);
   copy_to_lds(lds + M.ks, (const uint8_t*)a.ks, 256, lane);
   copy_to_lds(lds + M.kz, (const uint8_t*)a.kz, 256, lane);
   copy_to_lds(lds + M.vs, (const uint8_t*)a.vs, 256 * gv, lane);
@@ -209,16 +247,43 @@ __device__ __forceinline__ void vm_wait(int n) {
 
 // Number of copy_to_lds instructions in each staging group.
 __host__ __device__ inline int n_small_loads(int np, int gv) {
-  return (np * 4 + 1023) / 1024 + 2 + 2 * ((256 * gv + 1023) / 1024);
+  return ((np * 4 + 15) / 16 * 16 + 1023) / 1024 + 2 + 2 * ((256 * gv + 1023) / 1024);
 }
 __host__ __device__ inline int n_key_loads(int np) { return 4 + (np * 32 + 1023) / 1024; }
 
+__device__ __forceinline__ _Float16 lds_h(const uint8_t* base, int off) { return *(const _Float16*)(base + off); }
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t* base, int off) { return *(const uint32_t*)(base + off); }
 
-// Accumulate acc[j] += a * B_j for the 8 columns j of a 4-row block whose
-// B values come from 2-bit codes.
-// x[m]: 16 bits = codes of the lane's 8 columns for row m (m = 0..3).
-// lo[m], hi[m]: byte-planar 4-entry tables of row m.
-// B_j (fp16 x4) = rows 0..3 at column j.
+// A operand: half i read from byte offset a[i] + off; a[i] points into the
+// query / weight rows for the lane's own slot and into the zero block otherwise.
+__device__ __forceinline__ half4 load_a(const uint8_t* lds, const int a[4], int off) {
+  half4 r;
+  r[0] = lds_h(lds, a[0] + off);
+  r[1] = lds_h(lds, a[1] + off);
+  r[2] = lds_h(lds, a[2] + off);
+  r[3] = lds_h(lds, a[3] + off);
+  return r;
+}
+
+__device__ __forceinline__ float wave_max64(float v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float uniform(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+// O[j] += a * B_j for the 8 channel tiles j of one 16-token block in the
+// heads-in-rows layout (rows 0..3 = query heads, K = 4 tokens per lane).
+// x[m]: 16 bits = codes of the lane's 8 channels for token row m (m = 0..3);
+// lo[m], hi[m]: byte-plane tables of token row m.  Rows m and m + 1 share one
+// v_perm: selector bit 2 picks the second row's table.
 __device__ __forceinline__ void mma_lut_block(half4 a, const uint32_t x[4], const uint32_t lo[4], const uint32_t hi[4],
                                               float4v acc[8]) {
   const uint32_t y0 = perm(x[1], x[0], 0x05010400u);
@@ -236,10 +301,13 @@ __device__ __forceinline__ void mma_lut_block(half4 a, const uint32_t x[4], cons
   }
 }
 
-template <int GQ>
+// GQ: query heads per KV head; NP: promoted channels (16, 32, 48 or 64).
+// Both are compile-time so every block loop unrolls with immediate offsets.
+template <int GQ, int NP>
 __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, kq = lane >> 4;
   const int worker = blockIdx.x * kWaves + wave;
   const int total_workers = p.B * p.Hkv * p.splits;
@@ -247,30 +315,64 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   const int split = worker % p.splits;
   const int bh = worker / p.splits;
   const int b = bh / p.Hkv, kvh = bh % p.Hkv;
-  const LdsMap M = lds_map(p.np, p.gv);
+  constexpr int np = NP;
+  const int gv = p.gv;
+  const LdsMap M = lds_map(np, gv);
   uint8_t* lds = smem + wave * M.bytes;
   const int page0 = (int)(((int64_t)split * p.count) / p.splits);
   const int page1 = (int)(((int64_t)(split + 1) * p.count) / p.splits);
-  const int np = p.np, gv = p.gv;
   const bool bf16 = p.bf16 != 0;
 
-  // running softmax state, rows r = 0..3 live in lanes 0..15
-  float m_run[4], l_run[4];
+  // ---- per-lane constants ----
+  const int sh = 2 * (n & 3);             // bit offset of this lane's codes in each byte
+  const int qd = 4 * (n >> 2);            // byte offset of this lane's code dword in a 16-byte run
+  const int slot = n >> 2, head = n & 3;  // slot-layout A row n = 4 * slot + head
+  int aq[4];                              // promoted-query A sources (row at the lane's slot, else zeros)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    aq[i] = (i == slot && head < GQ) ? M.qp + kQpStride * head + 2 * kq : M.zero + 2 * kq;
+  // P V A source (heads in rows): weights of head n, or zeros
+  const int apv = n < GQ ? M.pt + kPtStride * n + 8 * kq : M.zero + 8 * kq;
+  // P V block blk, K index 4kq + m is token 16 blk + kq + 4m: the four lane
+  // groups then read code rows and tables in different banks; the weights are
+  // stored in that K order (wpos) so each A operand is one 8-byte read.
+  const int vtab = M.vlut + kVlutStride * ((8 * n) / p.vg) + 8 * kq;  // value tables of the lane's group
+  const int vcode = M.vc + 32 * kq + 2 * n;                           // value codes of the lane's channels
+
+  // ---- running state ----
+  // S (slot layout): lane (n, kq) holds heads 0..3 of tokens 64t + 16(n/4) + 4kq + n%4.
+  // O (heads in rows): lanes kq = 0 hold heads 0..3 of channels 8n + j in O[j].
+  float m_run[4], l_part[4];
   float4v O[8];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    m_run[r] = -INFINITY;
-    l_run[r] = 0.f;
+  for (int i = 0; i < 4; ++i) {
+    m_run[i] = -INFINITY;
+    l_part[i] = 0.f;
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) O[j] = float4v{0.f, 0.f, 0.f, 0.f};
 
   {
     uint16_t* q16 = (uint16_t*)(lds + M.q16);
-    for (int i = lane; i < GQ * kD; i += 64) {
+    for (int i = lane; i < 4 * kD; i += 64) {
       const int h = i / kD, c = i % kD;
-      const float qv = dev_load(p.query, (int64_t)b * p.q_sb + (int64_t)(kvh * GQ + h) * p.q_sh + c, p.q_dtype);
+      const float qv =
+          h < GQ ? dev_load(p.query, (int64_t)b * p.q_sb + (int64_t)(kvh * GQ + h) * p.q_sh + c, p.q_dtype) : 0.f;
       q16[i] = __builtin_bit_cast(uint16_t, (_Float16)qv);
+    }
+    *(uint32_t*)(lds + M.zero + 4 * lane) = 0u;
+  }
+  lds_sync();
+  // Q K A operands for channel blocks cb = 0..31 (natural channel order), kept
+  // in registers for the whole split: q[head][4cb + kq] at half `slot`.
+  half4 qa[kD / 4];
+  {
+    const uint16_t* q16 = (const uint16_t*)(lds + M.q16);
+#pragma unroll
+    for (int cb = 0; cb < kD / 4; ++cb) {
+      const _Float16 v = __builtin_bit_cast(_Float16, q16[head * kD + 4 * cb + kq]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qa[cb][i] = i == slot ? v : (_Float16)0.f;
     }
   }
   if (page0 < page1) {
@@ -279,6 +381,8 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     issue_keys(M, lds, a0, np, lane);
     issue_values(M, lds, a0, lane);
   }
+  const float c2 = p.scale * kLog2e;
+
 #pragma unroll 1
   for (int pg = page0; pg < page1; ++pg) {
     const bool has_next = pg + 1 < page1;
@@ -288,156 +392,133 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     // value codes (this page, 4 loads); the values may still be in flight
     vm_wait(4);
 
-    // ---- channel order: promoted slots first, then the rest ascending ----
+    // ---- promoted channels: flags and a private copy of the indices (the
+    // index region is refilled with the next page's before Q K runs) ----
     uint8_t* flag = lds + M.pt;
-    uint8_t* pmap = lds + M.pmap;
-    const int32_t* ki = (const int32_t*)(lds + M.ki);
+    uint8_t* pidx = lds + M.pidx;
     flag[lane] = 0;
     flag[lane + 64] = 0;
     lds_sync();
     if (lane < np) {
-      const int c = ki[lane] & 127;
-      flag[c] = (uint8_t)(lane + 1);
-      pmap[lane] = (uint8_t)c;
-    }
-    lds_sync();
-    {
-      const bool prom_a = flag[lane] != 0, prom_b = flag[lane + 64] != 0;
-      const uint64_t rest_a = __ballot(!prom_a), rest_b = __ballot(!prom_b);
-      const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-      const int ra = __popcll(rest_a & below);
-      const int rb = __popcll(rest_a) + __popcll(rest_b & below);
-      if (!prom_a) pmap[np + ra] = (uint8_t)lane;
-      if (!prom_b) pmap[np + rb] = (uint8_t)(lane + 64);
+      const int c = ((const int32_t*)(lds + M.ki))[lane] & 127;
+      flag[c] = 1;
+      pidx[lane] = (uint8_t)c;
     }
     lds_sync();
 
-    // ---- exact-value tables ----
-    const uint16_t* ks = (const uint16_t*)(lds + M.ks);
-    const uint16_t* kz = (const uint16_t*)(lds + M.kz);
-    uint32_t* klut = (uint32_t*)(lds + M.klut);
-    for (int pos = np + lane; pos < kD; pos += 64) {
-      const int c = pmap[pos];
-      uint32_t lo, hi;
-      build_lut4(ks[c], kz[c], bf16, &lo, &hi);
-      klut[2 * pos] = lo;
-      klut[2 * pos + 1] = hi;
-    }
-    if (lane < np) {
-      const int c = pmap[lane];
-      const uint32_t s2 = (uint32_t)ks[c] * 0x10001u, z2 = (uint32_t)kz[c] * 0x10001u;
-      uint32_t* t16 = (uint32_t*)(lds + M.klut16 + 32 * lane);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        // fp16 codes (2q, 2q+1)
-        const _Float16 c0 = (_Float16)(2 * q), c1 = (_Float16)(2 * q + 1);
-        const uint32_t codes = (uint32_t)__builtin_bit_cast(uint16_t, c0) |
-                               ((uint32_t)__builtin_bit_cast(uint16_t, c1) << 16);
-        t16[q] = lut_pair(codes, s2, z2, bf16);
-      }
-    }
+    // ---- exact-value tables and the promoted channels' query ----
     {
+      const uint16_t* ks = (const uint16_t*)(lds + M.ks);
+      const uint16_t* kz = (const uint16_t*)(lds + M.kz);
+#pragma unroll
+      for (int c = lane; c < kD; c += 64)
+        *(uint2*)(lds + M.klut + 8 * c) = flag[c] ? make_uint2(0u, 0u) : build_lut4(ks[c], kz[c], bf16);
+      // 4-bit tables: lanes (2j, 2j+1) build entries 0..7 / 8..15 of slot j
+#pragma unroll
+      for (int j0 = 0; j0 < np; j0 += 32) {
+        const int j = j0 + (lane >> 1);
+        if (j < np) {
+          const int half = lane & 1;
+          const int c = pidx[j];
+          const uint32_t s2 = (uint32_t)ks[c] * 0x10001u, z2 = (uint32_t)kz[c] * 0x10001u;
+          // fp16 code pairs (8 half + 2q, 8 half + 2q + 1), q = 0..3
+          const uint32_t e0 = half ? 0x48804800u : 0x3c000000u;  // (8, 9)   | (0, 1)
+          const uint32_t e1 = half ? 0x49804900u : 0x42004000u;  // (10, 11) | (2, 3)
+          const uint32_t e2 = half ? 0x4a804a00u : 0x45004400u;  // (12, 13) | (4, 5)
+          const uint32_t e3 = half ? 0x4b804b00u : 0x47004600u;  // (14, 15) | (6, 7)
+          const uint32_t v0 = lut_pair(e0, s2, z2, bf16), v1 = lut_pair(e1, s2, z2, bf16);
+          const uint32_t v2 = lut_pair(e2, s2, z2, bf16), v3 = lut_pair(e3, s2, z2, bf16);
+          uint8_t* t16 = lds + M.klut16 + 32 * j + 8 * half;
+          *(uint2*)t16 = make_uint2(perm(v1, v0, 0x06040200u), perm(v3, v2, 0x06040200u));
+          *(uint2*)(t16 + 16) = make_uint2(perm(v1, v0, 0x07050301u), perm(v3, v2, 0x07050301u));
+        }
+      }
       const uint16_t* vs = (const uint16_t*)(lds + M.vs);
       const uint16_t* vz = (const uint16_t*)(lds + M.vz);
-      uint32_t* vlut = (uint32_t*)(lds + M.vlut);
-      for (int i = lane; i < kPage * gv; i += 64) {
-        const int t = i / gv, g = i % gv;
-        uint32_t lo, hi;
-        build_lut4(vs[t * gv + g], vz[t * gv + g], bf16, &lo, &hi);
-        vlut[2 * (g * kPage + t)] = lo;
-        vlut[2 * (g * kPage + t) + 1] = hi;
+      for (int g = 0; g < gv; ++g) {
+#pragma unroll
+        for (int t = lane; t < kPage; t += 64)
+          *(uint2*)(lds + M.vlut + kVlutStride * g + 8 * t) = build_lut4(vs[t * gv + g], vz[t * gv + g], bf16);
       }
-    }
-    // permuted query, fp16
-    {
-      uint16_t* qp = (uint16_t*)(lds + M.qp);
       const uint16_t* q16 = (const uint16_t*)(lds + M.q16);
-      for (int i = lane; i < GQ * kD; i += 64) {
-        const int h = i / kD, pos = i % kD;
-        qp[h * kD + pos] = q16[h * kD + pmap[pos]];
+      uint16_t* qp = (uint16_t*)(lds + M.qp);
+#pragma unroll
+      for (int i = lane; i < GQ * np; i += 64) {
+        const int h = i / np, j = i % np;
+        qp[h * (kQpStride / 2) + j] = q16[h * kD + pidx[j]];
       }
     }
     lds_sync();
     if (has_next) issue_small(M, lds, nxt, np, gv, lane);
 
-    // ---- S = Q K over the page (columns: token 8n + j) ----
-    float4v S[8];
+    // ---- S = Q K; tile t covers tokens 64t + 16(n/4) + 4 slot + n%4 ----
+    float4v S[2];
+    S[0] = S[1] = float4v{0.f, 0.f, 0.f, 0.f};
+    // 2-bit codes of every channel (promoted channels have zero tables)
+    {
+      const int row = M.kl + 32 * kq + qd;
+      const int tab = M.klut + 8 * kq;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) S[j] = float4v{0.f, 0.f, 0.f, 0.f};
-    const uint8_t* kl = lds + M.kl;
-    const uint8_t* kh = lds + M.kh;
-    const uint16_t* klut16 = (const uint16_t*)(lds + M.klut16);
-#pragma unroll 1
-    for (int blk = 0; blk < kD / 16; ++blk) {
-      const int pos0 = blk * 16 + 4 * kq;
-      half4 a = half4{0, 0, 0, 0};
-      if (n < GQ) a = *(const half4*)(lds + M.qp + 2 * (n * kD + pos0));
-      if (blk * 16 < np) {
-        // promoted channels: 4-bit codes, one table lookup per element
-        uint32_t xl[4], xh[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const int c = pmap[pos0 + m];
-          xl[m] = *(const uint16_t*)(kl + 32 * c + 2 * n);
-          xh[m] = *(const uint16_t*)(kh + 32 * (pos0 + m) + 2 * n);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          uint16_t v[4];
-#pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            const uint32_t code = ((xl[m] >> (2 * j)) & 3u) | (((xh[m] >> (2 * j)) & 3u) << 2);
-            v[m] = klut16[(pos0 + m) * 16 + code];
-          }
-          uint2 w = make_uint2((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
-          S[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, __builtin_bit_cast(half4, w), S[j], 0, 0, 0);
-        }
-      } else {
-        uint32_t x[4], lo[4], hi[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const int c = pmap[pos0 + m];
-          x[m] = *(const uint16_t*)(kl + 32 * c + 2 * n);
-          const uint2 t = *(const uint2*)(klut + 2 * (pos0 + m));
-          lo[m] = t.x;
-          hi[m] = t.y;
-        }
-        mma_lut_block(a, x, lo, hi, S);
+      for (int cb = 0; cb < kD / 4; ++cb) {
+        const uint32_t w0 = lds_u32(lds, row + 128 * cb), w1 = lds_u32(lds, row + 128 * cb + 16);
+        const uint2 t = *(const uint2*)(lds + tab + 32 * cb);
+        S[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], lookup4((w0 >> sh) & 0x03030303u, t.x, t.y), S[0], 0, 0,
+                                                     0);
+        S[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], lookup4((w1 >> sh) & 0x03030303u, t.x, t.y), S[1], 0, 0,
+                                                     0);
       }
+    }
+    // promoted channels: 4-bit codes, slot j = 4pb + kq of the high codes
+#pragma unroll
+    for (int pb = 0; pb < np / 4; ++pb) {
+      const half4 a = load_a(lds, aq, 8 * pb);
+      const int j = 4 * pb + kq;
+      const int row = M.kl + 32 * pidx[j] + qd;
+      const uint32_t wl0 = lds_u32(lds, row), wl1 = lds_u32(lds, row + 16);
+      const int hrow = M.kh + 32 * j + qd;
+      const uint32_t wh0 = lds_u32(lds, hrow), wh1 = lds_u32(lds, hrow + 16);
+      const uint4 L = *(const uint4*)(lds + M.klut16 + 32 * j);
+      const uint4 H = *(const uint4*)(lds + M.klut16 + 32 * j + 16);
+      S[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, lookup16((wl0 >> sh) & 0x03030303u, wh0 >> sh, L, H), S[0], 0,
+                                                   0, 0);
+      S[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, lookup16((wl1 >> sh) & 0x03030303u, wh1 >> sh, L, H), S[1], 0,
+                                                   0, 0);
     }
     lds_sync();
     if (has_next) issue_keys(M, lds, nxt, np, lane);
 
-    // ---- online softmax (rows r < GQ in lanes 0..15) ----
-    float alpha[4];
+    // ---- online softmax in base 2 ----
     {
-      uint16_t* pt = (uint16_t*)(lds + M.pt);
+      float x[2][4];
+      bool over = false;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, S[j][r] * p.scale);
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-        const float m_new = fmaxf(m_run[r], mx);
-        alpha[r] = __expf(m_run[r] - m_new);
-        float sum = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float w = __expf(S[j][r] * p.scale - m_new);
-          sum += w;
-          if (kq == 0 && r < GQ) pt[r * kPage + 8 * n + j] = __builtin_bit_cast(uint16_t, (_Float16)w);
-        }
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
-        l_run[r] = l_run[r] * alpha[r] + sum;
-        m_run[r] = m_new;
+      for (int i = 0; i < GQ; ++i) {
+        x[0][i] = S[0][i] * c2;
+        x[1][i] = S[1][i] * c2;
+        over |= fmaxf(x[0][i], x[1][i]) > m_run[i] + kSlack;
       }
-    }
+      if (__ballot(over) != 0ull) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+        for (int i = 0; i < GQ; ++i) {
+          const float m_new = uniform(fmaxf(m_run[i], wave_max64(fmaxf(x[0][i], x[1][i]))));
+          const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_new);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) O[j][r] *= alpha[r];
+          for (int j = 0; j < 8; ++j) O[j][i] *= alpha;
+          l_part[i] *= alpha;
+          m_run[i] = m_new;
+        }
+      }
+      uint16_t* pt = (uint16_t*)(lds + M.pt);
+      const int tok = 16 * (n >> 2) + 4 * kq + (n & 3);
+      const int wpos = (tok & ~15) | ((tok & 3) << 2) | ((tok >> 2) & 3);  // K position of token tok
+#pragma unroll
+      for (int i = 0; i < GQ; ++i) {
+        const float p0 = __builtin_amdgcn_exp2f(x[0][i] - m_run[i]);
+        const float p1 = __builtin_amdgcn_exp2f(x[1][i] - m_run[i]);
+        l_part[i] += p0 + p1;
+        pt[i * (kPtStride / 2) + wpos] = __builtin_bit_cast(uint16_t, (_Float16)p0);
+        pt[i * (kPtStride / 2) + wpos + 64] = __builtin_bit_cast(uint16_t, (_Float16)p1);
+      }
     }
     lds_sync();
 
@@ -445,20 +526,15 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     // loads issued since
     vm_wait(has_next ? n_small_loads(np, gv) + n_key_loads(np) : 0);
 
-    // ---- O += P V (columns: channel 8n + j) ----
-    const uint8_t* vc = lds + M.vc;
-    const uint32_t* vlut = (const uint32_t*)(lds + M.vlut);
-    const int g = (8 * n) / p.vg;
-#pragma unroll 1
+    // ---- O += P V, heads in rows: block blk covers tokens 16 blk + kq + 4m ----
+#pragma unroll
     for (int blk = 0; blk < kPage / 16; ++blk) {
-      const int t0 = blk * 16 + 4 * kq;
-      half4 a = half4{0, 0, 0, 0};
-      if (n < GQ) a = *(const half4*)(lds + M.pt + 2 * (n * kPage + t0));
+      const half4 a = *(const half4*)(lds + apv + 32 * blk);
       uint32_t x[4], lo[4], hi[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        x[m] = *(const uint16_t*)(vc + 32 * (t0 + m) + 2 * n);
-        const uint2 t = *(const uint2*)(vlut + 2 * (g * kPage + t0 + m));
+        x[m] = *(const uint16_t*)(lds + vcode + 512 * blk + 128 * m);
+        const uint2 t = *(const uint2*)(lds + vtab + 128 * blk + 32 * m);
         lo[m] = t.x;
         hi[m] = t.y;
       }
@@ -469,17 +545,18 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   }
 
   // ---- partial state ----
-  if (lane < 16) {
 #pragma unroll
-    for (int r = 0; r < GQ; ++r) {
-      const int hq = kvh * GQ + r;
-      float* rec = p.ws + (((int64_t)b * p.Hq + hq) * p.split_stride + split) * (kD + 2);
-      if (lane == 0) {
-        rec[0] = m_run[r];
-        rec[1] = l_run[r];
-      }
+  for (int i = 0; i < GQ; ++i) {
+    const float l = wave_sum64(l_part[i]);
+    const int hq = kvh * GQ + i;
+    float* rec = p.ws + (((int64_t)b * p.Hq + hq) * p.split_stride + split) * (kD + 2);
+    if (lane == 0) {
+      rec[0] = m_run[i] * kLn2;
+      rec[1] = l;
+    }
+    if (kq == 0) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) rec[2 + 8 * n + j] = O[j][r];
+      for (int j = 0; j < 8; ++j) rec[2 + 8 * n + j] = O[j][i];
     }
   }
 }
@@ -517,20 +594,29 @@ int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, i
   const int64_t workers = (int64_t)p.B * p.Hkv * splits;
   const unsigned blocks = (unsigned)((workers + kWaves - 1) / kWaves);
   const size_t lds = fast_decode_lds_bytes(np, p.gv);
+  const dim3 grid(blocks), block(256);
+#define DKV_FAST_LAUNCH(G, N) hipLaunchKernelGGL((decode_pages_fast<G, N>), grid, block, lds, stream, p)
+#define DKV_FAST_NP(G)                         \
+  switch (np) {                                \
+    case 16: DKV_FAST_LAUNCH(G, 16); break;    \
+    case 32: DKV_FAST_LAUNCH(G, 32); break;    \
+    case 48: DKV_FAST_LAUNCH(G, 48); break;    \
+    default: DKV_FAST_LAUNCH(G, 64); break;    \
+  }
+  if (np != 16 && np != 32 && np != 48 && np != 64) {
+    set_error("fast decode supports 16, 32, 48 or 64 promoted channels");
+    return DKV_ERR_UNSUPPORTED;
+  }
   switch (p.GQ) {
-    case 1:
-      hipLaunchKernelGGL(decode_pages_fast<1>, dim3(blocks), dim3(256), lds, stream, p);
-      break;
-    case 2:
-      hipLaunchKernelGGL(decode_pages_fast<2>, dim3(blocks), dim3(256), lds, stream, p);
-      break;
-    case 4:
-      hipLaunchKernelGGL(decode_pages_fast<4>, dim3(blocks), dim3(256), lds, stream, p);
-      break;
+    case 1: DKV_FAST_NP(1); break;
+    case 2: DKV_FAST_NP(2); break;
+    case 4: DKV_FAST_NP(4); break;
     default:
       set_error("fast decode supports 1, 2 or 4 query heads per KV head");
       return DKV_ERR_UNSUPPORTED;
   }
+#undef DKV_FAST_NP
+#undef DKV_FAST_LAUNCH
   return dkv_check_launch("dkv_decode_attention(fast pages)");
 }
 

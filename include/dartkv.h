@@ -47,7 +47,7 @@ extern "C" {
 /* Thread-local description of the last error on this thread. */
 const char* dkv_last_error(void);
 
-/* ABI version; bumps when a struct below changes. */
+/* ABI version (3); bumps when a struct below changes. */
 int dkv_abi_version(void);
 
 /*
@@ -177,10 +177,20 @@ typedef struct dkv_segment {
  * [fast_first, fast_first + fast_count) must all be full 128-token pages with
  * head_dim 128, Dart keys with fast_promoted promoted channels (a multiple of
  * 16, at most 64, one key group per page), 2-bit values in groups of
- * fast_value_group channels (a multiple of 8 dividing 128), fp16 metadata and a
+ * fast_value_group channels (a multiple of 16 dividing 128), fp16 metadata and a
  * bf16 or fp16 cache, every field 16-byte aligned; the caller guarantees this.
  * Those pages are processed by the MFMA page kernel over `fast_splits` splits;
  * the other entries and the tail by the general kernel over `n_splits` splits.
+ *
+ * Dense rest: when rest_dense_tokens > 0 the caller guarantees that every entry
+ * outside the fast range and the tail are dense segments in the cache dtype
+ * (bf16 or fp16) with 16-byte aligned rows and at most rest_dense_tokens
+ * tokens each; then one wave per 32-token chunk handles them (head_dim 128, at
+ * most 8 query heads per KV head, n_splits = number of those segments *
+ * ceil(rest_dense_tokens / 32)).  A segment that breaks this yields NaN.
+ *
+ * Timing: fast_events[0] / [1], when not NULL, are hipEvent_t handles recorded
+ * on `stream` right before and right after the page kernel's launch.
  *
  * Replaces reference src/dart/fused_attention.py:654-771
  * (`fused_dart_attention`, one query token) and, for one query token,
@@ -202,6 +212,8 @@ typedef struct dkv_decode_args {
   void* workspace;
   int64_t workspace_bytes;
   int64_t fast_first, fast_count, fast_promoted, fast_value_group, fast_splits;
+  int64_t rest_dense_tokens;
+  void* fast_events[2];
 } dkv_decode_args;
 
 int64_t dkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t n_splits);

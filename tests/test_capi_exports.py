@@ -39,3 +39,27 @@ def test_library_loads_and_reports_errors_without_gpu():
     assert rc == _lib.DKV_ERR_INVALID
     assert b"bits" in lib.dkv_last_error()
     assert lib.dkv_decode_workspace_bytes(2, 4, 8, 3) == 2 * 4 * 3 * 10 * 4
+
+
+def test_ctypes_structs_match_the_header(tmp_path):
+    """Field offsets and sizes of the ctypes mirrors equal the C compiler's."""
+    import ctypes
+    from dartkv_amd import _lib
+    structs = {"dkv_segment": _lib.Segment, "dkv_decode_args": _lib.DecodeArgs,
+               "dkv_key_pages_args": _lib.KeyPagesArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dartkv.h"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'  printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = {tuple(l.split()[:2]): int(l.split()[2]) for l in out if l.strip()}
+    for cname, cls in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert got[(cname, field)] == getattr(cls, field).offset, (cname, field)
