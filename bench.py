@@ -147,6 +147,41 @@ def cpu_baseline(args, cfg, budget_s: float = 20.0) -> dict:
             "tok_s": round(1.0 / (dt * args.layers), 4)}
 
 
+def prefill_c3(torch, dart, synthetic, stream, cfg: dict) -> dict:
+    """C3 prefill: one append of [8, 8, 16384, 128] bf16 K/V into a 2-bit + 25 % cache, then 256 one-token appends.
+
+    GB/s counts the K/V bytes read plus the packed bytes written (pages, metadata, dense sink and tail).
+    """
+    B, H, T, D = 8, 8, 16384, 128
+    k, v, _ = synthetic.outlier_kv(B, H, T + 256, D, query_heads=32, dtype=torch.bfloat16, device="cuda:0")
+    kp, vp = k[:, :, :T].contiguous(), v[:, :, :T].contiguous()
+    ccfg = dict(cfg)
+    warm = dart.DartKVCache(dart.DartKVCacheConfig(**ccfg))
+    warm.append(kp[:, :, :1024], vp[:, :, :1024])
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(3):
+        cache = dart.DartKVCache(dart.DartKVCacheConfig(**ccfg))
+        torch.cuda.synchronize()
+        e0.record(stream)
+        cache.append(kp, vp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    ms = min(times)
+    read = 2 * B * H * T * D * 2
+    written = cache.storage_bytes
+    e0.record(stream)
+    for i in range(256):
+        cache.append(k[:, :, T + i:T + i + 1], v[:, :, T + i:T + i + 1])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return {"workload": "C3 prefill: batch 8, 8 KV heads, 16384 tokens, head_dim 128, bf16, 2-bit + 25 %",
+            "ms": round(ms, 3), "bytes_read": read, "bytes_written": written,
+            "gbs": round((read + written) / (ms * 1e-3) / 1e9, 2),
+            "append_us": round(e0.elapsed_time(e1) / 256 * 1e3, 2)}
+
+
 def config2_latency_us(torch, dart, synthetic, stream) -> float:
     """Mean time of one decode call on config 2 (B1, T1024, 8/32 heads, 2-bit + 25 %)."""
     k2, v2, q2 = synthetic.outlier_kv(1, 8, 1024, 128, query_heads=32, dtype=torch.bfloat16, device="cuda:0")
@@ -180,7 +215,7 @@ def main() -> int:
     p.add_argument("--bits", choices=["2b25", "4b"], default="2b25")
     p.add_argument("--splits", type=int, default=0, help="split-K count (0 = heuristic)")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--no-c2", action="store_true", help="skip the config-2 latency probe (clean profiles)")
+    p.add_argument("--no-c2", action="store_true", help="skip the config-2 latency and C3 prefill probes (clean profiles)")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="after timing, copy a MIB-MiB buffer 3 times (known bytes for PMC counter calibration)")
     args = p.parse_args()
@@ -236,6 +271,10 @@ def main() -> int:
     achieved = fast_bytes / (avg_kernel_ms * 1e-3) / 1e9
     tok_s = args.batch / (ms_per_step * 1e-3)
 
+    prefill = None
+    if not args.no_c2:
+        prefill = prefill_c3(torch, dart, synthetic, stream, cfg)
+
     if args.calibrate_copy:
         src = torch.empty(args.calibrate_copy << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
         dst = torch.empty_like(src)
@@ -274,6 +313,7 @@ def main() -> int:
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "decode_tok_s": round(tok_s, 2),
         "c2_latency_us": None if c2_us is None else round(c2_us, 2),
+        "prefill_c3": prefill,
         "wall_s_timed": round(wall, 3),
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",

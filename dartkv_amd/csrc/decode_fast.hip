@@ -454,18 +454,29 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     // ---- S = Q K; tile t covers tokens 64t + 16(n/4) + 4 slot + n%4 ----
     float4v S[2];
     S[0] = S[1] = float4v{0.f, 0.f, 0.f, 0.f};
-    // 2-bit codes of every channel (promoted channels have zero tables)
+    // 2-bit codes of every channel (promoted channels have zero tables);
+    // block cb + 1's codes and table are read before block cb is computed
     {
       const int row = M.kl + 32 * kq + qd;
       const int tab = M.klut + 8 * kq;
+      uint32_t w0 = lds_u32(lds, row), w1 = lds_u32(lds, row + 16);
+      uint2 t = *(const uint2*)(lds + tab);
 #pragma unroll
       for (int cb = 0; cb < kD / 4; ++cb) {
-        const uint32_t w0 = lds_u32(lds, row + 128 * cb), w1 = lds_u32(lds, row + 128 * cb + 16);
-        const uint2 t = *(const uint2*)(lds + tab + 32 * cb);
+        uint32_t nw0 = 0, nw1 = 0;
+        uint2 nt = make_uint2(0u, 0u);
+        if (cb + 1 < kD / 4) {
+          nw0 = lds_u32(lds, row + 128 * (cb + 1));
+          nw1 = lds_u32(lds, row + 128 * (cb + 1) + 16);
+          nt = *(const uint2*)(lds + tab + 32 * (cb + 1));
+        }
         S[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], lookup4((w0 >> sh) & 0x03030303u, t.x, t.y), S[0], 0, 0,
                                                      0);
         S[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], lookup4((w1 >> sh) & 0x03030303u, t.x, t.y), S[1], 0, 0,
                                                      0);
+        w0 = nw0;
+        w1 = nw1;
+        t = nt;
       }
     }
     // promoted channels: 4-bit codes, slot j = 4pb + kq of the high codes

@@ -10,6 +10,8 @@
 //   (quantization.py:96-109, mixed.py:72-94).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "dkv_capi_util.h"
 #include "dkv_device.h"
 #include "dkv_select.h"
@@ -71,6 +73,65 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_aligned(RowsParams p) 
       byte |= dev_group_code(row_elem(p, r, i), mn, s, qmax, p.src_dtype) << (j * p.bits);
     }
     out[b] = (uint8_t)byte;
+  }
+}
+
+// Contiguous rows, groups of 8 * L elements (L = 1..64 lanes, a power of two)
+// that tile the row exactly: every lane owns 8 consecutive elements (one
+// 16-byte load for 16-bit sources), the L lanes of a group reduce min/max with
+// cross-lane shuffles, and every lane stores its 8 codes packed (2, 4 or 8
+// bytes).  A wave's loads and stores are contiguous.
+template <int BITS>
+__global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int lanes_per_group) {
+  const int64_t lanes_per_row = p.n / 8;
+  const int64_t total = p.rows * lanes_per_row;
+  const float qmax = (float)((1 << BITS) - 1);
+  const int lane = threadIdx.x & 63;
+  for (int64_t v = (int64_t)blockIdx.x * kThreads + threadIdx.x; v - lane < total;
+       v += (int64_t)gridDim.x * kThreads) {
+    // whole waves stay in the loop so the shuffles see every lane of a group
+    const bool active = v < total;
+    const int64_t r = active ? v / lanes_per_row : 0;
+    const int64_t i0 = active ? (v % lanes_per_row) * 8 : 0;
+    float x[8];
+    if (p.src_dtype == kF32) {
+      const float4* src = (const float4*)((const float*)p.src + r * p.row_stride + i0);
+      const float4 a = src[0], b = src[1];
+      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+      x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+      const uint4 w = *(const uint4*)((const uint16_t*)p.src + r * p.row_stride + i0);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint16_t bits = (uint16_t)(ww[j / 2] >> (16 * (j % 2)));
+        x[j] = p.src_dtype == kBF16 ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
+      }
+    }
+    float mn = x[0], mx = x[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) {
+      mn = fminf(mn, x[j]);
+      mx = fmaxf(mx, x[j]);
+    }
+    for (int off = 1; off < lanes_per_group; off <<= 1) {
+      mn = fminf(mn, __shfl_xor(mn, off, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    }
+    if (!active) continue;
+    const float s = dev_group_scale(mn, mx, qmax, p.src_dtype);
+    if (i0 % p.group == 0) {
+      const int64_t g = i0 / p.group;
+      dev_store_meta(p.scale, r * p.groups + g, s, p.meta_dtype);
+      dev_store_meta(p.zero, r * p.groups + g, mn, p.meta_dtype);
+    }
+    uint64_t packed = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) packed |= (uint64_t)dev_group_code(x[j], mn, s, qmax, p.src_dtype) << (j * BITS);
+    uint8_t* out = p.values + r * p.packed_bytes + i0 * BITS / 8;
+    if (BITS == 2) *(uint16_t*)out = (uint16_t)packed;
+    else if (BITS == 4) *(uint32_t*)out = (uint32_t)packed;
+    else *(uint2*)out = make_uint2((uint32_t)packed, (uint32_t)(packed >> 32));
   }
 }
 
@@ -282,6 +343,230 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_kernel(KeyParams 
   }
 }
 
+// LDS-tiled key page kernel for 16-bit sources with unit channel stride:
+// one workgroup per (batch * head, page).  The page's [T][D] tile is staged
+// in LDS with 16-byte loads (rows padded by 4 bytes so a column read is
+// conflict-free), per-channel statistics and the channel scores are read from
+// LDS (same reduction order as channel_mean), the top-k selection runs on one
+// lane, codes are packed into LDS buffers, and the packed page is written out
+// with 16-byte stores.
+constexpr int kKeyTileMaxBytes = 48 * 1024;
+
+__host__ __device__ inline int key_tile_row_bytes(int D) { return 2 * D + 4; }
+
+__device__ __forceinline__ float tile_elem(const uint8_t* tile, int rs, int T, int t, int c, int dt) {
+  if (t >= T) t = T - 1;  // replicate the last token (mixed.py:196-197, quantization.py:174-177)
+  const uint16_t bits = *(const uint16_t*)(tile + t * rs + 2 * c);
+  return dt == kBF16 ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
+}
+
+// Token mean of f(x) over the T real tokens of channel c (mode 0: |x|;
+// mode 1: rnd(rnd(x - center)^2)) with ATen's CPU cascade order.
+__device__ float tile_channel_mean(const uint8_t* tile, int rs, int T, int c, int dt, int mode, float center) {
+  const int lp = cascade_level_power(T);
+  const int step = 1 << lp, mask = step - 1;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int i = 0;
+  auto term = [&](int t) -> float {
+    const float x = tile_elem(tile, rs, T, t, c, dt);
+    if (mode == 0) return fabsf(x);
+    if (mode == 2) return x;
+    const float d = dev_round_to(__fsub_rn(x, center), dt);
+    return dev_round_to(__fmul_rn(d, d), dt);
+  };
+  for (; i + step <= T;) {
+    for (int j = 0; j < step; ++j, ++i) acc[0] = __fadd_rn(acc[0], term(i));
+    for (int j = 1; j < 4; ++j) {
+      acc[j] = __fadd_rn(acc[j], acc[j - 1]);
+      acc[j - 1] = 0.f;
+      if ((i & (mask << (j * lp))) != 0) break;
+    }
+  }
+  for (; i < T; ++i) acc[0] = __fadd_rn(acc[0], term(i));
+  for (int j = 1; j < 4; ++j) acc[0] = __fadd_rn(acc[0], acc[j]);
+  return dev_round_to(__fdiv_rn(acc[0], (float)T), dt);
+}
+
+// mode kKeyAll: scores, selection on one lane, codes (small pages).
+// mode kKeyScores: scores only, written as D floats at the start of the
+//   page's low-code region (overwritten later by kKeyCodes).
+// mode kKeyCodes: codes with the promoted channels read back from `idx`.
+constexpr int kKeyAll = 0, kKeyScores = 1, kKeyCodes = 2;
+
+__global__ void __launch_bounds__(kThreads) quantize_key_pages_tiled(KeyParams k, int mode) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t ksm[];
+  const dkv_key_pages_args& a = k.a;
+  const int bh = blockIdx.x, page = blockIdx.y;
+  const int b = bh / (int)a.H, h = bh % (int)a.H;
+  const int D = (int)a.D, T = (int)a.page_tokens, dt = (int)a.src_dtype, meta = (int)a.meta_dtype;
+  const bool mixed = a.key_mode == DKV_KEY_MIXED;
+  const int K = mixed ? (int)a.promoted : 0;
+  const int G = (int)k.G, group = (int)a.group;
+  const int rs = key_tile_row_bytes(D);
+  const int bits = mixed ? 2 : (int)a.bits;
+  const int per_byte = 8 / bits;
+  const int row_bytes = mixed ? G * (int)k.nb : (int)k.pk;  // packed bytes per channel row
+
+  uint8_t* tile = ksm;                                           // [T][rs]
+  float* score = (float*)(ksm + ((T * rs + 15) & ~15));          // [D]
+  float* mn_s = score + D;                                       // [D][G]
+  float* sc_s = mn_s + D * G;                                    // [D][G]
+  int32_t* slot = (int32_t*)(sc_s + D * G);                      // [D]
+  int32_t* sel = slot + D;                                       // [D]
+  SelItem* work = (SelItem*)(sel + D);                           // [D]
+  uint8_t* lowb = (uint8_t*)(((uintptr_t)(work + D) + 15) & ~(uintptr_t)15);  // [D][row_bytes]
+  uint8_t* highb = lowb + ((D * row_bytes + 15) & ~15);          // [K][row_bytes]
+
+  // ---- stage the tile ----
+  const uint16_t* src = (const uint16_t*)a.src + b * a.sb + h * a.sh + (int64_t)page * T * a.st;
+  const int vecs = D / 8;
+  for (int i = threadIdx.x; i < T * vecs; i += kThreads) {
+    const int t = i / vecs, c8 = i % vecs;
+    const uint4 w = *(const uint4*)(src + (int64_t)t * a.st + 8 * c8);
+    uint32_t* dst = (uint32_t*)(tile + t * rs + 16 * c8);
+    dst[0] = w.x;
+    dst[1] = w.y;
+    dst[2] = w.z;
+    dst[3] = w.w;
+  }
+  for (int c = threadIdx.x; c < D; c += kThreads) slot[c] = -1;
+  __syncthreads();
+
+  // ---- per-channel statistics and scores ----
+  for (int c = threadIdx.x; c < D; c += kThreads) {
+    for (int g = 0; g < G; ++g) {
+      float mn = tile_elem(tile, rs, T, g * group, c, dt), mx = mn;
+      for (int j = 1; j < group; ++j) {
+        const float x = tile_elem(tile, rs, T, g * group + j, c, dt);
+        mn = fminf(mn, x);
+        mx = fmaxf(mx, x);
+      }
+      mn_s[c * G + g] = mn;
+      sc_s[c * G + g] = mx;  // max for now; the scale needs qmax, known after selection
+    }
+    if (mode != kKeyCodes && mixed && K > 0 && K < D && a.selection != DKV_SELECT_GIVEN) {
+      float sc;
+      if (a.selection == DKV_SELECT_MAGNITUDE) {
+        sc = tile_channel_mean(tile, rs, T, c, dt, 0, 0.f);
+      } else {
+        const float m = tile_channel_mean(tile, rs, T, c, dt, 2, 0.f);  // mixed.py:159-160
+        sc = tile_channel_mean(tile, rs, T, c, dt, 1, m);
+      }
+      if (mode == kKeyScores)
+        ((float*)(a.low + page * a.low_page_stride + (int64_t)bh * D * row_bytes))[c] = sc;
+      else
+        score[c] = sc;
+    }
+  }
+  if (mode == kKeyScores) return;
+  __syncthreads();
+
+  // ---- channel selection ----
+  if (mixed && K > 0) {
+    const int32_t* idx_in = (const int32_t*)((const char*)a.idx + page * a.idx_page_stride) + (int64_t)bh * K;
+    if (K < D && a.selection != DKV_SELECT_GIVEN) {
+      if (mode == kKeyCodes) {
+        for (int j = threadIdx.x; j < K; j += kThreads) sel[j] = idx_in[j];
+      } else if (threadIdx.x == 0) {
+        select_topk(score, D, K, work, sel);
+      }
+    } else {
+      for (int j = threadIdx.x; j < K; j += kThreads) sel[j] = (K == D) ? j : a.given_idx[h * K + j];
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < K; j += kThreads) {
+      const int32_t ch = sel[j];
+      if (ch >= 0 && ch < D) slot[ch] = j;
+    }
+    int32_t* idx_out = (int32_t*)((char*)a.idx + page * a.idx_page_stride) + (int64_t)bh * K;
+    for (int j = threadIdx.x; j < K; j += kThreads) idx_out[j] = sel[j];
+    __syncthreads();
+  }
+
+  // ---- scales and zero points ----
+  void* scale = (char*)a.scale + page * a.scale_page_stride;
+  void* zero = (char*)a.zero + page * a.zero_page_stride;
+  for (int i = threadIdx.x; i < D * G; i += kThreads) {
+    const int c = i / G;
+    const float qmax = mixed ? (slot[c] >= 0 ? 15.0f : 3.0f) : (float)((1 << a.bits) - 1);
+    const float mn = mn_s[i];
+    const float sc = dev_group_scale(mn, sc_s[i], qmax, dt);
+    sc_s[i] = sc;
+    dev_store_meta(scale, (int64_t)bh * D * G + i, sc, meta);
+    dev_store_meta(zero, (int64_t)bh * D * G + i, mn, meta);
+  }
+  __syncthreads();
+
+  // ---- codes: thread (channel c, byte p), channel fastest ----
+  for (int i = threadIdx.x; i < D * row_bytes; i += kThreads) {
+    const int c = i % D, p = i / D;
+    const int32_t sl = mixed ? slot[c] : -1;
+    const float qmax = mixed ? (sl >= 0 ? 15.0f : 3.0f) : (float)((1 << a.bits) - 1);
+    uint32_t lo = 0, hi = 0;
+    if (mixed) {
+      // byte p of a channel row: group p / nb, tokens 4 (p % nb) + j of that group
+      const int g = p / (int)k.nb, q = p % (int)k.nb;
+      const float mn = mn_s[c * G + g], sc = sc_s[c * G + g];
+      for (int j = 0; j < 4; ++j) {
+        const int w = 4 * q + j;
+        if (w >= group) break;
+        const uint32_t code = dev_group_code(tile_elem(tile, rs, T, g * group + w, c, dt), mn, sc, qmax, dt);
+        lo |= (code & 3u) << (2 * j);
+        hi |= (code >> 2) << (2 * j);
+      }
+      if (sl >= 0) highb[sl * row_bytes + p] = (uint8_t)hi;
+    } else {
+      const int padded = G * group;
+      for (int j = 0; j < per_byte; ++j) {
+        const int t = p * per_byte + j;
+        if (t >= padded) break;
+        const int g = t / group;
+        lo |= dev_group_code(tile_elem(tile, rs, T, t, c, dt), mn_s[c * G + g], sc_s[c * G + g], qmax, dt)
+              << (j * bits);
+      }
+    }
+    lowb[c * row_bytes + p] = (uint8_t)lo;
+  }
+  __syncthreads();
+
+  // ---- write the packed rows (contiguous per (batch, head)) ----
+  uint8_t* low = a.low + page * a.low_page_stride + (int64_t)bh * D * row_bytes;
+  const int lbytes = D * row_bytes;
+  for (int i = threadIdx.x; i < lbytes / 16; i += kThreads) ((uint4*)low)[i] = ((const uint4*)lowb)[i];
+  for (int i = (lbytes / 16) * 16 + threadIdx.x; i < lbytes; i += kThreads) low[i] = lowb[i];
+  if (mixed && K > 0) {
+    uint8_t* high = a.high + page * a.high_page_stride + (int64_t)bh * K * row_bytes;
+    const int hbytes = K * row_bytes;
+    for (int i = threadIdx.x; i < hbytes / 16; i += kThreads) ((uint4*)high)[i] = ((const uint4*)highb)[i];
+    for (int i = (hbytes / 16) * 16 + threadIdx.x; i < hbytes; i += kThreads) high[i] = highb[i];
+  }
+}
+
+// Promoted-channel selection for many pages at once: one lane per
+// (batch * head, page) runs the exact top-k on the scores kKeyScores left in
+// the page's low-code region and writes the channel indices.
+__global__ void __launch_bounds__(kThreads) key_select_pages(KeyParams k, int row_bytes) {
+  const dkv_key_pages_args& a = k.a;
+  const int64_t item = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t bhs = a.B * a.H;
+  if (item >= bhs * a.n_pages) return;
+  const int64_t page = item / bhs, bh = item % bhs;
+  const int D = (int)a.D, K = (int)a.promoted;
+  const float* score = (const float*)(a.low + page * a.low_page_stride + bh * D * row_bytes);
+  SelItem work[kThreads];
+  int32_t* idx_out = (int32_t*)((char*)a.idx + page * a.idx_page_stride) + bh * K;
+  select_topk(score, D, K, work, idx_out);
+}
+
+__host__ inline size_t key_tiled_smem(int D, int T, int G, int K, int row_bytes) {
+  size_t o = ((size_t)T * key_tile_row_bytes(D) + 15) & ~(size_t)15;
+  o += sizeof(float) * ((size_t)D + 2 * (size_t)D * G) + 2 * sizeof(int32_t) * D + sizeof(SelItem) * D;
+  o = (o + 15) & ~(size_t)15;
+  o += ((size_t)D * row_bytes + 15) & ~(size_t)15;
+  o += (size_t)K * row_bytes;
+  return o;
+}
+
 // ---------------------------------------------------------------------------
 // dequantize
 // ---------------------------------------------------------------------------
@@ -363,7 +648,19 @@ extern "C" int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, i
   p.scale = scale;
   p.zero = zero;
   hipStream_t s = (hipStream_t)stream;
-  if (group % p.per_byte == 0) {
+  const int esize = src_dtype == kF32 ? 4 : 2;
+  const bool vec = elem_stride == 1 && n % 8 == 0 && group % 8 == 0 && group <= 512 && (group & (group - 1)) == 0 &&
+                   n % group == 0 && ((uintptr_t)src % 16) == 0 && (row_stride * esize) % 16 == 0 &&
+                   (src_dtype == kF32 || src_dtype == kF16 || src_dtype == kBF16) && ((uintptr_t)values % 8) == 0 &&
+                   (p.packed_bytes * bits) % 8 == 0 && (p.packed_bytes % 8) == 0;
+  if (vec) {
+    const int64_t lanes = rows * (n / 8);
+    const int64_t blocks = std::min<int64_t>((lanes + kThreads - 1) / kThreads, 1 << 20);
+    const int lpg = (int)(group / 8);
+    if (bits == 2) hipLaunchKernelGGL(quantize_rows_vec<2>, dim3((unsigned)blocks), dim3(kThreads), 0, s, p, lpg);
+    else if (bits == 4) hipLaunchKernelGGL(quantize_rows_vec<4>, dim3((unsigned)blocks), dim3(kThreads), 0, s, p, lpg);
+    else hipLaunchKernelGGL(quantize_rows_vec<8>, dim3((unsigned)blocks), dim3(kThreads), 0, s, p, lpg);
+  } else if (group % p.per_byte == 0) {
     const int64_t items = rows * p.groups;
     hipLaunchKernelGGL(quantize_rows_aligned, dim3((unsigned)((items + kThreads - 1) / kThreads)), dim3(kThreads), 0,
                        s, p);
@@ -400,6 +697,33 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
   k.nb = (a.group + 3) / 4;
   const int per_byte = a.key_mode == DKV_KEY_UNIFORM ? (int)(8 / a.bits) : 4;
   k.pk = (k.G * a.group + per_byte - 1) / per_byte;
+  const int row_bytes = a.key_mode == DKV_KEY_MIXED ? (int)(k.G * k.nb) : (int)k.pk;
+  const int Kp = a.key_mode == DKV_KEY_MIXED ? (int)a.promoted : 0;
+  const size_t tiled = key_tiled_smem((int)a.D, (int)a.page_tokens, (int)k.G, Kp, row_bytes);
+  const bool use_tiled = (a.src_dtype == kBF16 || a.src_dtype == kF16) && a.sd == 1 && a.D % 8 == 0 &&
+                         a.D <= kThreads && a.st % 8 == 0 && a.sb % 8 == 0 && a.sh % 8 == 0 &&
+                         ((uintptr_t)a.src % 16) == 0 && ((a.page_tokens * a.st) % 8) == 0 &&
+                         (size_t)a.page_tokens * key_tile_row_bytes((int)a.D) <= (size_t)kKeyTileMaxBytes &&
+                         tiled <= 64 * 1024 && ((uintptr_t)a.low % 16) == 0 && (a.low_page_stride % 16) == 0 &&
+                         ((int64_t)a.D * row_bytes) % 16 == 0 &&
+                         (Kp == 0 || (((uintptr_t)a.high % 16) == 0 && (a.high_page_stride % 16) == 0 &&
+                                      ((int64_t)Kp * row_bytes) % 16 == 0));
+  if (use_tiled) {
+    const dim3 grid((unsigned)(a.B * a.H), (unsigned)a.n_pages);
+    hipStream_t s = (hipStream_t)stream;
+    const bool select = a.key_mode == DKV_KEY_MIXED && Kp > 0 && Kp < a.D && a.selection != DKV_SELECT_GIVEN;
+    if (select && row_bytes >= 4) {
+      // scores -> one lane per page selects -> codes
+      hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyScores);
+      const int64_t items = a.B * a.H * a.n_pages;
+      hipLaunchKernelGGL(key_select_pages, dim3((unsigned)((items + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
+                         k, row_bytes);
+      hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyCodes);
+    } else {
+      hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyAll);
+    }
+    return dkv_check_launch("dkv_quantize_key_pages");
+  }
   const size_t shmem = (size_t)a.D * (sizeof(float) + 2 * sizeof(int32_t) + sizeof(SelItem));
   DKV_CHECK(shmem <= 64 * 1024, DKV_ERR_UNSUPPORTED, "head_dim %lld is too large", (long long)a.D);
   hipLaunchKernelGGL(quantize_key_pages_kernel, dim3((unsigned)(a.B * a.H), (unsigned)a.n_pages), dim3(kThreads),
