@@ -105,8 +105,9 @@ __device__ __forceinline__ uint32_t round_pair_to_bf16_precision(uint32_t x) {
 }
 
 // Exact dequantized values for codes (c0, c1) of one (scale, zero) pair, as
-// an fp16 pair: fp16(fp16(code*s) + z), then bf16 precision if requested.
-__device__ __forceinline__ uint32_t lut_pair(uint32_t codes_h2, uint32_t s_h2, uint32_t z_h2, bool bf16) {
+// an fp16 pair: fp16(fp16(code*s) + z), then bf16 precision if BF16.
+template <bool BF16>
+__device__ __forceinline__ uint32_t lut_pair(uint32_t codes_h2, uint32_t s_h2, uint32_t z_h2) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   h2 c = __builtin_bit_cast(h2, codes_h2);
   h2 s = __builtin_bit_cast(h2, s_h2);
@@ -114,14 +115,15 @@ __device__ __forceinline__ uint32_t lut_pair(uint32_t codes_h2, uint32_t s_h2, u
   h2 prod = c * s;  // -ffp-contract=off keeps the multiply and the add separate
   h2 sum = prod + z;
   uint32_t r = __builtin_bit_cast(uint32_t, sum);
-  return bf16 ? round_pair_to_bf16_precision(r) : r;
+  return BF16 ? round_pair_to_bf16_precision(r) : r;
 }
 
 // Byte-plane table of the 4 values for codes 0..3: x = low bytes, y = high bytes.
-__device__ __forceinline__ uint2 build_lut4(uint32_t s, uint32_t z, bool bf16) {
+template <bool BF16>
+__device__ __forceinline__ uint2 build_lut4(uint32_t s, uint32_t z) {
   const uint32_t s2 = s * 0x10001u, z2 = z * 0x10001u;
-  const uint32_t v01 = lut_pair(0x3c000000u, s2, z2, bf16);  // codes (0, 1)
-  const uint32_t v23 = lut_pair(0x42004000u, s2, z2, bf16);  // codes (2, 3)
+  const uint32_t v01 = lut_pair<BF16>(0x3c000000u, s2, z2);  // codes (0, 1)
+  const uint32_t v23 = lut_pair<BF16>(0x42004000u, s2, z2);  // codes (2, 3)
   return make_uint2(perm(v23, v01, 0x06040200u), perm(v23, v01, 0x07050301u));
 }
 
@@ -166,16 +168,31 @@ struct PageAddr {
   const uint16_t *ks, *kz, *vs, *vz;
 };
 
-__device__ __forceinline__ PageAddr page_addr(const dkv_segment& s, int64_t bh) {
+// The descriptor is the same for the whole wave: it is read through the
+// constant address space (scalar loads) and its fields are kept in scalar
+// registers, so the address arithmetic runs on the scalar unit.
+typedef __attribute__((address_space(4))) const dkv_segment const_segment;
+
+__device__ __forceinline__ const_segment& descriptor(const dkv_segment* table, int i) {
+  return ((const_segment*)table)[i];
+}
+
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ PageAddr page_addr(const_segment& s, int64_t bh) {
   PageAddr p;
-  p.kl = (const uint8_t*)s.key[0] + bh * s.key_bh[0];
-  p.kh = (const uint8_t*)s.key[1] + bh * s.key_bh[1];
-  p.ki = (const int32_t*)s.key[2] + bh * s.key_bh[2];
-  p.ks = (const uint16_t*)s.key[3] + bh * s.key_bh[3];
-  p.kz = (const uint16_t*)s.key[4] + bh * s.key_bh[4];
-  p.vc = (const uint8_t*)s.value[0] + bh * s.value_bh[0];
-  p.vs = (const uint16_t*)s.value[1] + bh * s.value_bh[1];
-  p.vz = (const uint16_t*)s.value[2] + bh * s.value_bh[2];
+  p.kl = (const uint8_t*)uniform_u64(s.key[0] + (uint64_t)(bh * (int64_t)uniform_u64((uint64_t)s.key_bh[0])));
+  p.kh = (const uint8_t*)uniform_u64(s.key[1] + (uint64_t)(bh * (int64_t)uniform_u64((uint64_t)s.key_bh[1])));
+  p.ki = (const int32_t*)uniform_u64(s.key[2] + (uint64_t)(4 * bh * (int64_t)uniform_u64((uint64_t)s.key_bh[2])));
+  p.ks = (const uint16_t*)uniform_u64(s.key[3] + (uint64_t)(2 * bh * (int64_t)uniform_u64((uint64_t)s.key_bh[3])));
+  p.kz = (const uint16_t*)uniform_u64(s.key[4] + (uint64_t)(2 * bh * (int64_t)uniform_u64((uint64_t)s.key_bh[4])));
+  p.vc = (const uint8_t*)uniform_u64(s.value[0] + (uint64_t)(bh * (int64_t)uniform_u64((uint64_t)s.value_bh[0])));
+  p.vs = (const uint16_t*)uniform_u64(s.value[1] + (uint64_t)(2 * bh * (int64_t)uniform_u64((uint64_t)s.value_bh[1])));
+  p.vz = (const uint16_t*)uniform_u64(s.value[2] + (uint64_t)(2 * bh * (int64_t)uniform_u64((uint64_t)s.value_bh[2])));
   return p;
 }
 
@@ -279,6 +296,33 @@ __device__ __forceinline__ float uniform(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
+// 4-bit key tables of the NP promoted slots: lanes (2j, 2j+1) build entries
+// 0..7 / 8..15 of slot j (byte planes: low bytes at +0, high bytes at +16).
+template <bool BF16, int NP>
+__device__ __forceinline__ void build_lut16_tables(const LdsMap& M, uint8_t* lds, const uint16_t* ks,
+                                                   const uint16_t* kz, int lane) {
+  const uint8_t* pidx = lds + M.pidx;
+#pragma unroll
+  for (int j0 = 0; j0 < NP; j0 += 32) {
+    const int j = j0 + (lane >> 1);
+    if (j < NP) {
+      const int half = lane & 1;
+      const int c = pidx[j];
+      const uint32_t s2 = (uint32_t)ks[c] * 0x10001u, z2 = (uint32_t)kz[c] * 0x10001u;
+      // fp16 code pairs (8 half + 2q, 8 half + 2q + 1), q = 0..3
+      const uint32_t e0 = half ? 0x48804800u : 0x3c000000u;  // (8, 9)   | (0, 1)
+      const uint32_t e1 = half ? 0x49804900u : 0x42004000u;  // (10, 11) | (2, 3)
+      const uint32_t e2 = half ? 0x4a804a00u : 0x45004400u;  // (12, 13) | (4, 5)
+      const uint32_t e3 = half ? 0x4b804b00u : 0x47004600u;  // (14, 15) | (6, 7)
+      const uint32_t v0 = lut_pair<BF16>(e0, s2, z2), v1 = lut_pair<BF16>(e1, s2, z2);
+      const uint32_t v2 = lut_pair<BF16>(e2, s2, z2), v3 = lut_pair<BF16>(e3, s2, z2);
+      uint8_t* t16 = lds + M.klut16 + 32 * j + 8 * half;
+      *(uint2*)t16 = make_uint2(perm(v1, v0, 0x06040200u), perm(v3, v2, 0x06040200u));
+      *(uint2*)(t16 + 16) = make_uint2(perm(v1, v0, 0x07050301u), perm(v3, v2, 0x07050301u));
+    }
+  }
+}
+
 // O[j] += a * B_j for the 8 channel tiles j of one 16-token block in the
 // heads-in-rows layout (rows 0..3 = query heads, K = 4 tokens per lane).
 // x[m]: 16 bits = codes of the lane's 8 channels for token row m (m = 0..3);
@@ -301,9 +345,10 @@ __device__ __forceinline__ void mma_lut_block(half4 a, const uint32_t x[4], cons
   }
 }
 
-// GQ: query heads per KV head; NP: promoted channels (16, 32, 48 or 64).
-// Both are compile-time so every block loop unrolls with immediate offsets.
-template <int GQ, int NP>
+// GQ: query heads per KV head; NP: promoted channels (16, 32, 48 or 64);
+// BF16: cache dtype bf16 (else fp16).  All compile-time, so every block loop
+// unrolls with immediate offsets and the table builds carry no dtype tests.
+template <int GQ, int NP, bool BF16>
 __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
@@ -312,16 +357,17 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   const int worker = blockIdx.x * kWaves + wave;
   const int total_workers = p.B * p.Hkv * p.splits;
   if (worker >= total_workers) return;
-  const int split = worker % p.splits;
-  const int bh = worker / p.splits;
-  const int b = bh / p.Hkv, kvh = bh % p.Hkv;
+  // wave-uniform indices (kept in scalar registers)
+  const int split = __builtin_amdgcn_readfirstlane(worker % p.splits);
+  const int bh = __builtin_amdgcn_readfirstlane(worker / p.splits);
+  const int b = __builtin_amdgcn_readfirstlane(bh / p.Hkv), kvh = __builtin_amdgcn_readfirstlane(bh % p.Hkv);
   constexpr int np = NP;
+  constexpr bool bf16 = BF16;
   const int gv = p.gv;
   const LdsMap M = lds_map(np, gv);
   uint8_t* lds = smem + wave * M.bytes;
-  const int page0 = (int)(((int64_t)split * p.count) / p.splits);
-  const int page1 = (int)(((int64_t)(split + 1) * p.count) / p.splits);
-  const bool bf16 = p.bf16 != 0;
+  const int page0 = __builtin_amdgcn_readfirstlane((int)(((int64_t)split * p.count) / p.splits));
+  const int page1 = __builtin_amdgcn_readfirstlane((int)(((int64_t)(split + 1) * p.count) / p.splits));
 
   // ---- per-lane constants ----
   const int sh = 2 * (n & 3);             // bit offset of this lane's codes in each byte
@@ -376,7 +422,7 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     }
   }
   if (page0 < page1) {
-    const PageAddr a0 = page_addr(p.segs[p.first + page0], bh);
+    const PageAddr a0 = page_addr(descriptor(p.segs, p.first + page0), bh);
     issue_small(M, lds, a0, np, gv, lane);
     issue_keys(M, lds, a0, np, lane);
     issue_values(M, lds, a0, lane);
@@ -387,13 +433,12 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   for (int pg = page0; pg < page1; ++pg) {
     const bool has_next = pg + 1 < page1;
     PageAddr nxt;
-    if (has_next) nxt = page_addr(p.segs[p.first + pg + 1], bh);
+    if (has_next) nxt = page_addr(descriptor(p.segs, p.first + pg + 1), bh);
     // outstanding, oldest first: scales (this page), key codes (this page),
     // value codes (this page, 4 loads); the values may still be in flight
     vm_wait(4);
 
-    // ---- promoted channels: flags and a private copy of the indices (the
-    // index region is refilled with the next page's before Q K runs) ----
+    // ---- promoted channels: flags and a byte-wide copy of the indices ----
     uint8_t* flag = lds + M.pt;
     uint8_t* pidx = lds + M.pidx;
     flag[lane] = 0;
@@ -406,59 +451,27 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     }
     lds_sync();
 
-    // ---- exact-value tables and the promoted channels' query ----
-    {
-      const uint16_t* ks = (const uint16_t*)(lds + M.ks);
-      const uint16_t* kz = (const uint16_t*)(lds + M.kz);
+    // ---- 2-bit key tables (the 2-bit pass reads them) ----
+    const uint16_t* ks = (const uint16_t*)(lds + M.ks);
+    const uint16_t* kz = (const uint16_t*)(lds + M.kz);
 #pragma unroll
-      for (int c = lane; c < kD; c += 64)
-        *(uint2*)(lds + M.klut + 8 * c) = flag[c] ? make_uint2(0u, 0u) : build_lut4(ks[c], kz[c], bf16);
-      // 4-bit tables: lanes (2j, 2j+1) build entries 0..7 / 8..15 of slot j
-#pragma unroll
-      for (int j0 = 0; j0 < np; j0 += 32) {
-        const int j = j0 + (lane >> 1);
-        if (j < np) {
-          const int half = lane & 1;
-          const int c = pidx[j];
-          const uint32_t s2 = (uint32_t)ks[c] * 0x10001u, z2 = (uint32_t)kz[c] * 0x10001u;
-          // fp16 code pairs (8 half + 2q, 8 half + 2q + 1), q = 0..3
-          const uint32_t e0 = half ? 0x48804800u : 0x3c000000u;  // (8, 9)   | (0, 1)
-          const uint32_t e1 = half ? 0x49804900u : 0x42004000u;  // (10, 11) | (2, 3)
-          const uint32_t e2 = half ? 0x4a804a00u : 0x45004400u;  // (12, 13) | (4, 5)
-          const uint32_t e3 = half ? 0x4b804b00u : 0x47004600u;  // (14, 15) | (6, 7)
-          const uint32_t v0 = lut_pair(e0, s2, z2, bf16), v1 = lut_pair(e1, s2, z2, bf16);
-          const uint32_t v2 = lut_pair(e2, s2, z2, bf16), v3 = lut_pair(e3, s2, z2, bf16);
-          uint8_t* t16 = lds + M.klut16 + 32 * j + 8 * half;
-          *(uint2*)t16 = make_uint2(perm(v1, v0, 0x06040200u), perm(v3, v2, 0x06040200u));
-          *(uint2*)(t16 + 16) = make_uint2(perm(v1, v0, 0x07050301u), perm(v3, v2, 0x07050301u));
-        }
-      }
-      const uint16_t* vs = (const uint16_t*)(lds + M.vs);
-      const uint16_t* vz = (const uint16_t*)(lds + M.vz);
-      for (int g = 0; g < gv; ++g) {
-#pragma unroll
-        for (int t = lane; t < kPage; t += 64)
-          *(uint2*)(lds + M.vlut + kVlutStride * g + 8 * t) = build_lut4(vs[t * gv + g], vz[t * gv + g], bf16);
-      }
-      const uint16_t* q16 = (const uint16_t*)(lds + M.q16);
-      uint16_t* qp = (uint16_t*)(lds + M.qp);
-#pragma unroll
-      for (int i = lane; i < GQ * np; i += 64) {
-        const int h = i / np, j = i % np;
-        qp[h * (kQpStride / 2) + j] = q16[h * kD + pidx[j]];
-      }
-    }
+    for (int c = lane; c < kD; c += 64)
+      *(uint2*)(lds + M.klut + 8 * c) = flag[c] ? make_uint2(0u, 0u) : build_lut4<bf16>(ks[c], kz[c]);
     lds_sync();
-    if (has_next) issue_small(M, lds, nxt, np, gv, lane);
 
     // ---- S = Q K; tile t covers tokens 64t + 16(n/4) + 4 slot + n%4 ----
     float4v S[2];
     S[0] = S[1] = float4v{0.f, 0.f, 0.f, 0.f};
     // 2-bit codes of every channel (promoted channels have zero tables);
-    // block cb + 1's codes and table are read before block cb is computed
+    // block cb + 1's codes and table are read before block cb is computed.
+    // The tables the later passes need (value tables, 4-bit key tables, the
+    // promoted channels' query) are built in between, so their LDS latency
+    // overlaps the lookups.
     {
       const int row = M.kl + 32 * kq + qd;
       const int tab = M.klut + 8 * kq;
+      const uint16_t* vs = (const uint16_t*)(lds + M.vs);
+      const uint16_t* vz = (const uint16_t*)(lds + M.vz);
       uint32_t w0 = lds_u32(lds, row), w1 = lds_u32(lds, row + 16);
       uint2 t = *(const uint2*)(lds + tab);
 #pragma unroll
@@ -477,8 +490,34 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
         w0 = nw0;
         w1 = nw1;
         t = nt;
+        if (cb % 4 == 1 && cb / 4 < 4) {
+          // value table k = cb / 4 of this lane: token lane + 64 (k & 1), group k >> 1
+          // (groups beyond gv rebuild an existing table with identical contents)
+          const int k = cb / 4;
+          const int tt = lane + 64 * (k & 1), g = (k >> 1) % gv;
+          *(uint2*)(lds + M.vlut + kVlutStride * g + 8 * tt) = build_lut4<bf16>(vs[tt * gv + g], vz[tt * gv + g]);
+        }
+        if (cb == 18) build_lut16_tables<bf16, np>(M, lds, ks, kz, lane);
+        if (cb == 26) {
+          const uint16_t* q16 = (const uint16_t*)(lds + M.q16);
+          const uint8_t* pidx = lds + M.pidx;
+          uint16_t* qp = (uint16_t*)(lds + M.qp);
+#pragma unroll
+          for (int i = lane; i < GQ * np; i += 64) {
+            const int h = i / np, j = i % np;
+            qp[h * (kQpStride / 2) + j] = q16[h * kD + pidx[j]];
+          }
+        }
       }
     }
+    // value tables of groups 2.. (value groups narrower than 64 channels)
+    for (int i = 256 + lane; i < kPage * gv; i += 64) {
+      const int g = i >> 7, tt = i & 127;
+      const uint16_t* vs = (const uint16_t*)(lds + M.vs);
+      const uint16_t* vz = (const uint16_t*)(lds + M.vz);
+      *(uint2*)(lds + M.vlut + kVlutStride * g + 8 * tt) = build_lut4<bf16>(vs[tt * gv + g], vz[tt * gv + g]);
+    }
+    lds_sync();
     // promoted channels: 4-bit codes, slot j = 4pb + kq of the high codes
 #pragma unroll
     for (int pb = 0; pb < np / 4; ++pb) {
@@ -496,7 +535,10 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
                                                    0, 0);
     }
     lds_sync();
-    if (has_next) issue_keys(M, lds, nxt, np, lane);
+    if (has_next) {
+      issue_small(M, lds, nxt, np, gv, lane);
+      issue_keys(M, lds, nxt, np, lane);
+    }
 
     // ---- online softmax in base 2 ----
     {
@@ -606,7 +648,11 @@ int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, i
   const unsigned blocks = (unsigned)((workers + kWaves - 1) / kWaves);
   const size_t lds = fast_decode_lds_bytes(np, p.gv);
   const dim3 grid(blocks), block(256);
-#define DKV_FAST_LAUNCH(G, N) hipLaunchKernelGGL((decode_pages_fast<G, N>), grid, block, lds, stream, p)
+#define DKV_FAST_LAUNCH(G, N)                                                                  \
+  do {                                                                                         \
+    if (p.bf16) hipLaunchKernelGGL((decode_pages_fast<G, N, true>), grid, block, lds, stream, p);  \
+    else hipLaunchKernelGGL((decode_pages_fast<G, N, false>), grid, block, lds, stream, p);        \
+  } while (0)
 #define DKV_FAST_NP(G)                         \
   switch (np) {                                \
     case 16: DKV_FAST_LAUNCH(G, 16); break;    \
