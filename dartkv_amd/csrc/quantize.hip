@@ -544,18 +544,23 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_tiled(KeyParams k
 
 // Promoted-channel selection for many pages at once: one lane per
 // (batch * head, page) runs the exact top-k on the scores kKeyScores left in
-// the page's low-code region and writes the channel indices.
-__global__ void __launch_bounds__(kThreads) key_select_pages(KeyParams k, int row_bytes) {
+// the page's low-code region and writes the channel indices.  Each lane's
+// work array lives in its own slice of LDS (the selection is a chain of
+// dependent reads and writes, so LDS latency sets its speed).
+constexpr int kSelectLanes = 64;
+constexpr int kSelectMaxD = 128;
+
+__global__ void __launch_bounds__(kSelectLanes) key_select_pages(KeyParams k, int row_bytes) {
+  __shared__ SelItem work_all[kSelectLanes][kSelectMaxD];
   const dkv_key_pages_args& a = k.a;
-  const int64_t item = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t item = (int64_t)blockIdx.x * kSelectLanes + threadIdx.x;
   const int64_t bhs = a.B * a.H;
   if (item >= bhs * a.n_pages) return;
   const int64_t page = item / bhs, bh = item % bhs;
   const int D = (int)a.D, K = (int)a.promoted;
   const float* score = (const float*)(a.low + page * a.low_page_stride + bh * D * row_bytes);
-  SelItem work[kThreads];
   int32_t* idx_out = (int32_t*)((char*)a.idx + page * a.idx_page_stride) + bh * K;
-  select_topk(score, D, K, work, idx_out);
+  select_topk(score, D, K, work_all[threadIdx.x], idx_out);
 }
 
 __host__ inline size_t key_tiled_smem(int D, int T, int G, int K, int row_bytes) {
@@ -712,12 +717,12 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
     const dim3 grid((unsigned)(a.B * a.H), (unsigned)a.n_pages);
     hipStream_t s = (hipStream_t)stream;
     const bool select = a.key_mode == DKV_KEY_MIXED && Kp > 0 && Kp < a.D && a.selection != DKV_SELECT_GIVEN;
-    if (select && row_bytes >= 4) {
+    if (select && row_bytes >= 4 && a.D <= kSelectMaxD) {
       // scores -> one lane per page selects -> codes
       hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyScores);
       const int64_t items = a.B * a.H * a.n_pages;
-      hipLaunchKernelGGL(key_select_pages, dim3((unsigned)((items + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
-                         k, row_bytes);
+      hipLaunchKernelGGL(key_select_pages, dim3((unsigned)((items + kSelectLanes - 1) / kSelectLanes)),
+                         dim3(kSelectLanes), 0, s, k, row_bytes);
       hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyCodes);
     } else {
       hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyAll);
