@@ -201,6 +201,86 @@ def config2_latency_us(torch, dart, synthetic, stream) -> float:
     return e0.elapsed_time(e1) / 50 * 1e3
 
 
+QWEN3_8B = dict(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_attention_heads=32,
+                num_key_value_heads=8, head_dim=128, max_position_embeddings=40960, tie_word_embeddings=False)
+
+
+def decode_c4(torch, dart, batch: int = 16, prompt: int = 8192, steps: int = 128, layers: int = 36,
+              seed: int = 20260823) -> dict:
+    """C4: Qwen3-8B-shaped greedy decode through DartHFCache + the fused Qwen3 adapter.
+
+    Random-init bf16 weights (no checkpoint), ``batch`` x ``prompt`` random
+    token ids, one prefill, then ``steps`` greedy one-token steps; every
+    decode attention reads the packed pages (MFMA page kernel).  tok/s =
+    batch * steps / decode wall time.  ``hbm_bytes_per_step`` counts the
+    weights (all of them, LM head included) plus the average packed cache
+    bytes a step reads.
+    """
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+
+    from dartkv_amd.integrations import DartHFCache, attach_dart_fused_attention
+
+    cfg = Qwen3Config(num_hidden_layers=layers, layer_types=["full_attention"] * layers, **QWEN3_8B)
+    torch.manual_seed(seed)
+    t0 = time.perf_counter()
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device("cuda:0"):
+            model = Qwen3ForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    model = attach_dart_fused_attention(model).eval()
+    weight_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
+    ccfg = config_for("2b25")
+    ccfg["metadata_dtype"] = torch.float16
+    cache = DartHFCache(dart.DartKVCacheConfig(**ccfg))
+    ids = torch.randint(0, cfg.vocab_size, (batch, prompt), generator=torch.Generator().manual_seed(seed)).cuda()
+    torch.cuda.synchronize()
+    init_s = time.perf_counter() - t0
+    log(f"C4: model ready ({weight_bytes / 1e9:.2f} GB weights, {init_s:.1f} s); prefill {batch} x {prompt}")
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        out = model(ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+        nxt = out.logits[:, -1:].argmax(-1)
+        del out
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        kv_start = cache.storage_bytes
+        log(f"C4: prefill {prefill_s:.2f} s; packed cache {kv_start / 1e9:.2f} GB; {steps} decode steps")
+        tokens = [nxt]
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = model(nxt, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            nxt = out.logits[:, -1:].argmax(-1)
+            tokens.append(nxt)
+        torch.cuda.synchronize()
+        decode_s = time.perf_counter() - t0
+    kv_end = cache.storage_bytes
+    seq = cache.get_seq_length()
+    step_bytes = weight_bytes + (kv_start + kv_end) / 2
+    ms = decode_s / steps * 1e3
+    result = {
+        "workload": (f"C4 Qwen3-8B-shaped decode: {layers} layers, hidden 4096, 32/8 heads, head_dim 128, "
+                     f"vocab 151936, random bf16 weights; batch {batch}, {prompt} random prompt ids, {steps} greedy "
+                     "steps; cache 2-bit + 25 % key promotion, sink 32, page 128, kg 128, vg 64, fp16 metadata"),
+        "tok_s": round(batch * steps / decode_s, 2),
+        "ms_per_step": round(ms, 3),
+        "prefill_s": round(prefill_s, 3),
+        "seq_length_end": seq,
+        "weight_bytes": weight_bytes,
+        "kv_bytes_start": kv_start,
+        "kv_bytes_end": kv_end,
+        "hbm_bytes_per_step": int(step_bytes),
+        "step_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+        "roofline_tok_s": round(batch / (step_bytes / (HBM_PEAK_GBS * 1e9)), 1),
+        "compression_ratio": round(cache.compression_ratio, 3),
+    }
+    del model, cache, tokens, nxt, ids
+    torch.cuda.empty_cache()
+    return result
+
+
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -218,6 +298,10 @@ def main() -> int:
     p.add_argument("--no-c2", action="store_true", help="skip the config-2 latency and C3 prefill probes (clean profiles)")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="after timing, copy a MIB-MiB buffer 3 times (known bytes for PMC counter calibration)")
+    p.add_argument("--no-c4", action="store_true", help="skip the C4 Qwen3-8B-shaped decode leg")
+    p.add_argument("--c4-only", action="store_true", help="run only the C4 leg and print its JSON")
+    p.add_argument("--c4-steps", type=int, default=128)
+    p.add_argument("--c4-prompt", type=int, default=8192)
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the decode path shards by "
@@ -228,6 +312,10 @@ def main() -> int:
 
     import dartkv_amd as dart
     from dartkv_amd import synthetic
+
+    if args.c4_only:
+        print(json.dumps(decode_c4(torch, dart, prompt=args.c4_prompt, steps=args.c4_steps)), flush=True)
+        return 0
 
     cfg, caches, queries = build_caches(args, torch, dart, synthetic)
     nbytes = algorithmic_bytes(args.batch, args.kv_heads, args.q_heads, args.context, args.head_dim, cfg)
@@ -289,6 +377,16 @@ def main() -> int:
     if not args.no_c2:
         c2_us = config2_latency_us(torch, dart, synthetic, stream)
 
+    # C4: the Qwen3-8B-shaped end-to-end decode (tok/s), after the C5 caches are freed
+    c4 = None
+    if not args.no_c4:
+        del caches, queries, step
+        torch.cuda.empty_cache()
+        try:
+            c4 = decode_c4(torch, dart, prompt=args.c4_prompt, steps=args.c4_steps)
+        except (RuntimeError, ValueError, ImportError) as exc:
+            c4 = {"error": f"{type(exc).__name__}: {exc}"[:400]}
+
     result = {
         "metric": "packed-KV decode-attn GB/s (% HBM peak); decode tok/s, Qwen3-8B-shape",
         "value": round(gbs, 2),
@@ -314,6 +412,7 @@ def main() -> int:
         "decode_tok_s": round(tok_s, 2),
         "c2_latency_us": None if c2_us is None else round(c2_us, 2),
         "prefill_c3": prefill,
+        "c4_decode": c4,
         "wall_s_timed": round(wall, 3),
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",

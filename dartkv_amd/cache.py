@@ -210,8 +210,8 @@ class DartKVCache:
 
     def append(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         """Append a chunk without materializing the cache (reference cache.py:168-190)."""
-        self._validate_inputs(key_states, value_states)
         _lib.require_device(key_states, value_states)
+        self._validate_inputs(key_states, value_states)
         key_states = key_states.detach()
         value_states = value_states.detach()
         if key_states.stride(-1) != 1:

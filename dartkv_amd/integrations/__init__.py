@@ -1,0 +1,6 @@
+"""Integrations with external model libraries (reference src/dart/integrations/__init__.py)."""
+
+from .huggingface import DartCacheLayer, DartHFCache
+from .qwen3 import attach_dart_fused_attention, build_dart_qwen3_attention_class
+
+__all__ = ["DartCacheLayer", "DartHFCache", "attach_dart_fused_attention", "build_dart_qwen3_attention_class"]

@@ -1,0 +1,225 @@
+"""DartHFCache lifecycle and the Qwen3 fused-decode adapter.
+
+CPU tests cover the Transformers cache protocol and module replacement (no
+compute).  GPU tests follow the reference's own integration tests
+(reference tests/test_cache.py:265-305, tests/test_reproduction.py:355-389)
+and add a teacher-forced comparison: the adapted model (fused HIP decode over
+the packed pages) against the unmodified Transformers model whose cache hands
+it the dequantized contents of the same packed pages.  Both see the same
+cache state at every step, so their logits differ only by the attention
+arithmetic: max|a-b| / max|b| <= 1e-4 for fp32 models (fp32 cache, decode
+bar 1e-5) and <= 5e-2 for bf16 models (the Transformers side computes its
+scores and probabilities in bf16).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+transformers = pytest.importorskip("transformers")
+
+import dartkv_amd as dart  # noqa: E402
+from dartkv_amd.integrations import DartHFCache, attach_dart_fused_attention  # noqa: E402
+
+DEV = "cuda"
+
+
+def _tiny_qwen3_config(**over):
+    kw = dict(vocab_size=128, hidden_size=32, intermediate_size=64, num_hidden_layers=2, num_attention_heads=4,
+              num_key_value_heads=2, head_dim=8, max_position_embeddings=128,
+              layer_types=["full_attention", "full_attention"])
+    kw.update(over)
+    return transformers.Qwen3Config(**kw)
+
+
+def _kitty_config(meta=torch.float32):
+    """The Kitty-matching configuration of reference tests/test_reproduction.py:372-385."""
+    return dart.DartKVCacheConfig(key_bits=2, value_bits=2, key_group_size=8, value_group_size=8, sink_tokens=2,
+                                  page_size=8, local_tokens=1, value_local_tokens=8, hold_partial_pages=True,
+                                  promote_bits=4, promote_ratio=0.25, metadata_dtype=meta)
+
+
+# ---------------------------------------------------------------- CPU -----
+
+def test_cache_protocol_before_first_update():
+    cache = DartHFCache(dart.DartKVCacheConfig(page_size=8, key_group_size=8, value_group_size=8, sink_tokens=2))
+    assert isinstance(cache, transformers.Cache)
+    assert cache.get_seq_length() == 0 and cache.get_seq_length(None) == 0 and cache.get_seq_length(3) == 0
+    assert cache.get_mask_sizes(5, 0) == (5, 0)
+    assert cache.is_compileable is False
+    assert cache.is_sliding == []
+    assert cache.get_max_cache_shape() is None
+    assert cache.storage_bytes == 0 and cache.dense_bytes == 0 and cache.compression_ratio == 1.0
+    assert cache.page_table() is None and cache.page_runs() is None
+    assert cache.last_update_was_prefill(0) is False
+    with pytest.raises(RuntimeError, match="has not been initialized"):
+        cache.layer_for_attention(0)
+
+
+def test_cpu_update_raises_and_leaves_the_cache_untouched():
+    cache = DartHFCache(dart.DartKVCacheConfig(page_size=8, key_group_size=8, value_group_size=8, sink_tokens=2))
+    k = torch.randn(1, 2, 3, 8)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        cache.update(k, k.clone(), 0)
+    assert cache.get_seq_length() == 0 and cache._seen_tokens == 0
+    assert cache._layers == {}
+    assert cache.layers[0].cache.shape is None
+
+
+def test_attach_replaces_every_attention_and_keeps_weights():
+    torch.manual_seed(0)
+    model = transformers.Qwen3ForCausalLM(_tiny_qwen3_config())
+    before = {k: v.clone() for k, v in model.state_dict().items()}
+    attach_dart_fused_attention(model)
+    for i, layer in enumerate(model.model.layers):
+        assert type(layer.self_attn).__name__ == "DartQwen3Attention"
+        assert layer.self_attn.layer_idx == i
+    after = model.state_dict()
+    assert set(after) == set(before)
+    for k, v in before.items():
+        assert torch.equal(after[k], v), k
+    with pytest.raises(TypeError, match="Qwen3 causal-LM"):
+        attach_dart_fused_attention(torch.nn.Linear(2, 2))
+
+
+# ---------------------------------------------------------------- GPU -----
+
+@pytest.mark.gpu
+def test_reorder_rebuilds_pages_and_keeps_length():
+    """Reference tests/test_cache.py:265-279."""
+    torch.manual_seed(6)
+    config = dart.DartKVCacheConfig(page_size=2, key_group_size=2, value_group_size=4, sink_tokens=0,
+                                    metadata_dtype=torch.float32)
+    cache = DartHFCache(config)
+    keys = torch.randn(2, 1, 3, 8, device=DEV)
+    values = torch.randn_like(keys)
+    cache.update(keys, values, layer_idx=0)
+    old_table = cache.page_table()
+    restored_before, _ = cache.layer_for_attention(0).get()
+    cache.reorder_cache(torch.tensor([1, 1]))
+    assert cache.page_table() is not old_table
+    assert cache.get_seq_length() == 3
+    # both rows now hold row 1, re-packed from its dequantized contents
+    rows, _ = cache.layer_for_attention(0).get()
+    assert torch.equal(rows[0], rows[1])
+    next_keys = keys[1:2].expand(2, -1, -1, -1)
+    next_values = values[1:2].expand(2, -1, -1, -1)
+    restored, _ = cache.update(next_keys[:, :, :1, :], next_values[:, :, :1, :], layer_idx=0)
+    assert restored.shape == (2, 1, 4, 8)
+    assert restored_before.shape == (2, 1, 3, 8)
+
+
+@pytest.mark.gpu
+def test_post_quant_return_timing():
+    """Reference tests/test_cache.py:282-305: prefill returns the raw inputs, decode returns stored + new."""
+    torch.manual_seed(61)
+    config = dart.DartKVCacheConfig(page_size=4, local_tokens=4, sink_tokens=2, key_group_size=4, value_group_size=8,
+                                    promote_ratio=0.25, metadata_dtype=torch.float32)
+    cache = DartHFCache(config)
+    keys = torch.randn(1, 1, 11, 8, device=DEV)
+    values = torch.randn_like(keys)
+    prefill_keys, prefill_values = cache.update(keys, values, layer_idx=0)
+    assert torch.equal(prefill_keys, keys) and torch.equal(prefill_values, values)
+    assert cache.last_update_was_prefill(0)
+    stored_keys, stored_values = cache._layers[0].get()
+    assert not torch.equal(stored_keys, keys)
+    assert not torch.equal(stored_values, values)
+    next_keys = torch.randn(1, 1, 1, 8, device=DEV)
+    next_values = torch.randn_like(next_keys)
+    returned_keys, returned_values = cache.update(next_keys, next_values, layer_idx=0)
+    assert not cache.last_update_was_prefill(0)
+    assert torch.equal(returned_keys, torch.cat((stored_keys, next_keys), dim=-2))
+    assert torch.equal(returned_values, torch.cat((stored_values, next_values), dim=-2))
+    # the fused flag returns only the new tokens
+    k3 = torch.randn(1, 1, 1, 8, device=DEV)
+    only_k, only_v = cache.update(k3, k3.clone(), 0, {"dart_fused_attention": True})
+    assert torch.equal(only_k, k3) and only_k.data_ptr() != k3.data_ptr()
+    assert cache.get_seq_length() == 13 and cache._seen_tokens == 13
+    assert cache.storage_bytes == cache._layers[0].storage_bytes
+    assert cache.compression_ratio == cache.dense_bytes / cache.storage_bytes
+
+
+@pytest.mark.gpu
+def test_tiny_qwen3_generation_through_the_fused_decode():
+    """Reference tests/test_reproduction.py:355-389, on the ROCm device."""
+    torch.manual_seed(0)
+    model = attach_dart_fused_attention(transformers.Qwen3ForCausalLM(_tiny_qwen3_config()).to(DEV)).eval()
+    cache = DartHFCache(_kitty_config())
+    print("tiny qwen3 generate", flush=True)
+    with torch.inference_mode():
+        output = model.generate(input_ids=torch.randint(0, 128, (1, 13), device=DEV), max_new_tokens=20,
+                                do_sample=False, past_key_values=cache, disable_compile=True)
+    assert output.shape == (1, 33)
+    assert cache.get_seq_length() == 32
+
+
+class _DequantizedAfterAppend(DartHFCache):
+    """Hands the standard attention the dequantized cache including this step's token.
+
+    The prefill still returns the raw inputs (the same as ``DartHFCache``), so
+    both models build identical packed caches.
+    """
+
+    def update(self, key_states, value_states, layer_idx, cache_kwargs=None, *args, **kwargs):
+        prefill = layer_idx >= len(self.layers) or not self.layers[layer_idx].is_initialized
+        out = super().update(key_states, value_states, layer_idx, {"dart_fused_attention": True})
+        if prefill:
+            return out
+        return self.layers[layer_idx].cache.get()
+
+
+def _rel(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.float(), b.float()
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+def _teacher_forced(model_cfg, cache_cfg, dtype, batch, n, steps, tol, seed, min_fast=0):
+    torch.manual_seed(seed)
+    base = transformers.Qwen3ForCausalLM(model_cfg).to(device=DEV, dtype=dtype).eval()
+    with torch.no_grad():
+        for layer in base.model.layers:
+            layer.self_attn.k_norm.weight.mul_(2.0)     # sharper softmax than random init gives
+    fused = transformers.Qwen3ForCausalLM(model_cfg).to(device=DEV, dtype=dtype).eval()
+    fused.load_state_dict(base.state_dict())
+    attach_dart_fused_attention(fused)
+    ids = torch.randint(0, model_cfg.vocab_size, (batch, n + steps),
+                        generator=torch.Generator().manual_seed(seed)).to(DEV)
+    c_ref, c_fused = _DequantizedAfterAppend(cache_cfg), DartHFCache(cache_cfg)
+    with torch.inference_mode():
+        r = base(ids[:, :n], past_key_values=c_ref, use_cache=True).logits[:, -1]
+        f = fused(ids[:, :n], past_key_values=c_fused, use_cache=True).logits[:, -1]
+        worst = _rel(f, r)                             # prefill: the same dense path in both
+        for s in range(steps):
+            tok = ids[:, n + s:n + s + 1]
+            r = base(tok, past_key_values=c_ref, use_cache=True).logits[:, -1]
+            f = fused(tok, past_key_values=c_fused, use_cache=True).logits[:, -1]
+            assert not c_fused.last_update_was_prefill(0)
+            worst = max(worst, _rel(f, r))
+    for i in range(model_cfg.num_hidden_layers):
+        a, b = c_fused.layer_for_attention(i), c_ref.layer_for_attention(i)
+        assert a.get_seq_length() == b.get_seq_length() == n + steps
+        assert a.storage_bytes == b.storage_bytes
+        assert a.decode_plan(torch.device(DEV)).fast_count >= min_fast
+    print("teacher-forced worst logits rel err", worst, flush=True)
+    assert worst <= tol
+    return worst
+
+
+@pytest.mark.gpu
+def test_fused_decode_logits_match_the_dequantized_cache_fp32_kitty():
+    """General page kernel (head_dim 8, Kitty config, fp32 model and cache)."""
+    print("teacher-forced fp32 kitty", flush=True)
+    _teacher_forced(_tiny_qwen3_config(), _kitty_config(), torch.float32, 2, 19, steps=20, tol=1e-4, seed=5)
+
+
+@pytest.mark.gpu
+def test_fused_decode_logits_match_the_dequantized_cache_bf16_dart_pages():
+    """MFMA page kernel route: head_dim 128, page 128, 2-bit + 25 % promotion, sink 32, held tail, GQA 4."""
+    cfg = _tiny_qwen3_config(vocab_size=512, hidden_size=256, intermediate_size=512, num_attention_heads=8,
+                             num_key_value_heads=2, head_dim=128, max_position_embeddings=2048)
+    cache_cfg = dart.DartKVCacheConfig(bits=2, page_size=128, key_group_size=128, value_group_size=64,
+                                       promote_ratio=0.25, sink_tokens=32, hold_partial_pages=True,
+                                       metadata_dtype=torch.float16)
+    print("teacher-forced bf16 dart pages", flush=True)
+    _teacher_forced(cfg, cache_cfg, torch.bfloat16, 2, 32 + 128 * 3 + 100, steps=40, tol=5e-2, seed=9, min_fast=3)
