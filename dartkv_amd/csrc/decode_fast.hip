@@ -67,17 +67,16 @@ struct LdsMap {
 __host__ __device__ inline LdsMap lds_map(int np, int gv) {
   LdsMap m;
   int o = 0;
+  // Fields whose offsets depend only on NP come first, so they are
+  // compile-time constants in the kernel; the Gv-dependent ones follow.
   m.kl = o; o += 4096;                     // key low codes   [128 ch][32 B]
   m.vc = o; o += 4096;                     // value codes     [128 tok][32 B]
   m.kh = o; o += np * 32;                  // key high codes  [NP][32 B]
   m.ki = o; o += (np * 4 + 15) / 16 * 16;  // channel indices [NP] int32
   m.ks = o; o += 256;                      // key scale  [128] fp16
   m.kz = o; o += 256;                      // key zero   [128] fp16
-  m.vs = o; o += 256 * gv;                 // value scale [128 tok][Gv] fp16
-  m.vz = o; o += 256 * gv;                 // value zero  [128 tok][Gv] fp16
   m.klut = o; o += 1024;                   // 2-bit key tables [128 ch][LO, HI] (zero for promoted channels)
   m.klut16 = o; o += np * 32;              // 4-bit key tables [NP][LO 16 B, HI 16 B]
-  m.vlut = o; o += kVlutStride * gv;       // value tables [Gv][128 tok][LO, HI], padded rows
   m.pidx = o; o += 64;                     // promoted channels [NP] uint8 (a copy: ki is refilled early)
   m.q16 = o; o += 1024;                    // query [4][128 ch] fp16
   // A-operand sources; row strides put the rows one read touches in distinct
@@ -85,15 +84,34 @@ __host__ __device__ inline LdsMap lds_map(int np, int gv) {
   o = (o + 127) / 128 * 128;
   m.qp = o; o += 4 * kQpStride;            // query of the promoted channels [4][NP] fp16
   o = (o + 127) / 128 * 128;
-  m.pt = o; o += 4 * kPtStride;            // softmax weights [4][128 tok] fp16 (channel flags before)
+  m.pt = o; o += 4 * kPtStride;            // softmax weights [4][128 tok] fp16
   o = (o + 127) / 128 * 128 + 64;
   m.zero = o; o += 256;                    // zeros read by A-operand lanes without data
+  o = (o + 15) / 16 * 16;
+  m.vs = o; o += 256 * gv;                 // value scale [128 tok][Gv] fp16
+  m.vz = o; o += 256 * gv;                 // value zero  [128 tok][Gv] fp16
+  m.vlut = o; o += kVlutStride * gv;       // value tables [Gv][128 tok][LO, HI], padded rows
   m.bytes = (o + 15) / 16 * 16;
   return m;
 }
 
 __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
   return __builtin_amdgcn_perm(s0, s1, sel);
+}
+
+// Constants in registers the compiler cannot see through.  gfx9 VOP3
+// encodings take no literal and one scalar operand, so with two literal
+// constants (x & m) | c becomes v_and + v_or; with m in a scalar register and c
+// in a vector register it is one v_and_or_b32.  Made once per kernel.
+__device__ __forceinline__ uint32_t in_sgpr(uint32_t v) {
+  uint32_t r;
+  asm("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
+  return r;
+}
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t v) {
+  uint32_t r;
+  asm("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
+  return r;
 }
 
 // fp16 bit pattern of bf16(x) for an fp16 value x (round the 10-bit mantissa
@@ -135,12 +153,17 @@ __device__ __forceinline__ half4 lookup4(uint32_t e, uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(half4, make_uint2(perm(h4, l4, 0x05010400u), perm(h4, l4, 0x07030602u)));
 }
 
-// B operand from 4-bit codes: el = low 2 bits per byte (values 0..3), th =
-// high 2 bits in bits 0..1 of each byte (other bits ignored), L / H = low /
-// high bytes of table entries 0..15 (entry = low + 4 * high).
-__device__ __forceinline__ half4 lookup16(uint32_t el, uint32_t th, const uint4& L, const uint4& H) {
-  const uint32_t sel = el | ((th & 0x01010101u) << 2);              // entry within an 8-entry half
-  const uint32_t blend = ((th & 0x02020202u) << 1) | 0x03020100u;  // take the upper half's byte
+// B operand from 4-bit codes: el = low 2 bits per byte (values 0..3); wh =
+// the high-code dword, whose bits 8j + sh and 8j + sh + 1 are the high 2 bits
+// of byte j's entry; r2 = (sh - 2) & 31 and r1 = (sh - 1) & 31 rotate those
+// two bits to bit 2 of each byte.  L / H = low / high bytes of table entries
+// 0..15 (entry = low + 4 * high): the selector picks within an 8-entry half,
+// the blend takes the upper half's byte where the top bit is set.
+// m4 = 0x04040404 in a scalar register, ident = 0x03020100 in a vector register.
+__device__ __forceinline__ half4 lookup16(uint32_t el, uint32_t wh, uint32_t r2, uint32_t r1, const uint4& L,
+                                          const uint4& H, uint32_t m4, uint32_t ident) {
+  const uint32_t sel = (__builtin_amdgcn_alignbit(wh, wh, r2) & m4) | el;
+  const uint32_t blend = (__builtin_amdgcn_alignbit(wh, wh, r1) & m4) | ident;
   const uint32_t l4 = perm(perm(L.w, L.z, sel), perm(L.y, L.x, sel), blend);
   const uint32_t h4 = perm(perm(H.w, H.z, sel), perm(H.y, H.x, sel), blend);
   return __builtin_bit_cast(half4, make_uint2(perm(h4, l4, 0x05010400u), perm(h4, l4, 0x07030602u)));
@@ -200,11 +223,20 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 // Copy `bytes` (a multiple of 16) from global `src` to LDS `dst` with
 // global_load_lds_dwordx4: each instruction moves 64 x 16 bytes, lane l's
-// chunk landing at dst + 16 * l.  Completion is awaited with s_waitcnt vmcnt.
+// chunk landing at dst + 16 * l.  Completion is awaited with vm_wait(n),
+// which counts these instructions.  They are issued from inline assembly so
+// the compiler does not track them: its conservative aliasing of LDS DMA
+// against every later LDS store would otherwise insert vmcnt(0) before the
+// table writes of the next page and stall on the prefetch this overlaps.
+// (M0 holds the LDS destination; one wait state between writing M0 and the
+// load.)
+__device__ __forceinline__ void dma16(const uint8_t* src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory");
+}
 __device__ __forceinline__ void copy_to_lds(uint8_t* dst, const uint8_t* src, int bytes, int lane) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)dst);
   for (int off = 0; off < bytes; off += 1024) {
-    if (off + 16 * lane < bytes)
-      __builtin_amdgcn_global_load_lds((const void*)(src + off + 16 * lane), (lds_void*)(dst + off), 16, 0, 0);
+    if (off + 16 * lane < bytes) dma16(src + off + 16 * lane, base + off);
   }
 }
 
@@ -327,21 +359,28 @@ __device__ __forceinline__ void build_lut16_tables(const LdsMap& M, uint8_t* lds
 // heads-in-rows layout (rows 0..3 = query heads, K = 4 tokens per lane).
 // x[m]: 16 bits = codes of the lane's 8 channels for token row m (m = 0..3);
 // lo[m], hi[m]: byte-plane tables of token row m.  Rows m and m + 1 share one
-// v_perm: selector bit 2 picks the second row's table.
+// v_perm: selector bit 2 picks the second row's table.  m3 = 0x03030303 in a
+// scalar register, sel2 = 0x04000400 in a vector register.  All eight B
+// operands are formed before the MFMAs issue, so no MFMA waits on the VALU
+// result it reads.
 __device__ __forceinline__ void mma_lut_block(half4 a, const uint32_t x[4], const uint32_t lo[4], const uint32_t hi[4],
-                                              float4v acc[8]) {
+                                              float4v acc[8], uint32_t m3, uint32_t sel2) {
   const uint32_t y0 = perm(x[1], x[0], 0x05010400u);
   const uint32_t y1 = perm(x[3], x[2], 0x05010400u);
+  uint2 wk[4], wk4[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const uint32_t e0 = ((y0 >> (2 * k)) & 0x03030303u) | 0x04000400u;
-    const uint32_t e1 = ((y1 >> (2 * k)) & 0x03030303u) | 0x04000400u;
+    const uint32_t e0 = ((y0 >> (2 * k)) & m3) | sel2;
+    const uint32_t e1 = ((y1 >> (2 * k)) & m3) | sel2;
     const uint32_t lp0 = perm(lo[1], lo[0], e0), hp0 = perm(hi[1], hi[0], e0);
     const uint32_t lp1 = perm(lo[3], lo[2], e1), hp1 = perm(hi[3], hi[2], e1);
-    const uint2 wk = make_uint2(perm(hp0, lp0, 0x05010400u), perm(hp1, lp1, 0x05010400u));
-    const uint2 wk4 = make_uint2(perm(hp0, lp0, 0x07030602u), perm(hp1, lp1, 0x07030602u));
-    acc[k] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, __builtin_bit_cast(half4, wk), acc[k], 0, 0, 0);
-    acc[k + 4] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, __builtin_bit_cast(half4, wk4), acc[k + 4], 0, 0, 0);
+    wk[k] = make_uint2(perm(hp0, lp0, 0x05010400u), perm(hp1, lp1, 0x05010400u));
+    wk4[k] = make_uint2(perm(hp0, lp0, 0x07030602u), perm(hp1, lp1, 0x07030602u));
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    acc[k] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, __builtin_bit_cast(half4, wk[k]), acc[k], 0, 0, 0);
+    acc[k + 4] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, __builtin_bit_cast(half4, wk4[k]), acc[k + 4], 0, 0, 0);
   }
 }
 
@@ -428,6 +467,8 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     issue_values(M, lds, a0, lane);
   }
   const float c2 = p.scale * kLog2e;
+  const uint32_t m3 = in_sgpr(0x03030303u), m4 = in_sgpr(0x04040404u);
+  const uint32_t sel2 = in_vgpr(0x04000400u), ident = in_vgpr(0x03020100u);
 
 #pragma unroll 1
   for (int pg = page0; pg < page1; ++pg) {
@@ -438,25 +479,21 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     // value codes (this page, 4 loads); the values may still be in flight
     vm_wait(4);
 
-    // ---- promoted channels: flags and a byte-wide copy of the indices ----
-    uint8_t* flag = lds + M.pt;
+    // ---- 2-bit key tables of every channel, and a byte-wide copy of the
+    // promoted channels (the index region is refilled early) ----
     uint8_t* pidx = lds + M.pidx;
-    flag[lane] = 0;
-    flag[lane + 64] = 0;
-    lds_sync();
-    if (lane < np) {
-      const int c = ((const int32_t*)(lds + M.ki))[lane] & 127;
-      flag[c] = 1;
-      pidx[lane] = (uint8_t)c;
-    }
-    lds_sync();
-
-    // ---- 2-bit key tables (the 2-bit pass reads them) ----
     const uint16_t* ks = (const uint16_t*)(lds + M.ks);
     const uint16_t* kz = (const uint16_t*)(lds + M.kz);
+    int my_promoted = 0;
+    if (lane < np) {
+      my_promoted = ((const int32_t*)(lds + M.ki))[lane] & 127;
+      pidx[lane] = (uint8_t)my_promoted;
+    }
 #pragma unroll
-    for (int c = lane; c < kD; c += 64)
-      *(uint2*)(lds + M.klut + 8 * c) = flag[c] ? make_uint2(0u, 0u) : build_lut4<bf16>(ks[c], kz[c]);
+    for (int c = lane; c < kD; c += 64) *(uint2*)(lds + M.klut + 8 * c) = build_lut4<bf16>(ks[c], kz[c]);
+    lds_sync();
+    // promoted channels take the 4-bit pass: their 2-bit tables become zero
+    if (lane < np) *(uint2*)(lds + M.klut + 8 * my_promoted) = make_uint2(0u, 0u);
     lds_sync();
 
     // ---- S = Q K; tile t covers tokens 64t + 16(n/4) + 4 slot + n%4 ----
@@ -472,24 +509,23 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
       const int tab = M.klut + 8 * kq;
       const uint16_t* vs = (const uint16_t*)(lds + M.vs);
       const uint16_t* vz = (const uint16_t*)(lds + M.vz);
-      uint32_t w0 = lds_u32(lds, row), w1 = lds_u32(lds, row + 16);
-      uint2 t = *(const uint2*)(lds + tab);
+      constexpr int kAhead = 2;  // blocks whose codes and table are in flight
+      uint32_t w0[kD / 4], w1[kD / 4];
+      uint2 t[kD / 4];
+      auto load_cb = [&](int c) {
+        w0[c] = lds_u32(lds, row + 128 * c);
+        w1[c] = lds_u32(lds, row + 128 * c + 16);
+        t[c] = *(const uint2*)(lds + tab + 32 * c);
+      };
+#pragma unroll
+      for (int c = 0; c < kAhead; ++c) load_cb(c);
 #pragma unroll
       for (int cb = 0; cb < kD / 4; ++cb) {
-        uint32_t nw0 = 0, nw1 = 0;
-        uint2 nt = make_uint2(0u, 0u);
-        if (cb + 1 < kD / 4) {
-          nw0 = lds_u32(lds, row + 128 * (cb + 1));
-          nw1 = lds_u32(lds, row + 128 * (cb + 1) + 16);
-          nt = *(const uint2*)(lds + tab + 32 * (cb + 1));
-        }
-        S[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], lookup4((w0 >> sh) & 0x03030303u, t.x, t.y), S[0], 0, 0,
-                                                     0);
-        S[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], lookup4((w1 >> sh) & 0x03030303u, t.x, t.y), S[1], 0, 0,
-                                                     0);
-        w0 = nw0;
-        w1 = nw1;
-        t = nt;
+        if (cb + kAhead < kD / 4) load_cb(cb + kAhead);
+        S[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], lookup4((w0[cb] >> sh) & 0x03030303u, t[cb].x, t[cb].y),
+                                                     S[0], 0, 0, 0);
+        S[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], lookup4((w1[cb] >> sh) & 0x03030303u, t[cb].x, t[cb].y),
+                                                     S[1], 0, 0, 0);
         if (cb % 4 == 1 && cb / 4 < 4) {
           // value table k = cb / 4 of this lane: token lane + 64 (k & 1), group k >> 1
           // (groups beyond gv rebuild an existing table with identical contents)
@@ -518,21 +554,33 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
       *(uint2*)(lds + M.vlut + kVlutStride * g + 8 * tt) = build_lut4<bf16>(vs[tt * gv + g], vz[tt * gv + g]);
     }
     lds_sync();
-    // promoted channels: 4-bit codes, slot j = 4pb + kq of the high codes
+    // promoted channels: 4-bit codes, slot j = 4pb + kq of the high codes;
+    // block pb + 1's codes and tables are read before block pb is computed
+    {
+      const uint32_t r2 = (uint32_t)(sh - 2) & 31u, r1 = (uint32_t)(sh - 1) & 31u;
+      uint32_t wl0[np / 4], wl1[np / 4], wh0[np / 4], wh1[np / 4];
+      uint4 L[np / 4], H[np / 4];
+      auto load_pb = [&](int pb) {
+        const int j = 4 * pb + kq;
+        const int row = M.kl + 32 * pidx[j] + qd;
+        wl0[pb] = lds_u32(lds, row);
+        wl1[pb] = lds_u32(lds, row + 16);
+        const int hrow = M.kh + 32 * j + qd;
+        wh0[pb] = lds_u32(lds, hrow);
+        wh1[pb] = lds_u32(lds, hrow + 16);
+        L[pb] = *(const uint4*)(lds + M.klut16 + 32 * j);
+        H[pb] = *(const uint4*)(lds + M.klut16 + 32 * j + 16);
+      };
+      load_pb(0);
 #pragma unroll
-    for (int pb = 0; pb < np / 4; ++pb) {
-      const half4 a = load_a(lds, aq, 8 * pb);
-      const int j = 4 * pb + kq;
-      const int row = M.kl + 32 * pidx[j] + qd;
-      const uint32_t wl0 = lds_u32(lds, row), wl1 = lds_u32(lds, row + 16);
-      const int hrow = M.kh + 32 * j + qd;
-      const uint32_t wh0 = lds_u32(lds, hrow), wh1 = lds_u32(lds, hrow + 16);
-      const uint4 L = *(const uint4*)(lds + M.klut16 + 32 * j);
-      const uint4 H = *(const uint4*)(lds + M.klut16 + 32 * j + 16);
-      S[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, lookup16((wl0 >> sh) & 0x03030303u, wh0 >> sh, L, H), S[0], 0,
-                                                   0, 0);
-      S[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, lookup16((wl1 >> sh) & 0x03030303u, wh1 >> sh, L, H), S[1], 0,
-                                                   0, 0);
+      for (int pb = 0; pb < np / 4; ++pb) {
+        if (pb + 1 < np / 4) load_pb(pb + 1);
+        const half4 a = load_a(lds, aq, 8 * pb);
+        S[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+            a, lookup16((wl0[pb] >> sh) & 0x03030303u, wh0[pb], r2, r1, L[pb], H[pb], m4, ident), S[0], 0, 0, 0);
+        S[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+            a, lookup16((wl1[pb] >> sh) & 0x03030303u, wh1[pb], r2, r1, L[pb], H[pb], m4, ident), S[1], 0, 0, 0);
+      }
     }
     lds_sync();
     if (has_next) {
@@ -580,18 +628,26 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     vm_wait(has_next ? n_small_loads(np, gv) + n_key_loads(np) : 0);
 
     // ---- O += P V, heads in rows: block blk covers tokens 16 blk + kq + 4m ----
+    // (block blk + 1's weights, codes and tables are read before block blk is computed)
+    {
+      half4 a[kPage / 16];
+      uint32_t x[kPage / 16][4], lo[kPage / 16][4], hi[kPage / 16][4];
+      auto load_blk = [&](int blk) {
+        a[blk] = *(const half4*)(lds + apv + 32 * blk);
 #pragma unroll
-    for (int blk = 0; blk < kPage / 16; ++blk) {
-      const half4 a = *(const half4*)(lds + apv + 32 * blk);
-      uint32_t x[4], lo[4], hi[4];
+        for (int m = 0; m < 4; ++m) {
+          x[blk][m] = *(const uint16_t*)(lds + vcode + 512 * blk + 128 * m);
+          const uint2 t = *(const uint2*)(lds + vtab + 128 * blk + 32 * m);
+          lo[blk][m] = t.x;
+          hi[blk][m] = t.y;
+        }
+      };
+      load_blk(0);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        x[m] = *(const uint16_t*)(lds + vcode + 512 * blk + 128 * m);
-        const uint2 t = *(const uint2*)(lds + vtab + 128 * blk + 32 * m);
-        lo[m] = t.x;
-        hi[m] = t.y;
+      for (int blk = 0; blk < kPage / 16; ++blk) {
+        if (blk + 1 < kPage / 16) load_blk(blk + 1);
+        mma_lut_block(a[blk], x[blk], lo[blk], hi[blk], O, m3, sel2);
       }
-      mma_lut_block(a, x, lo, hi, O);
     }
     lds_sync();
     if (has_next) issue_values(M, lds, nxt, lane);
