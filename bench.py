@@ -206,19 +206,22 @@ QWEN3_8B = dict(vocab_size=151936, hidden_size=4096, intermediate_size=12288, nu
 
 
 def decode_c4(torch, dart, batch: int = 16, prompt: int = 8192, steps: int = 128, layers: int = 36,
-              seed: int = 20260823) -> dict:
+              seed: int = 20260823, graph: bool = True) -> dict:
     """C4: Qwen3-8B-shaped greedy decode through DartHFCache + the fused Qwen3 adapter.
 
     Random-init bf16 weights (no checkpoint), ``batch`` x ``prompt`` random
     token ids, one prefill, then ``steps`` greedy one-token steps; every
-    decode attention reads the packed pages (MFMA page kernel).  tok/s =
-    batch * steps / decode wall time.  ``hbm_bytes_per_step`` counts the
-    weights (all of them, LM head included) plus the average packed cache
-    bytes a step reads.
+    decode attention reads the packed pages (MFMA page kernel).  With
+    ``graph`` each step (model forward, argmax, position update) is captured
+    once in a HIP graph and replayed; a step that seals a page runs eagerly
+    and the graph is captured again after it.  tok/s = batch * steps / decode
+    wall time (captures and eager steps included).  ``hbm_bytes_per_step``
+    counts the weights (all of them, LM head included) plus the average
+    packed cache bytes a step reads.
     """
     from transformers import Qwen3Config, Qwen3ForCausalLM
 
-    from dartkv_amd.integrations import DartHFCache, attach_dart_fused_attention
+    from dartkv_amd.integrations import DartHFCache, GraphDecodeStep, attach_dart_fused_attention
 
     cfg = Qwen3Config(num_hidden_layers=layers, layer_types=["full_attention"] * layers, **QWEN3_8B)
     torch.manual_seed(seed)
@@ -242,18 +245,19 @@ def decode_c4(torch, dart, batch: int = 16, prompt: int = 8192, steps: int = 128
     with torch.inference_mode():
         t0 = time.perf_counter()
         out = model(ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
-        nxt = out.logits[:, -1:].argmax(-1)
+        next_ids = out.logits[:, -1:].argmax(-1)
         del out
+        position = torch.full((1, 1), prompt, dtype=torch.long, device="cuda:0")
         torch.cuda.synchronize()
         prefill_s = time.perf_counter() - t0
         kv_start = cache.storage_bytes
-        log(f"C4: prefill {prefill_s:.2f} s; packed cache {kv_start / 1e9:.2f} GB; {steps} decode steps")
-        tokens = [nxt]
+        log(f"C4: prefill {prefill_s:.2f} s; packed cache {kv_start / 1e9:.2f} GB; {steps} decode steps"
+            f"{' (HIP graph)' if graph else ''}")
+        runner = GraphDecodeStep(model, cache, next_ids, position, use_graph=graph)
+        tokens = []
         t0 = time.perf_counter()
         for _ in range(steps):
-            out = model(nxt, past_key_values=cache, use_cache=True, logits_to_keep=1)
-            nxt = out.logits[:, -1:].argmax(-1)
-            tokens.append(nxt)
+            tokens.append(runner.step().clone())
         torch.cuda.synchronize()
         decode_s = time.perf_counter() - t0
     kv_end = cache.storage_bytes
@@ -266,6 +270,9 @@ def decode_c4(torch, dart, batch: int = 16, prompt: int = 8192, steps: int = 128
                      "steps; cache 2-bit + 25 % key promotion, sink 32, page 128, kg 128, vg 64, fp16 metadata"),
         "tok_s": round(batch * steps / decode_s, 2),
         "ms_per_step": round(ms, 3),
+        "hip_graph": graph,
+        "graph_captures": runner.captures,
+        "eager_steps": runner.eager_steps,
         "prefill_s": round(prefill_s, 3),
         "seq_length_end": seq,
         "weight_bytes": weight_bytes,
@@ -276,7 +283,7 @@ def decode_c4(torch, dart, batch: int = 16, prompt: int = 8192, steps: int = 128
         "roofline_tok_s": round(batch / (step_bytes / (HBM_PEAK_GBS * 1e9)), 1),
         "compression_ratio": round(cache.compression_ratio, 3),
     }
-    del model, cache, tokens, nxt, ids
+    del model, cache, tokens, runner, ids
     torch.cuda.empty_cache()
     return result
 
@@ -302,6 +309,7 @@ def main() -> int:
     p.add_argument("--c4-only", action="store_true", help="run only the C4 leg and print its JSON")
     p.add_argument("--c4-steps", type=int, default=128)
     p.add_argument("--c4-prompt", type=int, default=8192)
+    p.add_argument("--c4-eager", action="store_true", help="C4 without HIP graph capture of the decode step")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the decode path shards by "
@@ -314,7 +322,8 @@ def main() -> int:
     from dartkv_amd import synthetic
 
     if args.c4_only:
-        print(json.dumps(decode_c4(torch, dart, prompt=args.c4_prompt, steps=args.c4_steps)), flush=True)
+        print(json.dumps(decode_c4(torch, dart, prompt=args.c4_prompt, steps=args.c4_steps, graph=not args.c4_eager)),
+              flush=True)
         return 0
 
     cfg, caches, queries = build_caches(args, torch, dart, synthetic)
@@ -383,7 +392,7 @@ def main() -> int:
         del caches, queries, step
         torch.cuda.empty_cache()
         try:
-            c4 = decode_c4(torch, dart, prompt=args.c4_prompt, steps=args.c4_steps)
+            c4 = decode_c4(torch, dart, prompt=args.c4_prompt, steps=args.c4_steps, graph=not args.c4_eager)
         except (RuntimeError, ValueError, ImportError) as exc:
             c4 = {"error": f"{type(exc).__name__}: {exc}"[:400]}
 

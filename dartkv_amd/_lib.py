@@ -26,7 +26,7 @@ KEY_DENSE, KEY_UNIFORM, KEY_MIXED = 0, 1, 2
 VALUE_DENSE, VALUE_UNIFORM = 0, 1
 SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
@@ -81,6 +81,7 @@ class DecodeArgs(ctypes.Structure):
         ("fast_value_group", ctypes.c_int64), ("fast_splits", ctypes.c_int64),
         ("rest_dense_tokens", ctypes.c_int64),
         ("fast_events", ctypes.c_void_p * 2),
+        ("tail_tokens_dev", ctypes.c_void_p),
     ]
 
 

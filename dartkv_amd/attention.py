@@ -50,6 +50,18 @@ def default_splits(batch: int, kv_heads: int, n_segments: int, target: int = 409
     return max(1, min(n_segments, -(-target // max(1, batch * kv_heads))))
 
 
+def page_kernel_splits(batch: int, kv_heads: int, pages: int) -> int:
+    """Split count of the MFMA page kernel.
+
+    One wave per split.  About 2,048 waves fill the device once (256 CUs x 8
+    resident waves); beyond that, up to 16 splits of at least 4 pages each
+    still help, since each split pays a fixed prologue.  Measured optimum at
+    C5 (512 (batch, kv head) pairs x 255 pages) and C4 (128 x 63): 16.
+    """
+    bh = max(1, batch * kv_heads)
+    return max(1, min(pages, max(-(-2048 // bh), min(16, -(-pages // 4)))))
+
+
 def _fast_enabled() -> bool:
     return os.environ.get("DKV_FORCE_GENERAL", "0") in ("", "0")
 
@@ -88,7 +100,7 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     if use_fast and rest and group <= 8 and plan.rest_dense >= 0 and (tail.tokens == 0 or _dense16_ok(tail)):
         dense_tokens = max(plan.rest_dense, tail.tokens)
     if fast_count:
-        fast_splits = n_splits or default_splits(batch, kv_heads, fast_count, target=8192)
+        fast_splits = n_splits or page_kernel_splits(batch, kv_heads, fast_count)
         fast_splits = max(1, min(fast_splits, fast_count))
         splits = rest * -(-dense_tokens // 32) if dense_tokens else (max(1, min(rest, 4)) if rest else 0)
     else:
@@ -125,6 +137,8 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
         a.fast_first, a.fast_count = plan.fast_first, fast_count
         a.fast_promoted, a.fast_value_group, a.fast_splits = plan.fast_promoted, plan.fast_value_group, fast_splits
     a.rest_dense_tokens = dense_tokens
+    if cache.device_tail is not None and plan.tail_is_pending:
+        a.tail_tokens_dev = cache.device_tail.data_ptr()
     if fast_events is not None:
         a.fast_events[0], a.fast_events[1] = fast_events[0].cuda_event, fast_events[1].cuda_event
     _lib.check(lib.dkv_decode_attention(a, _lib.stream_ptr(query.device)), "dkv_decode_attention")

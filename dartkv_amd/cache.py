@@ -171,6 +171,8 @@ class DartKVCache:
         self._tail_value: Optional[torch.Tensor] = None
         self._decode_plan_cache: Optional[_DecodePlan] = None
         self._random_channels: Optional[torch.Tensor] = None
+        # device copy of the held tail's length (replayable decode steps); None when off
+        self._tail_count_dev: Optional[torch.Tensor] = None
 
     # ---- reference properties ----
     @property
@@ -226,7 +228,11 @@ class DartKVCache:
             self._value_segments.append(value_states[..., :sink, :].clone())
             self._sealed_version += 1
         if sink < chunk:
-            self._append_remainder(key_states[..., sink:, :], value_states[..., sink:, :])
+            if not self._device_tail_append(key_states[..., sink:, :], value_states[..., sink:, :]):
+                if self._tail_count_dev is not None and torch.cuda.is_current_stream_capturing():
+                    raise RuntimeError("a captured append may only extend the held tail by one token")
+                self._append_remainder(key_states[..., sink:, :], value_states[..., sink:, :])
+                self._sync_device_tail()
         self._seen_tokens += chunk
         self._layout_version += 1
         self._invalidate_page_descriptors()
@@ -354,6 +360,7 @@ class DartKVCache:
         if self._pending_value is not None:
             self._pending_value = self._pending_value.to(device)
         self._tail_key = self._tail_value = None
+        self._tail_count_dev = None
         self._device = _descriptor_device(device, self._device)
         self._layout_version += 1
         self._sealed_version += 1
@@ -373,6 +380,7 @@ class DartKVCache:
         self._layout_version += 1
         self._sealed_version += 1
         self._decode_plan_cache = None
+        self._tail_count_dev = None
         self._invalidate_page_descriptors()
 
     def _invalidate_page_descriptors(self) -> None:
@@ -619,6 +627,83 @@ class DartKVCache:
         if n > self.config.page_size:
             self._value_segments.append(_slice_quantized_tensor(combined, self.config.page_size, n))
 
+    # ---- replayable decode steps ----
+    def enable_device_tail(self) -> None:
+        """Keep the held tail's length in device memory as well.
+
+        One-token appends that only extend the tail then write at the device
+        count and advance it on the device, and decode reads the count there,
+        so a decode step's launches can be captured in a graph and replayed.
+        The host-side state of a replayed append is advanced afterwards with
+        ``advance_device_tail``.  Appends that seal a page take the ordinary
+        path and resynchronize the device count.
+        """
+        if self.config.value_local_tokens:
+            raise ValueError("device-side tail counts need value_local_tokens == 0")
+        if not (self.config.hold_partial_pages or self.config.local_tokens):
+            raise ValueError("device-side tail counts need a held tail (hold_partial_pages or local_tokens)")
+        if self._shape is None:
+            raise RuntimeError("append the prompt before enabling device-side tail counts")
+        if self._tail_key is None:
+            B, H, D = self._shape
+            cap = self._tail_capacity()
+            self._tail_key = torch.empty(B, H, cap, D, dtype=self._dtype, device=self._device)
+            self._tail_value = torch.empty(B, H, cap, D, dtype=self._dtype, device=self._device)
+        if self._pending_key is not None and not self._pending_in_tail():
+            self._store_pending(self._pending_key, self._pending_value)
+            if not self._pending_in_tail():
+                raise RuntimeError("the held tail does not fit the tail buffer")
+        self._tail_count_dev = torch.zeros(1, dtype=torch.int64, device=self._device)
+        self._sync_device_tail()
+        self._sealed_version += 1
+
+    @property
+    def device_tail(self) -> Optional[torch.Tensor]:
+        """int64 [1] device tensor holding the held tail's length, or None."""
+        return self._tail_count_dev
+
+    def _pending_tokens(self) -> int:
+        return 0 if self._pending_key is None else self._pending_key.shape[-2]
+
+    def _sync_device_tail(self) -> None:
+        if self._tail_count_dev is not None:
+            if self._pending_key is not None and not self._pending_in_tail():
+                self._store_pending(self._pending_key, self._pending_value)
+            self._tail_count_dev.fill_(self._pending_tokens())
+
+    def next_append_seals(self, tokens: int = 1) -> bool:
+        """Whether appending ``tokens`` tokens now would seal a page (or overflow the tail buffer)."""
+        c = self.config
+        total = self._pending_tokens() + tokens
+        return (max(0, total - c.local_tokens) // c.page_size) > 0 or total > self._tail_capacity()
+
+    def _device_tail_append(self, key_states: torch.Tensor, value_states: torch.Tensor) -> bool:
+        if self._tail_count_dev is None or key_states.shape[-2] != 1 or self.next_append_seals(1):
+            return False
+        if self._pending_key is not None and not self._pending_in_tail():
+            return False
+        self._tail_key.index_copy_(2, self._tail_count_dev, key_states)
+        self._tail_value.index_copy_(2, self._tail_count_dev, value_states)
+        self._tail_count_dev.add_(1)
+        total = self._pending_tokens() + 1
+        self._pending_key = self._tail_key[..., :total, :]
+        self._pending_value = self._tail_value[..., :total, :]
+        return True
+
+    def advance_device_tail(self, tokens: int = 1) -> None:
+        """Host-side bookkeeping of ``tokens`` one-token appends replayed on the device."""
+        if self._tail_count_dev is None:
+            raise RuntimeError("device-side tail counts are not enabled")
+        for _ in range(tokens):
+            if self.next_append_seals(1):
+                raise RuntimeError("a replayed append cannot seal a page")
+            total = self._pending_tokens() + 1
+            self._pending_key = self._tail_key[..., :total, :]
+            self._pending_value = self._tail_value[..., :total, :]
+            self._seen_tokens += 1
+        self._layout_version += 1
+        self._invalidate_page_descriptors()
+
     # ---- decode plan ----
     def decode_plan(self, device: torch.device) -> _DecodePlan:
         """Device table of segment descriptors for the decode kernel.
@@ -630,8 +715,9 @@ class DartKVCache:
         if plan is not None and plan.version == self._sealed_version and plan.device == device:
             return plan
         pairs = self.iter_segments()
-        tail_is_pending = (self.config.value_local_tokens == 0 and self._pending_in_tail())
-        sealed = pairs[:-1] if tail_is_pending else pairs
+        tail_in_pairs = self.config.value_local_tokens == 0 and self._pending_in_tail()
+        sealed = pairs[:-1] if tail_in_pairs else pairs
+        tail_is_pending = tail_in_pairs or self._tail_count_dev is not None
         keepalive: list = []
         descs = (_lib.Segment * max(1, len(sealed)))()
         n_tokens = 0
@@ -874,11 +960,18 @@ def _rest_dense(cache: DartKVCache, descs, count: int, fast: Tuple[int, int, int
 
 
 def tail_segment(cache: DartKVCache):
-    """Descriptor of the held tail (pending tokens in the tail buffer)."""
+    """Descriptor of the held tail (pending tokens in the tail buffer).
+
+    With device-side tail counts the descriptor spans the whole tail buffer
+    (its capacity) and the kernels read the live count from the device.
+    """
     desc = _lib.Segment()
-    if cache._pending_key is None:
+    if cache._tail_count_dev is not None:
+        pk, pv = cache._tail_key, cache._tail_value
+    elif cache._pending_key is None:
         return desc
-    pk, pv = cache._pending_key, cache._pending_value
+    else:
+        pk, pv = cache._pending_key, cache._pending_value
     desc.tokens = pk.shape[-2]
     desc.key_kind = _lib.KEY_DENSE
     desc.value_kind = _lib.VALUE_DENSE

@@ -43,7 +43,14 @@ struct DecodeParams {
 // fast range, then the tail.
 __device__ __forceinline__ dkv_segment general_segment(const DecodeParams& p, int v) {
   const int rest = (int)p.a.n_segments - p.skip_count;
-  if (v >= rest) return p.a.tail;
+  if (v >= rest) {
+    dkv_segment t = p.a.tail;
+    if (p.a.tail_tokens_dev != nullptr) {
+      const int64_t n = *p.a.tail_tokens_dev;
+      t.tokens = (int32_t)(n < 0 ? 0 : (n < t.tokens ? n : t.tokens));
+    }
+    return t;
+  }
   return p.a.segments[v < p.skip_first ? v : v + p.skip_count];
 }
 

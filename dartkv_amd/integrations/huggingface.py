@@ -168,6 +168,31 @@ class DartHFCache(Cache):
     def get_max_length(self, layer_idx: Optional[int] = None) -> int:
         return -1
 
+    # ---- replayable decode steps ----
+    def enable_graph_decode(self) -> None:
+        """Keep every layer's held-tail length on the device (``DartKVCache.enable_device_tail``).
+
+        A one-token decode step through the fused adapter then launches the
+        same kernels with the same arguments every step, so it can be captured
+        in a HIP graph and replayed; call ``advance_graph_step`` once per
+        replay after the first one (capturing runs the host-side bookkeeping of
+        one step).  A step whose append would seal a page
+        (``graph_step_seals``) must run eagerly, and the graph be captured
+        again after it.
+        """
+        for layer in self.layers:
+            layer.cache.enable_device_tail()
+
+    def graph_step_seals(self) -> bool:
+        """Whether the next one-token step would seal a page in any layer."""
+        return any(layer.cache.next_append_seals(1) for layer in self.layers if layer.is_initialized)
+
+    def advance_graph_step(self, steps: int = 1) -> None:
+        """Host-side bookkeeping of ``steps`` replayed one-token decode steps."""
+        for layer in self.layers:
+            layer.cache.advance_device_tail(steps)
+        self._seen_tokens += steps
+
     # ---- descriptors ----
     def page_table(self, layer_idx: int = 0, *, device: torch.device | str | None = None, rebuild: bool = False):
         """Expose a layer's cached Dart page table to fused attention callers."""

@@ -47,7 +47,7 @@ extern "C" {
 /* Thread-local description of the last error on this thread. */
 const char* dkv_last_error(void);
 
-/* ABI version (3); bumps when a struct below changes. */
+/* ABI version (4); bumps when a struct below changes. */
 int dkv_abi_version(void);
 
 /*
@@ -192,6 +192,12 @@ typedef struct dkv_segment {
  * Timing: fast_events[0] / [1], when not NULL, are hipEvent_t handles recorded
  * on `stream` right before and right after the page kernel's launch.
  *
+ * Replayable launches: when tail_tokens_dev is not NULL, the kernels read the
+ * tail's token count from that device int64 when they run, clamped to
+ * [0, tail.tokens]; tail.tokens then gives the tail's capacity (and sizes the
+ * splits).  A caller that captures these launches in a graph and appends to
+ * the tail on the device between replays keeps the count there.
+ *
  * Replaces reference src/dart/fused_attention.py:654-771
  * (`fused_dart_attention`, one query token) and, for one query token,
  * src/dart/attention.py:32-87 (`streamed_dart_attention`).
@@ -214,6 +220,7 @@ typedef struct dkv_decode_args {
   int64_t fast_first, fast_count, fast_promoted, fast_value_group, fast_splits;
   int64_t rest_dense_tokens;
   void* fast_events[2];
+  const int64_t* tail_tokens_dev;
 } dkv_decode_args;
 
 int64_t dkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t n_splits);

@@ -223,3 +223,94 @@ def test_fused_decode_logits_match_the_dequantized_cache_bf16_dart_pages():
                                        metadata_dtype=torch.float16)
     print("teacher-forced bf16 dart pages", flush=True)
     _teacher_forced(cfg, cache_cfg, torch.bfloat16, 2, 32 + 128 * 3 + 100, steps=40, tol=5e-2, seed=9, min_fast=3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_device_tail_appends_and_decode_follow_the_oracle(dtype):
+    """One-token appends with the held tail's length on the device, through a page seal, against the oracle."""
+    from oracle import dart_oracle as O
+    from dartkv_amd import synthetic
+    cfg = dict(bits=2, page_size=128, key_group_size=128, value_group_size=64, promote_ratio=0.25, sink_tokens=32,
+               hold_partial_pages=True, metadata_dtype=torch.float16)
+    T0, steps = 32 + 128 + 120, 12
+    k, v, q = synthetic.outlier_kv(2, 4, T0 + steps, 128, query_heads=16, dtype=dtype, seed=31)
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    oc.append(k[:, :, :T0], v[:, :, :T0])
+    cache.append(k[:, :, :T0].to(DEV), v[:, :, :T0].to(DEV))
+    cache.enable_device_tail()
+    qd = q.to(DEV)
+    sealed_seen = False
+    for s in range(steps):
+        t = T0 + s
+        seals = cache.next_append_seals(1)
+        sealed_seen |= seals
+        oc.append(k[:, :, t:t + 1], v[:, :, t:t + 1])
+        cache.append(k[:, :, t:t + 1].to(DEV), v[:, :, t:t + 1].to(DEV))
+        assert int(cache.device_tail.item()) == cache._pending_tokens()
+        _, ref32 = O.streamed_attention(q, oc, return_fp32=True)
+        out32 = torch.empty(2, 16, 128, dtype=torch.float32, device=DEV)
+        dart.decode_attention(qd, cache, out_f32=out32)
+        torch.cuda.synchronize()
+        from tests.test_gpu_parity import rel_err, tolerance
+        err = rel_err(out32.unsqueeze(2), ref32)
+        print("step", s, "seal" if seals else "", "rel err", err, flush=True)
+        assert err <= tolerance(dtype), (s, err)
+    assert sealed_seen
+
+
+def _graph_model_and_cache_cfg():
+    cfg = _tiny_qwen3_config(vocab_size=512, hidden_size=256, intermediate_size=512, num_attention_heads=8,
+                             num_key_value_heads=2, head_dim=128, max_position_embeddings=2048)
+    cache_cfg = dart.DartKVCacheConfig(bits=2, page_size=128, key_group_size=128, value_group_size=64,
+                                       promote_ratio=0.25, sink_tokens=32, hold_partial_pages=True,
+                                       metadata_dtype=torch.float16)
+    return cfg, cache_cfg
+
+
+@pytest.mark.gpu
+def test_graph_replayed_decode_steps_match_eager_steps():
+    """Greedy steps captured in a HIP graph and replayed equal the same steps run eagerly, bit for bit,
+    across a page seal (eager step, then a new capture)."""
+    from dartkv_amd.integrations import GraphDecodeStep
+    cfg, cache_cfg = _graph_model_and_cache_cfg()
+    torch.manual_seed(17)
+    model = transformers.Qwen3ForCausalLM(cfg).to(device=DEV, dtype=torch.bfloat16).eval()
+    with torch.no_grad():
+        for layer in model.model.layers:
+            layer.self_attn.k_norm.weight.mul_(2.0)
+    attach_dart_fused_attention(model)
+    prompt = 32 + 128 * 2 + 120
+    ids = torch.randint(0, cfg.vocab_size, (2, prompt), generator=torch.Generator().manual_seed(5)).to(DEV)
+    runs = {}
+    for use_graph in (False, True):
+        cache = DartHFCache(cache_cfg)
+        with torch.inference_mode():
+            out = model(ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            nxt = out.logits[:, -1:].argmax(-1)
+            pos = torch.full((1, 1), prompt, dtype=torch.long, device=DEV)
+            runner = GraphDecodeStep(model, cache, nxt, pos, use_graph=use_graph)
+            if not use_graph:
+                cache.enable_graph_decode()  # same kernels and splits as the graph run
+            logits, toks = [], []
+            print("graph" if use_graph else "eager", "decode steps", flush=True)
+            for _ in range(16):
+                toks.append(runner.step().clone())
+                logits.append(runner.logits.clone())
+        torch.cuda.synchronize()
+        runs[use_graph] = (logits, toks, cache, runner)
+    le, te, ce, re_ = runs[False]
+    lg, tg, cg, rg = runs[True]
+    assert rg.captures == 2 and rg.eager_steps == 2 and rg.replays == 12, (rg.captures, rg.eager_steps, rg.replays)
+    for s in range(16):
+        assert torch.equal(te[s], tg[s]), s
+        assert torch.equal(le[s], lg[s]), s
+    assert cg.get_seq_length() == ce.get_seq_length() == prompt + 16
+    assert cg.storage_bytes == ce.storage_bytes
+    for i in range(cfg.num_hidden_layers):
+        a, b = cg.layer_for_attention(i), ce.layer_for_attention(i)
+        assert int(a.device_tail.item()) == a._pending_tokens() == b._pending_tokens()
+        ka, va = a.get()
+        kb, vb = b.get()
+        assert torch.equal(ka, kb) and torch.equal(va, vb)
