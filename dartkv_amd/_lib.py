@@ -26,7 +26,7 @@ KEY_DENSE, KEY_UNIFORM, KEY_MIXED = 0, 1, 2
 VALUE_DENSE, VALUE_UNIFORM = 0, 1
 SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
@@ -88,9 +88,20 @@ class DecodeArgs(ctypes.Structure):
 assert ctypes.sizeof(Segment) == 160
 
 
+class DecodePrepArgs(ctypes.Structure):
+    _fields_ = [
+        ("qkv", ctypes.c_void_p), ("qkv_sb", ctypes.c_int64),
+        ("q_weight", ctypes.c_void_p), ("k_weight", ctypes.c_void_p), ("eps", ctypes.c_double),
+        ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p), ("q_out", ctypes.c_void_p),
+        ("tail_key", ctypes.c_void_p), ("tail_value", ctypes.c_void_p), ("tail_pos", ctypes.c_void_p),
+        ("B", ctypes.c_int64), ("Hq", ctypes.c_int64), ("Hkv", ctypes.c_int64), ("D", ctypes.c_int64),
+        ("cap", ctypes.c_int64), ("dtype", ctypes.c_int64),
+    ]
+
+
 EXPORTED = (
     "dkv_last_error", "dkv_abi_version", "dkv_quantize_rows", "dkv_quantize_key_pages", "dkv_dequantize_rows",
-    "dkv_dequantize_mixed", "dkv_decode_workspace_bytes", "dkv_decode_attention",
+    "dkv_dequantize_mixed", "dkv_decode_workspace_bytes", "dkv_decode_attention", "dkv_decode_prep",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -120,8 +131,9 @@ def load() -> ctypes.CDLL:
         lib.dkv_decode_workspace_bytes.argtypes = [i64, i64, i64, i64]
         lib.dkv_decode_workspace_bytes.restype = i64
         lib.dkv_decode_attention.argtypes = [ctypes.POINTER(DecodeArgs), vp]
+        lib.dkv_decode_prep.argtypes = [ctypes.POINTER(DecodePrepArgs), vp]
         for name in ("dkv_quantize_rows", "dkv_quantize_key_pages", "dkv_dequantize_rows", "dkv_dequantize_mixed",
-                     "dkv_decode_attention"):
+                     "dkv_decode_attention", "dkv_decode_prep"):
             getattr(lib, name).restype = ctypes.c_int
         if lib.dkv_abi_version() != ABI_VERSION:
             raise RuntimeError("libdartkv_hip.so ABI version mismatch; rebuild it")

@@ -690,6 +690,26 @@ class DartKVCache:
         self._pending_value = self._tail_value[..., :total, :]
         return True
 
+    def prepared_append_ok(self) -> bool:
+        """Whether the next one-token append may be written into the tail by the decode-step
+        preparation kernel (``dkv_decode_prep``) and committed with ``commit_prepared_append``."""
+        return (self._tail_count_dev is not None and self._seen_tokens >= self.config.sink_tokens
+                and not self.next_append_seals(1)
+                and (self._pending_key is None or self._pending_in_tail()))
+
+    def commit_prepared_append(self) -> None:
+        """Account for one token per sequence written at the device tail count: advance the count
+        on the device and the host-side state."""
+        if not self.prepared_append_ok():
+            raise RuntimeError("no prepared one-token append is possible now")
+        self._tail_count_dev.add_(1)
+        total = self._pending_tokens() + 1
+        self._pending_key = self._tail_key[..., :total, :]
+        self._pending_value = self._tail_value[..., :total, :]
+        self._seen_tokens += 1
+        self._layout_version += 1
+        self._invalidate_page_descriptors()
+
     def advance_device_tail(self, tokens: int = 1) -> None:
         """Host-side bookkeeping of ``tokens`` one-token appends replayed on the device."""
         if self._tail_count_dev is None:

@@ -183,6 +183,20 @@ class DartHFCache(Cache):
         for layer in self.layers:
             layer.cache.enable_device_tail()
 
+    def prepared_append_ok(self, layer_idx: int) -> bool:
+        """Whether layer ``layer_idx`` can take its next token from the decode-step preparation kernel."""
+        return (layer_idx < len(self.layers) and self.layers[layer_idx].is_initialized
+                and self.layers[layer_idx].cache.prepared_append_ok())
+
+    def commit_prepared_append(self, layer_idx: int) -> None:
+        """The update bookkeeping (reference huggingface.py:46-68) of a token written by the
+        preparation kernel into layer ``layer_idx``'s tail."""
+        layer = self.layers[layer_idx]
+        layer.cache.commit_prepared_append()
+        layer.last_update_prefill = False
+        if layer_idx == 0:
+            self._seen_tokens += 1
+
     def graph_step_seals(self) -> bool:
         """Whether the next one-token step would seal a page in any layer."""
         return any(layer.cache.next_append_seals(1) for layer in self.layers if layer.is_initialized)

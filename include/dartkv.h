@@ -47,7 +47,7 @@ extern "C" {
 /* Thread-local description of the last error on this thread. */
 const char* dkv_last_error(void);
 
-/* ABI version (4); bumps when a struct below changes. */
+/* ABI version (5); bumps when a struct below changes. */
 int dkv_abi_version(void);
 
 /*
@@ -222,6 +222,39 @@ typedef struct dkv_decode_args {
   void* fast_events[2];
   const int64_t* tail_tokens_dev;
 } dkv_decode_args;
+
+/*
+ * Decode-step preparation for the Qwen3 adapter, one new token per sequence:
+ * qkv[b] holds the projected query heads, key heads and value heads of
+ * sequence b (Hq + 2 Hkv rows of D = 128 elements, row stride qkv_sb elements,
+ * cache dtype bf16 or fp16).  Query and key heads get RMSNorm (fp32 x *
+ * rsqrt(mean(x^2) + eps), rounded, times q_weight / k_weight[D], rounded) and
+ * the rotary embedding (x*cos + rotate_half(x)*sin, each product and the sum
+ * rounded; cos, sin [D] for this token's position).  Queries go to
+ * q_out[B][Hq][D]; keys and values to tail_key / tail_value[B][Hkv][cap][D] at
+ * token index *tail_pos (a device int64, read when the kernel runs; positions
+ * outside [0, cap) write nothing).  *tail_pos itself is not changed.
+ *
+ * Replaces, for one query token, the Transformers Qwen3 q_norm / k_norm and
+ * apply_rotary_pos_emb calls of reference src/dart/integrations/qwen3.py:48-53
+ * and the append of the new key/value in src/dart/integrations/huggingface.py:68.
+ */
+typedef struct dkv_decode_prep_args {
+  const void* qkv;
+  int64_t qkv_sb;
+  const void* q_weight;
+  const void* k_weight;
+  double eps;
+  const void* cos;
+  const void* sin;
+  void* q_out;
+  void* tail_key;
+  void* tail_value;
+  const int64_t* tail_pos;
+  int64_t B, Hq, Hkv, D, cap, dtype;
+} dkv_decode_prep_args;
+
+int dkv_decode_prep(const dkv_decode_prep_args* args, void* stream);
 
 int64_t dkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t n_splits);
 

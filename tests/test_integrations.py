@@ -314,3 +314,97 @@ def test_graph_replayed_decode_steps_match_eager_steps():
         ka, va = a.get()
         kb, vb = b.get()
         assert torch.equal(ka, kb) and torch.equal(va, vb)
+
+
+def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 numbers at |x| (for x != 0)."""
+    e = torch.floor(torch.log2(x.float().abs().clamp_min(2.0 ** -126)))
+    return torch.exp2(e - 7)
+
+
+@pytest.mark.gpu
+def test_decode_prep_matches_the_transformers_ops():
+    """dkv_decode_prep vs Qwen3RMSNorm + apply_rotary_pos_emb + the tail append (bf16).
+
+    The kernel's mean of squares sums in another order than torch's, so an
+    element may differ by one bf16 unit in the last place; values are copied
+    exactly; tail slots other than the device position are untouched."""
+    from transformers.models.qwen3 import modeling_qwen3 as m
+    from dartkv_amd import _lib
+    torch.manual_seed(3)
+    B, Hq, Hkv, D, cap, pos = 5, 8, 2, 128, 130, 77
+    dt = torch.bfloat16
+    cfg = _tiny_qwen3_config(hidden_size=256, num_attention_heads=Hq, num_key_value_heads=Hkv, head_dim=D)
+    qkv = (torch.randn(B, (Hq + 2 * Hkv) * D, device=DEV) * 3).to(dt)
+    qn, kn = m.Qwen3RMSNorm(D, eps=1e-6).to(DEV, dt), m.Qwen3RMSNorm(D, eps=1e-6).to(DEV, dt)
+    with torch.no_grad():
+        qn.weight.copy_(torch.rand(D) * 2)
+        kn.weight.copy_(torch.rand(D) * 2)
+    rot = m.Qwen3RotaryEmbedding(cfg).to(DEV)
+    cos, sin = rot(qkv.view(B, 1, -1), torch.full((1, 1), 1234, device=DEV))
+    q_ref = qn(qkv[:, :Hq * D].view(B, 1, Hq, D)).transpose(1, 2)
+    k_ref = kn(qkv[:, Hq * D:(Hq + Hkv) * D].view(B, 1, Hkv, D)).transpose(1, 2)
+    q_ref, k_ref = m.apply_rotary_pos_emb(q_ref, k_ref, cos, sin)
+    v_ref = qkv[:, (Hq + Hkv) * D:].view(B, Hkv, D)
+    tail_k = torch.full((B, Hkv, cap, D), 7.0, device=DEV, dtype=dt)
+    tail_v = torch.full_like(tail_k, 7.0)
+    pos_dev = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    q_out = torch.empty(B, Hq, 1, D, device=DEV, dtype=dt)
+    a = _lib.DecodePrepArgs()
+    a.qkv, a.qkv_sb = qkv.data_ptr(), qkv.stride(0)
+    a.q_weight, a.k_weight, a.eps = qn.weight.data_ptr(), kn.weight.data_ptr(), 1e-6
+    a.cos, a.sin, a.q_out = cos.data_ptr(), sin.data_ptr(), q_out.data_ptr()
+    a.tail_key, a.tail_value, a.tail_pos = tail_k.data_ptr(), tail_v.data_ptr(), pos_dev.data_ptr()
+    a.B, a.Hq, a.Hkv, a.D, a.cap, a.dtype = B, Hq, Hkv, D, cap, _lib.dtype_code(dt)
+    _lib.check(_lib.load().dkv_decode_prep(a, _lib.stream_ptr(torch.device(DEV))), "dkv_decode_prep")
+    torch.cuda.synchronize()
+    for got, ref in ((q_out, q_ref), (tail_k[:, :, pos:pos + 1], k_ref)):
+        d = (got.float() - ref.float()).abs()
+        assert bool((d <= _bf16_ulp(ref)).all()), float(d.max())
+        assert float((d == 0).float().mean()) >= 0.99
+    assert torch.equal(tail_v[:, :, pos], v_ref)
+    others = torch.ones(cap, dtype=torch.bool)
+    others[pos] = False
+    assert bool((tail_k[:, :, others] == 7.0).all()) and bool((tail_v[:, :, others] == 7.0).all())
+    assert int(pos_dev.item()) == pos
+    # a position outside the tail writes nothing
+    pos_dev.fill_(cap)
+    before = tail_k.clone()
+    _lib.check(_lib.load().dkv_decode_prep(a, _lib.stream_ptr(torch.device(DEV))), "dkv_decode_prep")
+    torch.cuda.synchronize()
+    assert torch.equal(tail_k, before)
+
+
+@pytest.mark.gpu
+def test_prepared_decode_path_matches_the_transformers_path():
+    """Teacher-forced logits of the adapter's prepared path (fused QKV GEMM + dkv_decode_prep, device tail)
+    against its Transformers-ops path on the same weights; bf16, tolerance as the other bf16 model tests."""
+    from dartkv_amd.integrations import GraphDecodeStep
+    cfg, cache_cfg = _graph_model_and_cache_cfg()
+    torch.manual_seed(23)
+    model = transformers.Qwen3ForCausalLM(cfg).to(device=DEV, dtype=torch.bfloat16).eval()
+    with torch.no_grad():
+        for layer in model.model.layers:
+            layer.self_attn.k_norm.weight.mul_(2.0)
+    attach_dart_fused_attention(model)
+    assert model.model.layers[0].self_attn._dart_qkv is not None
+    prompt, steps = 32 + 128 + 100, 40
+    ids = torch.randint(0, cfg.vocab_size, (2, prompt + steps), generator=torch.Generator().manual_seed(2)).to(DEV)
+    logits = {}
+    for prepared in (False, True):
+        cache = DartHFCache(cache_cfg)
+        out = []
+        with torch.inference_mode():
+            model(ids[:, :prompt], past_key_values=cache, use_cache=True)
+            if prepared:
+                cache.enable_graph_decode()
+            for s in range(steps):
+                assert cache.prepared_append_ok(0) == (prepared and not cache.graph_step_seals())
+                pos = torch.full((1, 1), prompt + s, dtype=torch.long, device=DEV)
+                o = model(ids[:, prompt + s:prompt + s + 1], position_ids=pos, past_key_values=cache, use_cache=True)
+                out.append(o.logits[:, -1].float())
+        logits[prepared] = (out, cache)
+    worst = max(_rel(a, b) for a, b in zip(logits[True][0], logits[False][0]))
+    print("prepared vs transformers path: worst logits rel err", worst, flush=True)
+    assert worst <= 5e-2
+    assert logits[True][1].get_seq_length() == logits[False][1].get_seq_length() == prompt + steps
