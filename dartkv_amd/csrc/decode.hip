@@ -279,6 +279,10 @@ constexpr int kDenseChunk = 32;
 constexpr int kDenseDim = 128;
 constexpr int kDenseMaxGroup = 8;
 
+// Every head slot of the dense kernel computes (the query of slots >= G is
+// zero), so the unrolled loops carry no per-head branches; only the record
+// writes are guarded.
+#define DKV_ALL_HEADS(h) _Pragma("unroll") for (int h = 0; h < MG; ++h)
 template <int MG>
 __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodeParams p, int chunks) {
   __shared__ float qsh[kDenseWaves][kDenseDim * MG];      // [c][MG]
@@ -303,27 +307,60 @@ __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodePara
                   seg.tokens <= chunks * kDenseChunk;
   const int t0 = chunk * kDenseChunk;
   const int nt = ok ? max(0, min(kDenseChunk, seg.tokens - t0)) : 0;
-  const uint16_t* kbase = (const uint16_t*)seg.key[0] + bh * seg.key_bh[0];
-  const uint16_t* vbase = (const uint16_t*)seg.value[0] + bh * seg.value_bh[0];
+  typedef __attribute__((address_space(1))) const uint16_t gu16;
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(1))) const u32x4 gu4;
+  typedef __attribute__((address_space(1))) const uint32_t gu32;
+  gu16* kbase = (gu16*)(seg.key[0] + 2 * (uint64_t)(bh * seg.key_bh[0]));
+  gu16* vbase = (gu16*)(seg.value[0] + 2 * (uint64_t)(bh * seg.value_bh[0]));
 
-  // ---- all loads first ----
-  float qv[kDenseDim * MG / 64];
-#pragma unroll
-  for (int r = 0; r < kDenseDim * MG / 64; ++r) {
-    const int i = lane + 64 * r, c = i / MG, h = i % MG;
-    qv[r] = h < G ? dev_load(a.query, (int64_t)b * a.q_sb + (int64_t)(kvh * G + h) * a.q_sh + c, (int)a.q_dtype)
-                  : 0.f;
-  }
+  // ---- all loads first: unconditional (rows past the chunk's tokens re-read
+  // the segment's last row and are zeroed), so every load is issued before the
+  // first wait ----
   const int kt = lane & (kDenseChunk - 1), khalf = lane >> 5;  // token, channel half of the Q K lane
   uint4 krow[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u)
-    krow[u] = kt < nt ? *((const uint4*)(kbase + (int64_t)(t0 + kt) * kDenseDim + 64 * khalf) + u)
-                      : make_uint4(0u, 0u, 0u, 0u);
   uint32_t vpair[kDenseChunk];
+  const int last = nt > 0 ? nt - 1 : 0;
+  if (nt > 0) {
+    const int krow_t = t0 + (kt < nt ? kt : last);
 #pragma unroll
-  for (int u = 0; u < kDenseChunk; ++u)
-    vpair[u] = u < nt ? *(const uint32_t*)(vbase + (int64_t)(t0 + u) * kDenseDim + 2 * lane) : 0u;
+    for (int u = 0; u < 8; ++u) {
+      const u32x4 w = *((gu4*)(kbase + (int64_t)krow_t * kDenseDim + 64 * khalf) + u);
+      krow[u] = make_uint4(w.x, w.y, w.z, w.w);
+    }
+#pragma unroll
+    for (int u = 0; u < kDenseChunk; ++u)
+      vpair[u] = *(gu32*)(vbase + (int64_t)(t0 + (u < nt ? u : last)) * kDenseDim + 2 * lane);
+  }
+  // the query after the K/V loads, so one wait covers them all
+  float qv[kDenseDim * MG / 64];
+  dev_load_n(a.query, (int)a.q_dtype, qv, [&](int r) -> int64_t {
+    const int i = lane + 64 * r, c = i / MG, h = i % MG;
+    return h < G ? (int64_t)b * a.q_sb + (int64_t)(kvh * G + h) * a.q_sh + c : -1;
+  });
+  if (nt > 0) {
+    // every load is issued before the first use
+    asm volatile("" ::"v"(krow[0].x), "v"(krow[1].x), "v"(krow[2].x), "v"(krow[3].x), "v"(krow[4].x),
+                 "v"(krow[5].x), "v"(krow[6].x), "v"(krow[7].x), "v"(vpair[0]), "v"(vpair[1]), "v"(vpair[2]),
+                 "v"(vpair[3]), "v"(vpair[4]), "v"(vpair[5]), "v"(vpair[6]), "v"(vpair[7]), "v"(vpair[8]),
+                 "v"(vpair[9]), "v"(vpair[10]), "v"(vpair[11]), "v"(vpair[12]), "v"(vpair[13]), "v"(vpair[14]),
+                 "v"(vpair[15]));
+    asm volatile("" ::"v"(vpair[16]), "v"(vpair[17]), "v"(vpair[18]), "v"(vpair[19]), "v"(vpair[20]),
+                 "v"(vpair[21]), "v"(vpair[22]), "v"(vpair[23]), "v"(vpair[24]), "v"(vpair[25]), "v"(vpair[26]),
+                 "v"(vpair[27]), "v"(vpair[28]), "v"(vpair[29]), "v"(vpair[30]), "v"(vpair[31]));
+    if (kt >= nt) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) krow[u] = make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < kDenseChunk; ++u)
+      if (u >= nt) vpair[u] = 0u;
+  } else {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) krow[u] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int u = 0; u < kDenseChunk; ++u) vpair[u] = 0u;
+  }
 #pragma unroll
   for (int r = 0; r < kDenseDim * MG / 64; ++r) qs[lane + 64 * r] = qv[r];
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -332,7 +369,7 @@ __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodePara
 
   // ---- logits ----
   float logit[MG];
-  DKV_FOR_HEAD(h) logit[h] = 0.f;
+  DKV_ALL_HEADS(h) logit[h] = 0.f;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const uint32_t ww[4] = {krow[u].x, krow[u].y, krow[u].z, krow[u].w};
@@ -341,12 +378,12 @@ __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodePara
       const uint16_t bits = (uint16_t)(ww[i / 2] >> (16 * (i % 2)));
       const float kv = bf ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
       const float* qc = qs + (64 * khalf + 8 * u + i) * MG;
-      DKV_FOR_HEAD(h) logit[h] = fmaf(qc[h], kv, logit[h]);
+      DKV_ALL_HEADS(h) logit[h] = fmaf(qc[h], kv, logit[h]);
     }
   }
   const float scale = (float)a.scale;
   float m[MG], l[MG];
-  DKV_FOR_HEAD(h) {
+  DKV_ALL_HEADS(h) {
     const float lg = kt < nt ? (logit[h] + __shfl_xor(logit[h], 32, 64)) * scale : -INFINITY;
     m[h] = wave_max(lg);
     const float w = kt < nt ? expf(lg - m[h]) : 0.f;
@@ -359,13 +396,13 @@ __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodePara
 
   // ---- weighted values: channels 2 lane, 2 lane + 1 ----
   float pv0[MG], pv1[MG];
-  DKV_FOR_HEAD(h) pv0[h] = pv1[h] = 0.f;
+  DKV_ALL_HEADS(h) pv0[h] = pv1[h] = 0.f;
 #pragma unroll
   for (int u = 0; u < kDenseChunk; ++u) {
     const float v0 = bf ? bf16_to_f32((uint16_t)vpair[u]) : (float)__builtin_bit_cast(_Float16, (uint16_t)vpair[u]);
     const float v1 = bf ? bf16_to_f32((uint16_t)(vpair[u] >> 16))
                         : (float)__builtin_bit_cast(_Float16, (uint16_t)(vpair[u] >> 16));
-    DKV_FOR_HEAD(h) {
+    DKV_ALL_HEADS(h) {
       const float w = ws[h * kDenseChunk + u];
       pv0[h] = fmaf(w, v0, pv0[h]);
       pv1[h] = fmaf(w, v1, pv1[h]);

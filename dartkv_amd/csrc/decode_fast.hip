@@ -439,12 +439,13 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
 
   {
     uint16_t* q16 = (uint16_t*)(lds + M.q16);
-    for (int i = lane; i < 4 * kD; i += 64) {
-      const int h = i / kD, c = i % kD;
-      const float qv =
-          h < GQ ? dev_load(p.query, (int64_t)b * p.q_sb + (int64_t)(kvh * GQ + h) * p.q_sh + c, p.q_dtype) : 0.f;
-      q16[i] = __builtin_bit_cast(uint16_t, (_Float16)qv);
-    }
+    float qv[4 * kD / 64];
+    dev_load_n(p.query, p.q_dtype, qv, [&](int r) -> int64_t {
+      const int i = lane + 64 * r, h = i / kD, c = i % kD;
+      return h < GQ ? (int64_t)b * p.q_sb + (int64_t)(kvh * GQ + h) * p.q_sh + c : -1;
+    });
+#pragma unroll
+    for (int r = 0; r < 4 * kD / 64; ++r) q16[lane + 64 * r] = __builtin_bit_cast(uint16_t, (_Float16)qv[r]);
     *(uint32_t*)(lds + M.zero + 4 * lane) = 0u;
   }
   lds_sync();

@@ -23,6 +23,34 @@ __device__ __forceinline__ float dev_load(const void* base, int64_t index, int d
   return ((const float*)base)[index];
 }
 
+// x[r] = element idx(r) of `base` (dtype dt) as fp32 for r < N, or 0 where
+// idx(r) < 0 (element 0 is read there, so base must hold at least one
+// element).  The dtype is tested once and every load is unconditional, so all
+// N loads are issued before the first wait (a per-element dtype switch or a
+// per-lane branch makes the compiler wait for each load in turn).
+template <int N, typename IndexFn>
+__device__ __forceinline__ void dev_load_n(const void* base, int dt, float (&x)[N], IndexFn idx) {
+  int64_t at[N];
+#pragma unroll
+  for (int r = 0; r < N; ++r) at[r] = idx(r);
+  if (dt == kBF16 || dt == kF16) {
+    uint16_t raw[N];
+#pragma unroll
+    for (int r = 0; r < N; ++r) raw[r] = ((const uint16_t*)base)[at[r] >= 0 ? at[r] : 0];
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+      const float v = dt == kBF16 ? bf16_to_f32(raw[r]) : (float)__builtin_bit_cast(_Float16, raw[r]);
+      x[r] = at[r] >= 0 ? v : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+      const float v = ((const float*)base)[at[r] >= 0 ? at[r] : 0];
+      x[r] = at[r] >= 0 ? v : 0.f;
+    }
+  }
+}
+
 __device__ __forceinline__ void dev_store(void* base, int64_t index, float v, int dt) {
   if (dt == kBF16) {
     ((uint16_t*)base)[index] = bf16_bits_rne(v);
