@@ -8,10 +8,11 @@ packed cache resident in HBM, each layer a separate cache.
 
 One step = one decode token for all 64 sequences through all 36 layers:
 36 calls of the decode attention (MFMA page kernel, dense sink/tail kernel,
-split merge).  ``value`` is the algorithmic bytes those calls must read and
-write (packed pages, dense sink and tail, query, output) per second of the
-whole step.  ``roofline`` is the page kernel alone: its pages' bytes over its
-mean duration, timed with HIP events recorded around its launch.
+split merge); ``--bits 4b`` runs the 4-bit uniform variant.  ``value`` is
+the algorithmic bytes those calls must read and write (packed pages, dense
+sink and tail, query, output) per second of the whole step.  ``roofline`` is
+the page kernel alone: its pages' bytes over its mean duration, timed with
+HIP events recorded around its launch.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3]
 
@@ -361,11 +362,14 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_begin.elapsed_time(t_end)
-    kernel_ms = [e0.elapsed_time(e1) for e0, e1 in events] if plan.fast_count else [float("nan")]
-    avg_kernel_ms = sum(kernel_ms) / len(kernel_ms)
+    avg_kernel_ms = None
+    if plan.fast_count:
+        kernel_ms = [e0.elapsed_time(e1) for e0, e1 in events]
+        avg_kernel_ms = sum(kernel_ms) / len(kernel_ms)
     ms_per_step = total_ms / args.steps
     gbs = nbytes * args.layers / (ms_per_step * 1e-3) / 1e9
-    achieved = fast_bytes / (avg_kernel_ms * 1e-3) / 1e9
+    achieved = fast_bytes / (avg_kernel_ms * 1e-3) / 1e9 if avg_kernel_ms else None
+    kernel = "decode_pages_fast" if plan.fast_promoted else "decode_pages_uniform"
     tok_s = args.batch / (ms_per_step * 1e-3)
 
     prefill = None
@@ -423,11 +427,11 @@ def main() -> int:
         "prefill_c3": prefill,
         "c4_decode": c4,
         "wall_s_timed": round(wall, 3),
-        "roofline": {
+        "roofline": None if achieved is None else {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic("decode_pages_fast", "c5") if args.bits == "2b25" else None,
-            "kernel": "decode_pages_fast (MFMA page kernel)",
+            "traffic": measured_traffic(kernel, "c5" if args.bits == "2b25" else f"c5_{args.bits}"),
+            "kernel": f"{kernel} (MFMA page kernel)",
             "algorithmic_bytes_per_launch": fast_bytes,
             "avg_kernel_us": round(avg_kernel_ms * 1e3, 2),
         },

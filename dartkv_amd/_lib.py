@@ -26,7 +26,7 @@ KEY_DENSE, KEY_UNIFORM, KEY_MIXED = 0, 1, 2
 VALUE_DENSE, VALUE_UNIFORM = 0, 1
 SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
@@ -82,6 +82,7 @@ class DecodeArgs(ctypes.Structure):
         ("rest_dense_tokens", ctypes.c_int64),
         ("fast_events", ctypes.c_void_p * 2),
         ("tail_tokens_dev", ctypes.c_void_p),
+        ("fast_key_bits", ctypes.c_int64), ("fast_value_bits", ctypes.c_int64),
     ]
 
 

@@ -100,8 +100,10 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     if use_fast and rest and group <= 8 and plan.rest_dense >= 0 and (tail.tokens == 0 or _dense16_ok(tail)):
         dense_tokens = max(plan.rest_dense, tail.tokens)
     if fast_count:
-        fast_splits = n_splits or page_kernel_splits(batch, kv_heads, fast_count)
-        fast_splits = max(1, min(fast_splits, fast_count))
+        # the uniform page kernel splits over half pages
+        units = fast_count if plan.fast_promoted else 2 * fast_count
+        fast_splits = n_splits or page_kernel_splits(batch, kv_heads, units)
+        fast_splits = max(1, min(fast_splits, units))
         splits = rest * -(-dense_tokens // 32) if dense_tokens else (max(1, min(rest, 4)) if rest else 0)
     else:
         fast_splits = 0
@@ -136,6 +138,7 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     if fast_count:
         a.fast_first, a.fast_count = plan.fast_first, fast_count
         a.fast_promoted, a.fast_value_group, a.fast_splits = plan.fast_promoted, plan.fast_value_group, fast_splits
+        a.fast_key_bits, a.fast_value_bits = plan.fast_key_bits, plan.fast_value_bits
     a.rest_dense_tokens = dense_tokens
     if cache.device_tail is not None and plan.tail_is_pending:
         a.tail_tokens_dev = cache.device_tail.data_ptr()

@@ -17,7 +17,7 @@ import sys
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libdartkv_hip.so")
-SOURCES = ["capi.hip", "quantize.hip", "decode.hip", "decode_fast.hip", "prep.hip"]
+SOURCES = ["capi.hip", "quantize.hip", "decode.hip", "decode_fast.hip", "decode_uniform.hip", "prep.hip"]
 ARCH = os.environ.get("DKV_OFFLOAD_ARCH", "gfx950")
 
 

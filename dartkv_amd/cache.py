@@ -123,15 +123,15 @@ class DartKVCacheConfig:
 class _DecodePlan:
     """Device table of sealed segment descriptors plus the tensors it points into.
 
-    ``fast_first``/``fast_count`` mark the run of table entries the MFMA page
-    kernel may take (full 128-token Dart pages in its layout); ``fast_promoted``
-    and ``fast_value_group`` are that run's promoted-channel count and value
-    group size.  ``rest_dense`` is the most tokens of any sealed entry outside
+    ``fast_first``/``fast_count`` mark the run of table entries a page kernel
+    may take (full 128-token pages in its layout); ``fast_promoted`` (0 for
+    uniform pages), ``fast_value_group``, ``fast_key_bits`` and
+    ``fast_value_bits`` describe that run.  ``rest_dense`` is the most tokens of any sealed entry outside
     that run when the dense decode kernel can read all of them, else -1.
     """
 
     def __init__(self, version: int, device: torch.device, table: Optional[torch.Tensor], count: int,
-                 keepalive: list, tail_is_pending: bool, n_tokens: int, fast: Tuple[int, int, int, int],
+                 keepalive: list, tail_is_pending: bool, n_tokens: int, fast: Tuple[int, int, int, int, int, int],
                  rest_dense: int = -1) -> None:
         self.version = version
         self.device = device
@@ -140,7 +140,8 @@ class _DecodePlan:
         self.keepalive = keepalive
         self.tail_is_pending = tail_is_pending
         self.n_tokens = n_tokens
-        self.fast_first, self.fast_count, self.fast_promoted, self.fast_value_group = fast
+        (self.fast_first, self.fast_count, self.fast_promoted, self.fast_value_group, self.fast_key_bits,
+         self.fast_value_bits) = fast
         self.rest_dense = rest_dense
 
 
@@ -919,26 +920,46 @@ def _dense_block(t: torch.Tensor, keepalive: list) -> Tuple[int, int]:
     return c.data_ptr(), T * D
 
 
-def _fast_run(cache: DartKVCache, descs, count: int) -> Tuple[int, int, int, int]:
-    """Longest run of descriptors the MFMA page kernel handles: (first, count, promoted, value group)."""
+def _fast_run(cache: DartKVCache, descs, count: int) -> Tuple[int, int, int, int, int, int]:
+    """Longest run of descriptors a page kernel handles:
+    (first, count, promoted, value group, key bits, value bits).
+
+    Dart pages (promoted > 0: 2-bit keys with 4-bit promoted channels, 2-bit
+    values) go to the lookup-table page kernel; uniform pages (promoted 0:
+    2/4/8-bit keys along the tokens in one group per page, 2/4/8-bit values)
+    to the arithmetic one.  Both need full 128-token pages, head_dim 128, fp16
+    metadata, value groups that are multiples of 16 dividing 128, and every
+    block 16-byte aligned per (batch, head)."""
+    none = (0, 0, 0, 0, 0, 0)
     if cache.shape is None or cache.dtype not in (torch.bfloat16, torch.float16):
-        return (0, 0, 0, 0)
+        return none
     c = cache.config
     if (cache.shape[-1] != 128 or c.page_size != 128 or c.metadata_dtype != torch.float16
-            or c.promote_ratio <= 0.0 or c.resolved_key_group_size != 128 or c.resolved_value_bits != 2):
-        return (0, 0, 0, 0)
+            or c.resolved_key_group_size != 128):
+        return none
     vg = c.resolved_value_group_size
-    K = promoted_count(128, c.promote_ratio)
-    if vg % 16 or 128 % vg or K % 16 or K > 64:
-        return (0, 0, 0, 0)
+    if vg % 16 or 128 % vg:
+        return none
+    if c.promote_ratio > 0.0:
+        K = promoted_count(128, c.promote_ratio)
+        kbits, vbits = 2, c.resolved_value_bits
+        if K % 16 or K > 64 or vbits != 2:
+            return none
+        key_blocks = ((0, 1), (1, 1), (2, 4), (3, 2), (4, 2))  # (descriptor slot, element bytes)
+    else:
+        K = 0
+        kbits, vbits = c.resolved_key_bits, c.resolved_value_bits
+        key_blocks = ((0, 1), (3, 2), (4, 2))
+    key_kind = _lib.KEY_MIXED if K else _lib.KEY_UNIFORM
 
     def ok(d) -> bool:
-        if not (d.tokens == 128 and d.key_kind == _lib.KEY_MIXED and d.value_kind == _lib.VALUE_UNIFORM
-                and d.promoted == K and d.key_group == 128 and d.value_bits == 2 and d.value_group == vg):
+        if not (d.tokens == 128 and d.key_kind == key_kind and d.value_kind == _lib.VALUE_UNIFORM
+                and d.key_group == 128 and d.value_bits == vbits and d.value_group == vg):
             return False
-        sizes = (1, 1, 4, 2, 2)
-        for i in range(5):
-            if d.key[i] % 16 or (d.key_bh[i] * sizes[i]) % 16:
+        if (d.promoted != K) if K else (d.key_bits != kbits):
+            return False
+        for i, size in key_blocks:
+            if d.key[i] % 16 or (d.key_bh[i] * size) % 16:
                 return False
         for i, size in enumerate((1, 2, 2)):
             if d.value[i] % 16 or (d.value_bh[i] * size) % 16:
@@ -957,7 +978,9 @@ def _fast_run(cache: DartKVCache, descs, count: int) -> Tuple[int, int, int, int
         if j - i > best[1]:
             best = (i, j - i)
         i = j
-    return (best[0], best[1], K, vg)
+    if best[1] == 0:
+        return none
+    return (best[0], best[1], K, vg, kbits, vbits)
 
 
 def _dense16_ok(d) -> bool:
@@ -966,7 +989,7 @@ def _dense16_ok(d) -> bool:
             and d.value[0] % 16 == 0 and (d.key_bh[0] * 2) % 16 == 0 and (d.value_bh[0] * 2) % 16 == 0)
 
 
-def _rest_dense(cache: DartKVCache, descs, count: int, fast: Tuple[int, int, int, int]) -> int:
+def _rest_dense(cache: DartKVCache, descs, count: int, fast: Tuple[int, ...]) -> int:
     """Most tokens of any sealed entry outside the fast run when all of them are
     dense 16-bit with aligned rows and head_dim is 128 (0 if there are none);
     -1 when the dense decode kernel cannot take them."""

@@ -497,13 +497,26 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
     DKV_CHECK(a.cache_dtype == dkv::kBF16 || a.cache_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED,
               "fast page path needs a bf16 or fp16 cache");
     DKV_CHECK(a.meta_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED, "fast page path needs fp16 metadata");
-    DKV_CHECK(a.fast_promoted % 16 == 0 && a.fast_promoted >= 16 && a.fast_promoted <= 64, DKV_ERR_UNSUPPORTED,
-              "fast page path needs 16, 32, 48 or 64 promoted channels");
     DKV_CHECK(a.fast_value_group % 16 == 0 && a.fast_value_group > 0 && 128 % a.fast_value_group == 0,
               DKV_ERR_UNSUPPORTED, "fast page path needs a value group that is a multiple of 16 dividing 128");
-    DKV_CHECK(a.fast_splits >= 1 && a.fast_splits <= fast_count, DKV_ERR_INVALID, "fast_splits out of range");
-    DKV_CHECK(dkv::fast_decode_max_loads((int)a.fast_promoted, (int)(128 / a.fast_value_group)) < 16,
-              DKV_ERR_UNSUPPORTED, "fast page path: value group too small");
+    if (a.fast_promoted > 0) {
+      DKV_CHECK(a.fast_promoted % 16 == 0 && a.fast_promoted >= 16 && a.fast_promoted <= 64, DKV_ERR_UNSUPPORTED,
+                "fast page path needs 16, 32, 48 or 64 promoted channels");
+      DKV_CHECK(a.fast_key_bits == 0 || a.fast_key_bits == 2, DKV_ERR_UNSUPPORTED,
+                "fast page path: Dart pages have 2-bit base key codes");
+      DKV_CHECK(a.fast_value_bits == 0 || a.fast_value_bits == 2, DKV_ERR_UNSUPPORTED,
+                "fast page path: Dart pages need 2-bit values");
+      DKV_CHECK(a.fast_splits >= 1 && a.fast_splits <= fast_count, DKV_ERR_INVALID, "fast_splits out of range");
+      DKV_CHECK(dkv::fast_decode_max_loads((int)a.fast_promoted, (int)(128 / a.fast_value_group)) < 16,
+                DKV_ERR_UNSUPPORTED, "fast page path: value group too small");
+    } else {
+      DKV_CHECK((a.fast_key_bits == 2 || a.fast_key_bits == 4 || a.fast_key_bits == 8) &&
+                    (a.fast_value_bits == 2 || a.fast_value_bits == 4 || a.fast_value_bits == 8),
+                DKV_ERR_UNSUPPORTED, "fast uniform pages need 2, 4 or 8-bit keys and values");
+      DKV_CHECK(a.fast_splits >= 1 && a.fast_splits <= 2 * fast_count, DKV_ERR_INVALID, "fast_splits out of range");
+      DKV_CHECK(dkv::uniform_decode_max_loads((int)a.fast_key_bits, (int)a.fast_value_bits) < 16,
+                DKV_ERR_UNSUPPORTED, "fast uniform pages: too many loads in flight");
+    }
   }
   const int64_t rest = a.n_segments - (fast_count > 0 ? fast_count : 0) + (a.tail.tokens > 0 ? 1 : 0);
   const int64_t general_splits = rest > 0 ? a.n_splits : 0;
@@ -517,8 +530,12 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
   if (fast_count > 0) {
     int rc = record_event(a.fast_events[0], s);
     if (rc) return rc;
-    rc = dkv::launch_fast_decode(a, (int)a.fast_first, (int)fast_count, (int)a.fast_promoted,
-                                 (int)a.fast_value_group, (int)fast_splits, (int)stride, s);
+    rc = a.fast_promoted > 0
+             ? dkv::launch_fast_decode(a, (int)a.fast_first, (int)fast_count, (int)a.fast_promoted,
+                                       (int)a.fast_value_group, (int)fast_splits, (int)stride, s)
+             : dkv::launch_uniform_decode(a, (int)a.fast_first, (int)fast_count, (int)a.fast_key_bits,
+                                          (int)a.fast_value_bits, (int)a.fast_value_group, (int)fast_splits,
+                                          (int)stride, s);
     if (rc) return rc;
     rc = record_event(a.fast_events[1], s);
     if (rc) return rc;

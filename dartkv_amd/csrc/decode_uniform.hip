@@ -1,0 +1,375 @@
+// Single-token decode over full uniform pages (gfx950, wave64).
+//
+// Scope: head_dim 128, 128-token pages, keys quantized uniformly with KB bits
+// along the tokens (one key group per page), values with VB bits along the
+// channels in groups of vg (16 | vg, vg | 128), KB, VB in {2, 4, 8}, fp16
+// metadata, bf16 or fp16 cache, up to 4 query heads per KV head.
+//
+// Each wave owns a split: a contiguous range of half pages (64 tokens; half
+// page q is half q & 1 of page q >> 1) of one (batch, kv head).  Per half page
+// it stages the half's key codes (every channel), value rows and scales in its
+// LDS, then
+//   * S = Q K with v_mfma_f32_16x16x16f16 in the slot layout (rows = 4 slots x
+//     4 query heads; a lane's four B values are four tokens of one channel,
+//     A carries the query at the lane's slot); one tile covers the 64 tokens;
+//   * an online softmax in base 2 (running max moves only beyond 8);
+//   * O += P V in the same slot layout (a lane's four B values are four
+//     channels of one token; A carries the weight at the lane's slot), two
+//     tiles of 64 channels.
+// Codes are dequantized arithmetically, exactly as the reference rounds:
+// byte permutes place each code under the fp16 exponent of 1024 (0x64xx =
+// 1024 + code), subtracting 1024 gives the code exactly in fp16, then
+// fp16(code * scale), fp16(+ zero) and, for bf16 caches, bf16 precision.  No
+// tables: a uniform page's value set per scale is the whole code range.
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "dkv_capi_util.h"
+#include "dkv_decode.h"
+#include "dkv_device.h"
+#include "dkv_page_common.h"
+
+using namespace dkv;
+
+namespace {
+
+constexpr int kHalfTok = 64;   // tokens per half page
+constexpr int kPtRow = 160;    // bytes between softmax-weight rows ([4][64] fp16, 8 banks apart)
+
+struct UMap {
+  int kc, vc, ks, kz, vs, vz, q16, pt, zero, bytes;
+};
+
+__host__ __device__ inline UMap umap(int kb, int vb, int gv) {
+  UMap m;
+  int o = 0;
+  m.kc = o; o += kD * 8 * kb;          // key codes of the half  [128 ch][8 KB bytes]
+  m.vc = o; o += kHalfTok * 16 * vb;   // value codes of the half [64 tok][16 VB bytes]
+  m.ks = o; o += 256;                  // key scale [128] fp16
+  m.kz = o; o += 256;                  // key zero  [128] fp16
+  m.vs = o; o += 128 * gv;             // value scale of the half [64 tok][Gv] fp16
+  m.vz = o; o += 128 * gv;             // value zero  of the half [64 tok][Gv] fp16
+  m.q16 = o; o += 1024;                // query [4][128 ch] fp16 (split start only)
+  o = (o + 127) / 128 * 128;
+  m.pt = o; o += 4 * kPtRow;           // softmax weights [4][64 tok] fp16
+  o = (o + 127) / 128 * 128 + 64;
+  m.zero = o; o += 256;                // zeros read by A-operand lanes without data
+  m.bytes = (o + 15) / 16 * 16;
+  return m;
+}
+
+// Staging: scales and key codes of a half page (issued after its Q K), then
+// value codes and value scales (issued after its P V).
+__host__ __device__ inline int n_key_loads_u(int kb) { return kb + 2; }
+__host__ __device__ inline int n_value_loads_u(int vb) { return vb + 2; }
+
+__device__ __forceinline__ void issue_keys_u(const UMap& M, uint8_t* lds, const PageAddr& a, int kb, int h,
+                                             int lane) {
+  copy_to_lds(lds + M.ks, (const uint8_t*)a.ks, 256, lane);
+  copy_to_lds(lds + M.kz, (const uint8_t*)a.kz, 256, lane);
+  // 16-byte chunk i of the half's codes: row i / cpr, column i % cpr
+  const int cpr = kb / 2;
+  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.kc));
+  for (int i0 = 0; i0 < kD * cpr; i0 += 64) {
+    const int i = i0 + lane, row = i / cpr, col = i % cpr;
+    dma16(a.kl + 16 * kb * row + 8 * kb * h + 16 * col, base + 16 * i0);
+  }
+}
+__device__ __forceinline__ void issue_values_u(const UMap& M, uint8_t* lds, const PageAddr& a, int vb, int gv, int h,
+                                               int lane) {
+  copy_to_lds(lds + M.vc, a.vc + 16 * vb * kHalfTok * h, 16 * vb * kHalfTok, lane);
+  copy_to_lds(lds + M.vs, (const uint8_t*)a.vs + 128 * gv * h, 128 * gv, lane);
+  copy_to_lds(lds + M.vz, (const uint8_t*)a.vz + 128 * gv * h, 128 * gv, lane);
+}
+
+// Four codes (one per byte of e, values 0..255) -> their dequantized values as
+// an fp16 B operand: fp16(fp16(code * s) + z), bf16 precision if BF16.  s2, z2
+// hold (s, s) and (z, z); the ops stay separate (-ffp-contract=off).
+template <bool BF16>
+__device__ __forceinline__ half4 dequant4(uint32_t e, uint32_t s2, uint32_t z2) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 off = {(_Float16)-1024.f, (_Float16)-1024.f};
+  const h2 s = __builtin_bit_cast(h2, s2), z = __builtin_bit_cast(h2, z2);
+  const h2 c01 = __builtin_bit_cast(h2, perm(0x64646464u, e, 0x04010400u)) + off;  // codes 0, 1
+  const h2 c23 = __builtin_bit_cast(h2, perm(0x64646464u, e, 0x04030402u)) + off;  // codes 2, 3
+  const h2 p01 = c01 * s, p23 = c23 * s;
+  uint32_t v01 = __builtin_bit_cast(uint32_t, p01 + z), v23 = __builtin_bit_cast(uint32_t, p23 + z);
+  if (BF16) {
+    v01 = round_pair_to_bf16_precision(v01);
+    v23 = round_pair_to_bf16_precision(v23);
+  }
+  return __builtin_bit_cast(half4, make_uint2(v01, v23));
+}
+
+// Lane n's position in a dword of B-bit codes: tpb = 8 / B codes per byte;
+// the lane reads dword n / tpb of a row and takes bit field n % tpb of each of
+// its 4 bytes, i.e. codes 4 tpb (n / tpb) + tpb j + n % tpb, j = 0..3.
+template <int B>
+__device__ __forceinline__ int code_index(int n, int j) {
+  constexpr int tpb = 8 / B;
+  return 4 * tpb * (n / tpb) + tpb * j + n % tpb;
+}
+template <int B>
+__device__ __forceinline__ uint32_t code_mask() {
+  return B == 8 ? 0xffffffffu : (B == 4 ? 0x0f0f0f0fu : 0x03030303u);
+}
+
+template <int GQ, int KB, int VB, bool BF16>
+__global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, kq = lane >> 4;
+  const int worker = blockIdx.x * kWaves + wave;
+  if (worker >= p.B * p.Hkv * p.splits) return;
+  const int split = __builtin_amdgcn_readfirstlane(worker % p.splits);
+  const int bh = __builtin_amdgcn_readfirstlane(worker / p.splits);
+  const int b = __builtin_amdgcn_readfirstlane(bh / p.Hkv), kvh = __builtin_amdgcn_readfirstlane(bh % p.Hkv);
+  const int gv = p.gv;
+  const UMap M = umap(KB, VB, gv);
+  uint8_t* lds = smem + wave * M.bytes;
+  const int hp0 = __builtin_amdgcn_readfirstlane((int)(((int64_t)split * 2 * p.count) / p.splits));
+  const int hp1 = __builtin_amdgcn_readfirstlane((int)(((int64_t)(split + 1) * 2 * p.count) / p.splits));
+
+  // ---- per-lane constants ----
+  constexpr int ktpb = 8 / KB, vtpb = 8 / VB;
+  const int slot = n >> 2, head = n & 3;                   // slot-layout A row n = 4 * slot + head
+  const int krow = M.kc + 8 * KB * kq + 4 * (n / ktpb);    // key code dword of channel kq, + 32 KB per block
+  const int kshift = KB * (n % ktpb);
+  const int vdw = 4 * (n / vtpb);                          // value code dword in a row (tile 0)
+  const int vshift = VB * (n % vtpb);
+  const int vch0 = code_index<VB>(n, 0);                   // first channel of the lane (tile 0)
+  const int vg0 = vch0 / p.vg, vg1 = (vch0 + 64) / p.vg;   // value groups of tiles 0 and 1
+  int aq[4];  // P V A sources: the weight row of the lane's head at its slot, else zeros
+#pragma unroll
+  for (int i = 0; i < 4; ++i) aq[i] = (i == slot && head < GQ) ? M.pt + kPtRow * head + 2 * kq : M.zero + 2 * kq;
+
+  // ---- running state ----
+  // S: lane (n, kq) holds heads 0..3 of half-page token code_index<KB>(n, kq).
+  // O[t]: lane (n, kq) holds heads 0..3 of channel 64 t + code_index<VB>(n, kq).
+  float m_run[4], l_part[4];
+  float4v O[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m_run[i] = -INFINITY;
+    l_part[i] = 0.f;
+  }
+  O[0] = O[1] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  {
+    uint16_t* q16 = (uint16_t*)(lds + M.q16);
+    float qv[4 * kD / 64];
+    dev_load_n(p.query, p.q_dtype, qv, [&](int r) -> int64_t {
+      const int i = lane + 64 * r, h = i / kD, c = i % kD;
+      return h < GQ ? (int64_t)b * p.q_sb + (int64_t)(kvh * GQ + h) * p.q_sh + c : -1;
+    });
+#pragma unroll
+    for (int r = 0; r < 4 * kD / 64; ++r) q16[lane + 64 * r] = __builtin_bit_cast(uint16_t, (_Float16)qv[r]);
+    *(uint32_t*)(lds + M.zero + 4 * lane) = 0u;
+  }
+  lds_sync();
+  half4 qa[kD / 4];  // Q K A operands: q[head][4cb + kq] at half `slot`
+  {
+    const uint16_t* q16 = (const uint16_t*)(lds + M.q16);
+#pragma unroll
+    for (int cb = 0; cb < kD / 4; ++cb) {
+      const _Float16 v = __builtin_bit_cast(_Float16, q16[head * kD + 4 * cb + kq]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qa[cb][i] = i == slot ? v : (_Float16)0.f;
+    }
+  }
+  if (hp0 < hp1) {
+    const PageAddr a0 = page_addr(descriptor(p.segs, p.first + (hp0 >> 1)), bh);
+    issue_keys_u(M, lds, a0, KB, hp0 & 1, lane);
+    issue_values_u(M, lds, a0, VB, gv, hp0 & 1, lane);
+  }
+  const float c2 = p.scale * kLog2e;
+  const uint32_t kmask = code_mask<KB>(), vmask = code_mask<VB>();
+
+#pragma unroll 1
+  for (int hq = hp0; hq < hp1; ++hq) {
+    const bool has_next = hq + 1 < hp1;
+    PageAddr nxt;
+    if (has_next) nxt = page_addr(descriptor(p.segs, p.first + ((hq + 1) >> 1)), bh);
+    const int nh = (hq + 1) & 1;
+    // outstanding, oldest first: key scales + codes (this half), values (this half)
+    vm_wait(n_value_loads_u(VB));
+
+    // ---- S = Q K over the half's 64 tokens ----
+    float4v S = float4v{0.f, 0.f, 0.f, 0.f};
+    {
+      const uint16_t* ks = (const uint16_t*)(lds + M.ks);
+      const uint16_t* kz = (const uint16_t*)(lds + M.kz);
+      constexpr int kAhead = 2;
+      uint32_t w[kD / 4], s2[kD / 4], z2[kD / 4];
+      auto load_cb = [&](int c) {
+        w[c] = lds_u32(lds, krow + 32 * KB * c);
+        s2[c] = (uint32_t)ks[4 * c + kq];
+        z2[c] = (uint32_t)kz[4 * c + kq];
+      };
+#pragma unroll
+      for (int c = 0; c < kAhead; ++c) load_cb(c);
+#pragma unroll
+      for (int cb = 0; cb < kD / 4; ++cb) {
+        if (cb + kAhead < kD / 4) load_cb(cb + kAhead);
+        const uint32_t e = (w[cb] >> kshift) & kmask;
+        S = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], dequant4<BF16>(e, s2[cb] * 0x10001u, z2[cb] * 0x10001u),
+                                                  S, 0, 0, 0);
+      }
+    }
+    lds_sync();
+    if (has_next) issue_keys_u(M, lds, nxt, KB, nh, lane);
+
+    // ---- online softmax in base 2 ----
+    {
+      float x[4];
+      bool over = false;
+#pragma unroll
+      for (int i = 0; i < GQ; ++i) {
+        x[i] = S[i] * c2;
+        over |= x[i] > m_run[i] + kSlack;
+      }
+      if (__ballot(over) != 0ull) {
+#pragma unroll
+        for (int i = 0; i < GQ; ++i) {
+          const float m_new = uniform(fmaxf(m_run[i], wave_max64(x[i])));
+          const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_new);
+          O[0][i] *= alpha;
+          O[1][i] *= alpha;
+          l_part[i] *= alpha;
+          m_run[i] = m_new;
+        }
+      }
+      uint16_t* pt = (uint16_t*)(lds + M.pt);
+      const int tok = code_index<KB>(n, kq);
+#pragma unroll
+      for (int i = 0; i < GQ; ++i) {
+        const float pv = __builtin_amdgcn_exp2f(x[i] - m_run[i]);
+        l_part[i] += pv;
+        pt[i * (kPtRow / 2) + tok] = __builtin_bit_cast(uint16_t, (_Float16)pv);
+      }
+    }
+    lds_sync();
+
+    // this half's values are older than the next half's key loads issued since
+    vm_wait(has_next ? n_key_loads_u(KB) : 0);
+
+    // ---- O += P V: token group tg = tokens 4 tg .. 4 tg + 3, lane's token 4 tg + kq ----
+    {
+      const uint16_t* vs = (const uint16_t*)(lds + M.vs);
+      const uint16_t* vz = (const uint16_t*)(lds + M.vz);
+      half4 a[kHalfTok / 4];
+      uint32_t w0[kHalfTok / 4], w1[kHalfTok / 4], s0[kHalfTok / 4], z0[kHalfTok / 4], s1[kHalfTok / 4],
+          z1[kHalfTok / 4];
+      auto load_tg = [&](int tg) {
+        const int t = 4 * tg + kq;
+        a[tg] = load_a(lds, aq, 8 * tg);
+        w0[tg] = lds_u32(lds, M.vc + 16 * VB * t + vdw);
+        w1[tg] = lds_u32(lds, M.vc + 16 * VB * t + 8 * VB + vdw);
+        s0[tg] = vs[t * gv + vg0];
+        z0[tg] = vz[t * gv + vg0];
+        s1[tg] = vs[t * gv + vg1];
+        z1[tg] = vz[t * gv + vg1];
+      };
+      load_tg(0);
+#pragma unroll
+      for (int tg = 0; tg < kHalfTok / 4; ++tg) {
+        if (tg + 1 < kHalfTok / 4) load_tg(tg + 1);
+        const half4 b0 = dequant4<BF16>((w0[tg] >> vshift) & vmask, s0[tg] * 0x10001u, z0[tg] * 0x10001u);
+        const half4 b1 = dequant4<BF16>((w1[tg] >> vshift) & vmask, s1[tg] * 0x10001u, z1[tg] * 0x10001u);
+        O[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[tg], b0, O[0], 0, 0, 0);
+        O[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[tg], b1, O[1], 0, 0, 0);
+      }
+    }
+    lds_sync();
+    if (has_next) issue_values_u(M, lds, nxt, VB, gv, nh, lane);
+  }
+
+  // ---- partial state ----
+  const int ch = code_index<VB>(n, kq);
+#pragma unroll
+  for (int i = 0; i < GQ; ++i) {
+    const float l = wave_sum64(l_part[i]);
+    const int hq = kvh * GQ + i;
+    float* rec = p.ws + (((int64_t)b * p.Hq + hq) * p.split_stride + split) * (kD + 2);
+    if (lane == 0) {
+      rec[0] = m_run[i] * kLn2;
+      rec[1] = l;
+    }
+    rec[2 + ch] = O[0][i];
+    rec[2 + 64 + ch] = O[1][i];
+  }
+}
+
+}  // namespace
+
+namespace dkv {
+
+// The kernel waits until at most one half page's key or value loads are in
+// flight; vm_wait takes counts below 16.
+int uniform_decode_max_loads(int kb, int vb) {
+  return n_key_loads_u(kb) > n_value_loads_u(vb) ? n_key_loads_u(kb) : n_value_loads_u(vb);
+}
+
+int launch_uniform_decode(const dkv_decode_args& a, int first, int count, int kb, int vb, int vg, int splits,
+                          int split_stride, hipStream_t stream) {
+  FastParams p;
+  p.segs = a.segments;
+  p.first = first;
+  p.count = count;
+  p.B = (int)a.B;
+  p.Hq = (int)a.Hq;
+  p.Hkv = (int)a.Hkv;
+  p.GQ = (int)(a.Hq / a.Hkv);
+  p.splits = splits;
+  p.split_stride = split_stride;
+  p.np = 0;
+  p.vg = vg;
+  p.gv = kD / vg;
+  p.bf16 = a.cache_dtype == kBF16 ? 1 : 0;
+  p.scale = (float)a.scale;
+  p.query = a.query;
+  p.q_dtype = (int)a.q_dtype;
+  p.q_sb = a.q_sb;
+  p.q_sh = a.q_sh;
+  p.ws = (float*)a.workspace;
+  const int64_t workers = (int64_t)p.B * p.Hkv * splits;
+  const dim3 grid((unsigned)((workers + kWaves - 1) / kWaves)), block(256);
+  const size_t lds = (size_t)kWaves * umap(kb, vb, p.gv).bytes;
+  if ((kb != 2 && kb != 4 && kb != 8) || (vb != 2 && vb != 4 && vb != 8)) {
+    set_error("uniform page decode supports 2, 4 and 8-bit codes");
+    return DKV_ERR_UNSUPPORTED;
+  }
+  if (p.GQ != 1 && p.GQ != 2 && p.GQ != 4) {
+    set_error("uniform page decode supports 1, 2 or 4 query heads per KV head");
+    return DKV_ERR_UNSUPPORTED;
+  }
+#define DKV_U_LAUNCH(G, K, V)                                                                            \
+  do {                                                                                                   \
+    if (p.bf16) hipLaunchKernelGGL((decode_pages_uniform<G, K, V, true>), grid, block, lds, stream, p);  \
+    else hipLaunchKernelGGL((decode_pages_uniform<G, K, V, false>), grid, block, lds, stream, p);        \
+  } while (0)
+#define DKV_U_V(G, K)                                   \
+  switch (vb) {                                         \
+    case 2: DKV_U_LAUNCH(G, K, 2); break;               \
+    case 4: DKV_U_LAUNCH(G, K, 4); break;               \
+    default: DKV_U_LAUNCH(G, K, 8); break;              \
+  }
+#define DKV_U_K(G)                                      \
+  switch (kb) {                                         \
+    case 2: DKV_U_V(G, 2); break;                       \
+    case 4: DKV_U_V(G, 4); break;                       \
+    default: DKV_U_V(G, 8); break;                      \
+  }
+  switch (p.GQ) {
+    case 1: DKV_U_K(1); break;
+    case 2: DKV_U_K(2); break;
+    default: DKV_U_K(4); break;
+  }
+#undef DKV_U_K
+#undef DKV_U_V
+#undef DKV_U_LAUNCH
+  return dkv_check_launch("dkv_decode_attention(uniform pages)");
+}
+
+}  // namespace dkv

@@ -18,4 +18,11 @@ size_t fast_decode_lds_bytes(int np, int gv);
 int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, int vg, int splits,
                        int split_stride, hipStream_t stream);
 
+// Uniform pages (KB-bit keys along tokens, VB-bit values along channels):
+// the largest load count one wait must cover, and the launch (splits over
+// half pages).
+int uniform_decode_max_loads(int kb, int vb);
+int launch_uniform_decode(const dkv_decode_args& a, int first, int count, int kb, int vb, int vg, int splits,
+                          int split_stride, hipStream_t stream);
+
 }  // namespace dkv

@@ -47,7 +47,7 @@ extern "C" {
 /* Thread-local description of the last error on this thread. */
 const char* dkv_last_error(void);
 
-/* ABI version (5); bumps when a struct below changes. */
+/* ABI version (6); bumps when a struct below changes. */
 int dkv_abi_version(void);
 
 /*
@@ -181,6 +181,11 @@ typedef struct dkv_segment {
  * bf16 or fp16 cache, every field 16-byte aligned; the caller guarantees this.
  * Those pages are processed by the MFMA page kernel over `fast_splits` splits;
  * the other entries and the tail by the general kernel over `n_splits` splits.
+ * With fast_promoted == 0 the run is instead uniform pages: keys quantized
+ * with fast_key_bits bits along the tokens (one key group per page), values
+ * with fast_value_bits bits along the channels in groups of fast_value_group
+ * (2, 4 or 8 bits each), split over half pages (fast_splits at most
+ * 2 * fast_count).  For Dart pages fast_key_bits and fast_value_bits are 0 or 2.
  *
  * Dense rest: when rest_dense_tokens > 0 the caller guarantees that every entry
  * outside the fast range and the tail are dense segments in the cache dtype
@@ -221,6 +226,7 @@ typedef struct dkv_decode_args {
   int64_t rest_dense_tokens;
   void* fast_events[2];
   const int64_t* tail_tokens_dev;
+  int64_t fast_key_bits, fast_value_bits;
 } dkv_decode_args;
 
 /*

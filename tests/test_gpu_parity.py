@@ -207,3 +207,49 @@ def test_fast_page_kernel_split_counts_agree():
     for o in outs:
         assert rel_err(o.unsqueeze(2), ref32) <= 2e-3
         assert rel_err(o.unsqueeze(2), outs[0].unsqueeze(2)) <= 1e-3
+
+
+@pytest.mark.parametrize("kb,vb,B,Hkv,Hq,T,dtype,vg", [
+    (4, 4, 1, 8, 32, 1024, torch.bfloat16, 64),   # config 5's 4-bit variant shape
+    (2, 2, 3, 4, 16, 2000, torch.bfloat16, 64),
+    (8, 8, 2, 2, 4, 1500, torch.float16, 32),     # GQA 2, fp16 cache
+    (4, 2, 2, 4, 4, 700, torch.bfloat16, 128),    # GQA 1, mixed widths
+    (2, 8, 1, 2, 8, 900, torch.float16, 16),
+    (8, 4, 2, 3, 12, 1100, torch.bfloat16, 64),
+])
+def test_uniform_page_kernel_vs_oracle_and_general(kb, vb, B, Hkv, Hq, T, dtype, vg):
+    """Uniform pages (no promoted channels): the arithmetic page kernel against the oracle and the general
+    kernel, with a sink and a held tail around the page run."""
+    dart = _dkv()
+    cache, q, ref32 = _oracle_and_cache(B, Hkv, Hq, T, dtype, seed=11 + T + kb, value_group_size=vg,
+                                        promote_ratio=0.0, key_bits=kb, value_bits=vb)
+    plan = cache.decode_plan(q.device)
+    print("case", kb, vb, B, Hkv, Hq, T, dtype, vg, "fast pages", plan.fast_count, "of", plan.count, flush=True)
+    assert plan.fast_count == (T - 32) // 128
+    assert (plan.fast_promoted, plan.fast_key_bits, plan.fast_value_bits) == (0, kb, vb)
+    out_fast = torch.empty(B, Hq, 128, dtype=torch.float32, device=DEV)
+    out_gen = torch.empty_like(out_fast)
+    dart.decode_attention(q, cache, out_f32=out_fast, fast=True)
+    dart.decode_attention(q, cache, out_f32=out_gen, fast=False)
+    torch.cuda.synchronize()
+    e_fast = rel_err(out_fast.unsqueeze(2), ref32)
+    e_gen = rel_err(out_gen.unsqueeze(2), ref32)
+    print("rel err fast", e_fast, "general", e_gen, flush=True)
+    assert e_gen <= 2e-3
+    assert e_fast <= 2e-3
+
+
+def test_uniform_page_kernel_split_counts_agree():
+    """Splits over half pages: odd counts start and end mid-page; all agree within the fp16 rounding of
+    the softmax weights."""
+    dart = _dkv()
+    cache, q, ref32 = _oracle_and_cache(2, 8, 32, 3000, torch.bfloat16, seed=5, promote_ratio=0.0, bits=4)
+    pages = cache.decode_plan(q.device).fast_count
+    outs = []
+    for splits in (1, 3, 7, 2 * pages):
+        o = torch.empty(2, 32, 128, dtype=torch.float32, device=DEV)
+        dart.decode_attention(q, cache, out_f32=o, n_splits=splits, fast=True)
+        outs.append(o.cpu())
+    for o in outs:
+        assert rel_err(o.unsqueeze(2), ref32) <= 2e-3
+        assert rel_err(o.unsqueeze(2), outs[0].unsqueeze(2)) <= 1e-3
