@@ -6,9 +6,10 @@
 // metadata, bf16 or fp16 cache, up to 4 query heads per KV head.
 //
 // Each wave owns a split: a contiguous range of half pages (64 tokens; half
-// page q is half q & 1 of page q >> 1) of one (batch, kv head).  Per half page
-// it stages the half's key codes (every channel), value rows and scales in its
-// LDS, then
+// page q is half q & 1 of page q >> 1) of one (batch, kv head).  It stages a
+// page's key codes (every channel) and key scales once, when the page starts
+// (for 8-bit keys, whose LDS would double, each half stages its own half of
+// every key row), and each half's value rows and scales; then per half page
 //   * S = Q K with v_mfma_f32_16x16x16f16 in the slot layout (rows = 4 slots x
 //     4 query heads; a lane's four B values are four tokens of one channel,
 //     A carries the query at the lane's slot); one tile covers the 64 tokens;
@@ -40,10 +41,16 @@ struct UMap {
   int kc, vc, ks, kz, vs, vz, q16, pt, zero, bytes;
 };
 
+// Key rows staged per page (2: both halves of every channel's 16 KB-byte row)
+// or per half page (1).  A half row is half a 128-byte line for 2- and 4-bit
+// keys; staging it per half would fetch the line again once L2 has dropped it.
+__host__ __device__ constexpr int key_rows_per_stage(int kb) { return kb <= 4 ? 2 : 1; }
+
 __host__ __device__ inline UMap umap(int kb, int vb, int gv) {
   UMap m;
   int o = 0;
-  m.kc = o; o += kD * 8 * kb;          // key codes of the half  [128 ch][8 KB bytes]
+  const int kf = key_rows_per_stage(kb);
+  m.kc = o; o += kD * 8 * kb * kf;     // key codes [128 ch][8 KB kf bytes]
   m.vc = o; o += kHalfTok * 16 * vb;   // value codes of the half [64 tok][16 VB bytes]
   m.ks = o; o += 256;                  // key scale [128] fp16
   m.kz = o; o += 256;                  // key zero  [128] fp16
@@ -58,15 +65,21 @@ __host__ __device__ inline UMap umap(int kb, int vb, int gv) {
   return m;
 }
 
-// Staging: scales and key codes of a half page (issued after its Q K), then
-// value codes and value scales (issued after its P V).
-__host__ __device__ inline int n_key_loads_u(int kb) { return kb + 2; }
+// Staging: key scales and codes of a page (or half page, see above), issued
+// after the Q K of the half before it, then value codes and value scales of a
+// half page (issued after the P V of the half before it).
+__host__ __device__ inline int n_key_loads_u(int kb) { return kb * key_rows_per_stage(kb) + 2; }
 __host__ __device__ inline int n_value_loads_u(int vb) { return vb + 2; }
 
 __device__ __forceinline__ void issue_keys_u(const UMap& M, uint8_t* lds, const PageAddr& a, int kb, int h,
                                              int lane) {
   copy_to_lds(lds + M.ks, (const uint8_t*)a.ks, 256, lane);
   copy_to_lds(lds + M.kz, (const uint8_t*)a.kz, 256, lane);
+  const int kf = key_rows_per_stage(kb);
+  if (kf == 2) {  // whole rows: one contiguous block
+    copy_to_lds(lds + M.kc, a.kl, kD * 16 * kb, lane);
+    return;
+  }
   // 16-byte chunk i of the half's codes: row i / cpr, column i % cpr
   const int cpr = kb / 2;
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.kc));
@@ -134,7 +147,8 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
   // ---- per-lane constants ----
   constexpr int ktpb = 8 / KB, vtpb = 8 / VB;
   const int slot = n >> 2, head = n & 3;                   // slot-layout A row n = 4 * slot + head
-  const int krow = M.kc + 8 * KB * kq + 4 * (n / ktpb);    // key code dword of channel kq, + 32 KB per block
+  constexpr int kf = key_rows_per_stage(KB);
+  const int krow = M.kc + 8 * KB * kf * kq + 4 * (n / ktpb);  // key code dword of channel kq, + 32 KB kf per block
   const int kshift = KB * (n % ktpb);
   const int vdw = 4 * (n / vtpb);                          // value code dword in a row (tile 0)
   const int vshift = VB * (n % vtpb);
@@ -192,7 +206,9 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
     PageAddr nxt;
     if (has_next) nxt = page_addr(descriptor(p.segs, p.first + ((hq + 1) >> 1)), bh);
     const int nh = (hq + 1) & 1;
-    // outstanding, oldest first: key scales + codes (this half), values (this half)
+    // the next half needs new key rows unless it is the second half of a page staged whole
+    const bool keys_next = has_next && (kf == 1 || nh == 0);
+    // outstanding, oldest first: key scales + codes (if staged for this half), values (this half)
     vm_wait(n_value_loads_u(VB));
 
     // ---- S = Q K over the half's 64 tokens ----
@@ -202,8 +218,9 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
       const uint16_t* kz = (const uint16_t*)(lds + M.kz);
       constexpr int kAhead = 2;
       uint32_t w[kD / 4], s2[kD / 4], z2[kD / 4];
+      const int kh = krow + (kf == 2 ? 8 * KB * (hq & 1) : 0);
       auto load_cb = [&](int c) {
-        w[c] = lds_u32(lds, krow + 32 * KB * c);
+        w[c] = lds_u32(lds, kh + 32 * KB * kf * c);
         s2[c] = (uint32_t)ks[4 * c + kq];
         z2[c] = (uint32_t)kz[4 * c + kq];
       };
@@ -218,7 +235,7 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
       }
     }
     lds_sync();
-    if (has_next) issue_keys_u(M, lds, nxt, KB, nh, lane);
+    if (keys_next) issue_keys_u(M, lds, nxt, KB, nh, lane);
 
     // ---- online softmax in base 2 ----
     {
@@ -252,7 +269,7 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
     lds_sync();
 
     // this half's values are older than the next half's key loads issued since
-    vm_wait(has_next ? n_key_loads_u(KB) : 0);
+    vm_wait(keys_next ? n_key_loads_u(KB) : 0);
 
     // ---- O += P V: token group tg = tokens 4 tg .. 4 tg + 3, lane's token 4 tg + kq ----
     {
