@@ -17,11 +17,14 @@
 //   * O += P V in the same slot layout (a lane's four B values are four
 //     channels of one token; A carries the weight at the lane's slot), two
 //     tiles of 64 channels.
-// Codes are dequantized arithmetically, exactly as the reference rounds:
-// byte permutes place each code under the fp16 exponent of 1024 (0x64xx =
-// 1024 + code), subtracting 1024 gives the code exactly in fp16, then
-// fp16(code * scale), fp16(+ zero) and, for bf16 caches, bf16 precision.  No
-// tables: a uniform page's value set per scale is the whole code range.
+// Codes are dequantized arithmetically, exactly as the reference rounds: the
+// code exactly in fp16, then fp16(code * scale), fp16(+ zero) and, for bf16
+// caches, bf16 precision.  Codes below 16 become fp16 through the fp8
+// converter: the e4m3 pattern of a code c < 16 is c * 2^-9 (subnormals and
+// the first binade are evenly spaced), and the converter's power-of-two scale
+// 2^9 restores c.  8-bit codes use byte permutes under the fp16 exponent of
+// 1024 (0x64xx = 1024 + code) and subtract 1024.  Scales and zero points are
+// duplicated into (s, s, z, z) tables once per page (keys) or half (values).
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -38,7 +41,7 @@ constexpr int kHalfTok = 64;   // tokens per half page
 constexpr int kPtRow = 160;    // bytes between softmax-weight rows ([4][64] fp16, 8 banks apart)
 
 struct UMap {
-  int kc, vc, ks, kz, vs, vz, q16, pt, zero, bytes;
+  int kc, vc, ks, kz, vs, vz, kt, vt, q16, pt, zero, bytes;
 };
 
 // Key rows staged per page (2: both halves of every channel's 16 KB-byte row)
@@ -56,6 +59,8 @@ __host__ __device__ inline UMap umap(int kb, int vb, int gv) {
   m.kz = o; o += 256;                  // key zero  [128] fp16
   m.vs = o; o += 128 * gv;             // value scale of the half [64 tok][Gv] fp16
   m.vz = o; o += 128 * gv;             // value zero  of the half [64 tok][Gv] fp16
+  m.kt = o; o += kD * 8;               // key (s, s, z, z) per channel [128] (fp16 pairs)
+  m.vt = o; o += kHalfTok * 8 * gv;    // value (s, s, z, z) of the half [64 tok][Gv]
   m.q16 = o; o += 1024;                // query [4][128 ch] fp16 (split start only)
   o = (o + 127) / 128 * 128;
   m.pt = o; o += 4 * kPtRow;           // softmax weights [4][64 tok] fp16
@@ -95,16 +100,22 @@ __device__ __forceinline__ void issue_values_u(const UMap& M, uint8_t* lds, cons
   copy_to_lds(lds + M.vz, (const uint8_t*)a.vz + 128 * gv * h, 128 * gv, lane);
 }
 
-// Four codes (one per byte of e, values 0..255) -> their dequantized values as
-// an fp16 B operand: fp16(fp16(code * s) + z), bf16 precision if BF16.  s2, z2
-// hold (s, s) and (z, z); the ops stay separate (-ffp-contract=off).
-template <bool BF16>
-__device__ __forceinline__ half4 dequant4(uint32_t e, uint32_t s2, uint32_t z2) {
+// Four codes (one per byte of e, values 0..2^B - 1) -> their dequantized
+// values as an fp16 B operand: fp16(fp16(code * s) + z), bf16 precision if
+// BF16.  sz holds (s, s) and (z, z); the ops stay separate (-ffp-contract=off).
+template <int B, bool BF16>
+__device__ __forceinline__ half4 dequant4(uint32_t e, uint2 sz) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  const h2 off = {(_Float16)-1024.f, (_Float16)-1024.f};
-  const h2 s = __builtin_bit_cast(h2, s2), z = __builtin_bit_cast(h2, z2);
-  const h2 c01 = __builtin_bit_cast(h2, perm(0x64646464u, e, 0x04010400u)) + off;  // codes 0, 1
-  const h2 c23 = __builtin_bit_cast(h2, perm(0x64646464u, e, 0x04030402u)) + off;  // codes 2, 3
+  const h2 s = __builtin_bit_cast(h2, sz.x), z = __builtin_bit_cast(h2, sz.y);
+  h2 c01, c23;  // codes 0, 1 and 2, 3
+  if (B <= 4) {
+    c01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(e, 512.f, false);
+    c23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(e, 512.f, true);
+  } else {
+    const h2 off = {(_Float16)-1024.f, (_Float16)-1024.f};
+    c01 = __builtin_bit_cast(h2, perm(0x64646464u, e, 0x04010400u)) + off;
+    c23 = __builtin_bit_cast(h2, perm(0x64646464u, e, 0x04030402u)) + off;
+  }
   const h2 p01 = c01 * s, p23 = c23 * s;
   uint32_t v01 = __builtin_bit_cast(uint32_t, p01 + z), v23 = __builtin_bit_cast(uint32_t, p23 + z);
   if (BF16) {
@@ -125,6 +136,15 @@ __device__ __forceinline__ int code_index(int n, int j) {
 template <int B>
 __device__ __forceinline__ uint32_t code_mask() {
   return B == 8 ? 0xffffffffu : (B == 4 ? 0x0f0f0f0fu : 0x03030303u);
+}
+
+// (s, s, z, z) table entries from fp16 scale / zero arrays: lanes take
+// entries lane, lane + 64, ... of n.
+__device__ __forceinline__ void build_sz_table(uint8_t* lds, int dst, int src_s, int src_z, int n, int lane) {
+  const uint16_t* s = (const uint16_t*)(lds + src_s);
+  const uint16_t* z = (const uint16_t*)(lds + src_z);
+  for (int i = lane; i < n; i += 64)
+    *(uint2*)(lds + dst + 8 * i) = make_uint2((uint32_t)s[i] * 0x10001u, (uint32_t)z[i] * 0x10001u);
 }
 
 template <int GQ, int KB, int VB, bool BF16>
@@ -210,19 +230,21 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
     const bool keys_next = has_next && (kf == 1 || nh == 0);
     // outstanding, oldest first: key scales + codes (if staged for this half), values (this half)
     vm_wait(n_value_loads_u(VB));
+    if (hq == hp0 || kf == 1 || (hq & 1) == 0) {  // keys staged for this half: their (s, s, z, z) table
+      build_sz_table(lds, M.kt, M.ks, M.kz, kD, lane);
+      lds_sync();
+    }
 
     // ---- S = Q K over the half's 64 tokens ----
     float4v S = float4v{0.f, 0.f, 0.f, 0.f};
     {
-      const uint16_t* ks = (const uint16_t*)(lds + M.ks);
-      const uint16_t* kz = (const uint16_t*)(lds + M.kz);
       constexpr int kAhead = 2;
-      uint32_t w[kD / 4], s2[kD / 4], z2[kD / 4];
+      uint32_t w[kD / 4];
+      uint2 sz[kD / 4];
       const int kh = krow + (kf == 2 ? 8 * KB * (hq & 1) : 0);
       auto load_cb = [&](int c) {
         w[c] = lds_u32(lds, kh + 32 * KB * kf * c);
-        s2[c] = (uint32_t)ks[4 * c + kq];
-        z2[c] = (uint32_t)kz[4 * c + kq];
+        sz[c] = *(const uint2*)(lds + M.kt + 8 * (4 * c + kq));
       };
 #pragma unroll
       for (int c = 0; c < kAhead; ++c) load_cb(c);
@@ -230,12 +252,14 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
       for (int cb = 0; cb < kD / 4; ++cb) {
         if (cb + kAhead < kD / 4) load_cb(cb + kAhead);
         const uint32_t e = (w[cb] >> kshift) & kmask;
-        S = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], dequant4<BF16>(e, s2[cb] * 0x10001u, z2[cb] * 0x10001u),
-                                                  S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], dequant4<KB, BF16>(e, sz[cb]), S, 0, 0, 0);
       }
     }
     lds_sync();
     if (keys_next) issue_keys_u(M, lds, nxt, KB, nh, lane);
+    // this half's values are older than the next half's key loads issued since
+    vm_wait(keys_next ? n_key_loads_u(KB) : 0);
+    build_sz_table(lds, M.vt, M.vs, M.vz, kHalfTok * gv, lane);
 
     // ---- online softmax in base 2 ----
     {
@@ -268,32 +292,25 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
     }
     lds_sync();
 
-    // this half's values are older than the next half's key loads issued since
-    vm_wait(keys_next ? n_key_loads_u(KB) : 0);
-
     // ---- O += P V: token group tg = tokens 4 tg .. 4 tg + 3, lane's token 4 tg + kq ----
     {
-      const uint16_t* vs = (const uint16_t*)(lds + M.vs);
-      const uint16_t* vz = (const uint16_t*)(lds + M.vz);
       half4 a[kHalfTok / 4];
-      uint32_t w0[kHalfTok / 4], w1[kHalfTok / 4], s0[kHalfTok / 4], z0[kHalfTok / 4], s1[kHalfTok / 4],
-          z1[kHalfTok / 4];
+      uint32_t w0[kHalfTok / 4], w1[kHalfTok / 4];
+      uint2 sz0[kHalfTok / 4], sz1[kHalfTok / 4];
       auto load_tg = [&](int tg) {
         const int t = 4 * tg + kq;
         a[tg] = load_a(lds, aq, 8 * tg);
         w0[tg] = lds_u32(lds, M.vc + 16 * VB * t + vdw);
         w1[tg] = lds_u32(lds, M.vc + 16 * VB * t + 8 * VB + vdw);
-        s0[tg] = vs[t * gv + vg0];
-        z0[tg] = vz[t * gv + vg0];
-        s1[tg] = vs[t * gv + vg1];
-        z1[tg] = vz[t * gv + vg1];
+        sz0[tg] = *(const uint2*)(lds + M.vt + 8 * (t * gv + vg0));
+        sz1[tg] = *(const uint2*)(lds + M.vt + 8 * (t * gv + vg1));
       };
       load_tg(0);
 #pragma unroll
       for (int tg = 0; tg < kHalfTok / 4; ++tg) {
         if (tg + 1 < kHalfTok / 4) load_tg(tg + 1);
-        const half4 b0 = dequant4<BF16>((w0[tg] >> vshift) & vmask, s0[tg] * 0x10001u, z0[tg] * 0x10001u);
-        const half4 b1 = dequant4<BF16>((w1[tg] >> vshift) & vmask, s1[tg] * 0x10001u, z1[tg] * 0x10001u);
+        const half4 b0 = dequant4<VB, BF16>((w0[tg] >> vshift) & vmask, sz0[tg]);
+        const half4 b1 = dequant4<VB, BF16>((w1[tg] >> vshift) & vmask, sz1[tg]);
         O[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[tg], b0, O[0], 0, 0, 0);
         O[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[tg], b1, O[1], 0, 0, 0);
       }
