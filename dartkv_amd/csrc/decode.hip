@@ -269,11 +269,16 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
 
 // Dense 16-bit segments (the sink and the held tail): one wave per (batch,
 // kv head, segment, 32-token chunk), fp32 dot products as the reference's
-// eager attention computes them.  Every global load of a wave is issued
-// before the first use (query, the chunk's K rows and V rows), so a wave costs
-// one memory round trip.  Q K: lane = (token, half of the channels), the two
-// halves combined across lanes l and l^32; P V: lane = channel pair.  The
-// wave writes one record at split slot split_offset + segment * chunks + chunk.
+// eager attention computes them.  Q K: lane = (token, half of the channels),
+// the two halves combined across lanes l and l^32; P V: lane = channel pair.
+// The K and V rows are loaded straight into registers (rows past the chunk's
+// tokens re-read its last row; their logits become -inf and their weights 0),
+// the query and the softmax weights are read from LDS as broadcasts.  Each
+// step's LDS reads are addressed through the previous step's accumulator, so
+// only one step's values are live: unrolled whole, the compiler issued all
+// 128 x MG query reads first and kept them in registers (one wave per SIMD).
+// The wave
+// writes one record at split slot split_offset + segment * chunks + chunk.
 constexpr int kDenseWaves = 4;
 constexpr int kDenseChunk = 32;
 constexpr int kDenseDim = 128;
@@ -283,10 +288,44 @@ constexpr int kDenseMaxGroup = 8;
 // zero), so the unrolled loops carry no per-head branches; only the record
 // writes are guarded.
 #define DKV_ALL_HEADS(h) _Pragma("unroll") for (int h = 0; h < MG; ++h)
+
+template <bool BF>
+__device__ __forceinline__ float dense_elem(uint16_t bits) {
+  return BF ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
+}
+
+// An offset the compiler must treat as computed from every dep[h]: reads
+// addressed with it cannot be issued before all of them are.  (Depending on
+// one head only let the compiler finish that head's chain first and keep the
+// other heads' query values live across all steps.)
 template <int MG>
+__device__ __forceinline__ int after(int offset, const float (&dep)[MG]) {
+#pragma unroll
+  for (int h = 0; h < MG; ++h) asm volatile("" : "+v"(offset) : "v"(dep[h]));
+  return offset;
+}
+
+// MG consecutive floats from LDS (one read for MG = 2, 4; two for 8)
+template <int MG>
+__device__ __forceinline__ void lds_heads(const float* src, float (&x)[MG]) {
+  if (MG == 1) {
+    x[0] = src[0];
+  } else if (MG == 2) {
+    const float2 v = *(const float2*)src;
+    x[0] = v.x; x[1 % MG] = v.y;
+  } else {
+#pragma unroll
+    for (int j = 0; j < MG; j += 4) {
+      const float4 v = *(const float4*)(src + j);
+      x[j] = v.x; x[(j + 1) % MG] = v.y; x[(j + 2) % MG] = v.z; x[(j + 3) % MG] = v.w;
+    }
+  }
+}
+
+template <int MG, bool BF>
 __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodeParams p, int chunks) {
-  __shared__ float qsh[kDenseWaves][kDenseDim * MG];      // [c][MG]
-  __shared__ float wsh[kDenseWaves][MG * kDenseChunk];    // [h][t] weights of the chunk
+  __shared__ __attribute__((aligned(16))) float qsh[kDenseWaves][kDenseDim * MG];    // [c][MG]
+  __shared__ __attribute__((aligned(16))) float wsh[kDenseWaves][kDenseChunk * MG];  // [t][MG] weights
   const dkv_decode_args& a = p.a;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -298,7 +337,6 @@ __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodePara
   const int b = bhi / (int)a.Hkv, kvh = bhi % (int)a.Hkv;
   const int64_t bh = (int64_t)bhi;
   const int G = p.group;
-  const bool bf = a.cache_dtype == kBF16;
   float* qs = qsh[wave];
   float* ws = wsh[wave];
 
@@ -307,105 +345,89 @@ __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodePara
                   seg.tokens <= chunks * kDenseChunk;
   const int t0 = chunk * kDenseChunk;
   const int nt = ok ? max(0, min(kDenseChunk, seg.tokens - t0)) : 0;
-  typedef __attribute__((address_space(1))) const uint16_t gu16;
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(1))) const u32x4 gu4;
   typedef __attribute__((address_space(1))) const uint32_t gu32;
-  gu16* kbase = (gu16*)(seg.key[0] + 2 * (uint64_t)(bh * seg.key_bh[0]));
-  gu16* vbase = (gu16*)(seg.value[0] + 2 * (uint64_t)(bh * seg.value_bh[0]));
-
-  // ---- all loads first: unconditional (rows past the chunk's tokens re-read
-  // the segment's last row and are zeroed), so every load is issued before the
-  // first wait ----
+  const uint16_t* kbase = (const uint16_t*)(seg.key[0] + 2 * (uint64_t)(bh * seg.key_bh[0]));
+  const uint16_t* vbase = (const uint16_t*)(seg.value[0] + 2 * (uint64_t)(bh * seg.value_bh[0]));
   const int kt = lane & (kDenseChunk - 1), khalf = lane >> 5;  // token, channel half of the Q K lane
-  uint4 krow[8];
-  uint32_t vpair[kDenseChunk];
   const int last = nt > 0 ? nt - 1 : 0;
+
+  // K rows (8 x 16 B per lane) and V pairs (one dword per token), issued
+  // before the query so one wait covers them; the query goes to LDS as fp32
+  u32x4 krow[8];
+  uint32_t vpair[kDenseChunk];
   if (nt > 0) {
-    const int krow_t = t0 + (kt < nt ? kt : last);
+    gu4* krp = (gu4*)(kbase + (int64_t)(t0 + (kt < nt ? kt : last)) * kDenseDim + 64 * khalf);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const u32x4 w = *((gu4*)(kbase + (int64_t)krow_t * kDenseDim + 64 * khalf) + u);
-      krow[u] = make_uint4(w.x, w.y, w.z, w.w);
-    }
+    for (int u = 0; u < 8; ++u) krow[u] = krp[u];
 #pragma unroll
     for (int u = 0; u < kDenseChunk; ++u)
       vpair[u] = *(gu32*)(vbase + (int64_t)(t0 + (u < nt ? u : last)) * kDenseDim + 2 * lane);
   }
-  // the query after the K/V loads, so one wait covers them all
-  float qv[kDenseDim * MG / 64];
-  dev_load_n(a.query, (int)a.q_dtype, qv, [&](int r) -> int64_t {
-    const int i = lane + 64 * r, c = i / MG, h = i % MG;
-    return h < G ? (int64_t)b * a.q_sb + (int64_t)(kvh * G + h) * a.q_sh + c : -1;
-  });
+  {
+    float qv[kDenseDim * MG / 64];
+    dev_load_n(a.query, (int)a.q_dtype, qv, [&](int r) -> int64_t {
+      const int i = lane + 64 * r, c = i / MG, h = i % MG;
+      return h < G ? (int64_t)b * a.q_sb + (int64_t)(kvh * G + h) * a.q_sh + c : -1;
+    });
+#pragma unroll
+    for (int r = 0; r < kDenseDim * MG / 64; ++r) qs[lane + 64 * r] = qv[r];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  float m[MG], l[MG], pv0[MG], pv1[MG];
   if (nt > 0) {
-    // every load is issued before the first use
-    asm volatile("" ::"v"(krow[0].x), "v"(krow[1].x), "v"(krow[2].x), "v"(krow[3].x), "v"(krow[4].x),
-                 "v"(krow[5].x), "v"(krow[6].x), "v"(krow[7].x), "v"(vpair[0]), "v"(vpair[1]), "v"(vpair[2]),
-                 "v"(vpair[3]), "v"(vpair[4]), "v"(vpair[5]), "v"(vpair[6]), "v"(vpair[7]), "v"(vpair[8]),
-                 "v"(vpair[9]), "v"(vpair[10]), "v"(vpair[11]), "v"(vpair[12]), "v"(vpair[13]), "v"(vpair[14]),
-                 "v"(vpair[15]));
-    asm volatile("" ::"v"(vpair[16]), "v"(vpair[17]), "v"(vpair[18]), "v"(vpair[19]), "v"(vpair[20]),
-                 "v"(vpair[21]), "v"(vpair[22]), "v"(vpair[23]), "v"(vpair[24]), "v"(vpair[25]), "v"(vpair[26]),
-                 "v"(vpair[27]), "v"(vpair[28]), "v"(vpair[29]), "v"(vpair[30]), "v"(vpair[31]));
-    if (kt >= nt) {
+    // ---- logits: 8 steps of 8 channels ----
+    float logit[MG];
+    DKV_ALL_HEADS(h) logit[h] = 0.f;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) krow[u] = make_uint4(0u, 0u, 0u, 0u);
+    for (int u = 0; u < 8; ++u) {
+      const uint32_t ww[4] = {krow[u].x, krow[u].y, krow[u].z, krow[u].w};
+      const int qo = after<MG>((64 * khalf + 8 * u) * MG, logit);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float kv = dense_elem<BF>((uint16_t)(ww[i / 2] >> (16 * (i % 2))));
+        float q[MG];
+        lds_heads<MG>(qs + qo + i * MG, q);
+        DKV_ALL_HEADS(h) logit[h] = fmaf(q[h], kv, logit[h]);
+      }
     }
-#pragma unroll
-    for (int u = 0; u < kDenseChunk; ++u)
-      if (u >= nt) vpair[u] = 0u;
-  } else {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) krow[u] = make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-    for (int u = 0; u < kDenseChunk; ++u) vpair[u] = 0u;
-  }
-#pragma unroll
-  for (int r = 0; r < kDenseDim * MG / 64; ++r) qs[lane + 64 * r] = qv[r];
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // ---- logits ----
-  float logit[MG];
-  DKV_ALL_HEADS(h) logit[h] = 0.f;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const uint32_t ww[4] = {krow[u].x, krow[u].y, krow[u].z, krow[u].w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint16_t bits = (uint16_t)(ww[i / 2] >> (16 * (i % 2)));
-      const float kv = bf ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
-      const float* qc = qs + (64 * khalf + 8 * u + i) * MG;
-      DKV_ALL_HEADS(h) logit[h] = fmaf(qc[h], kv, logit[h]);
-    }
-  }
-  const float scale = (float)a.scale;
-  float m[MG], l[MG];
-  DKV_ALL_HEADS(h) {
-    const float lg = kt < nt ? (logit[h] + __shfl_xor(logit[h], 32, 64)) * scale : -INFINITY;
-    m[h] = wave_max(lg);
-    const float w = kt < nt ? expf(lg - m[h]) : 0.f;
-    if (khalf == 0) ws[h * kDenseChunk + kt] = w;
-    l[h] = wave_sum(w) * 0.5f;  // every weight appears in two lanes
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // ---- weighted values: channels 2 lane, 2 lane + 1 ----
-  float pv0[MG], pv1[MG];
-  DKV_ALL_HEADS(h) pv0[h] = pv1[h] = 0.f;
-#pragma unroll
-  for (int u = 0; u < kDenseChunk; ++u) {
-    const float v0 = bf ? bf16_to_f32((uint16_t)vpair[u]) : (float)__builtin_bit_cast(_Float16, (uint16_t)vpair[u]);
-    const float v1 = bf ? bf16_to_f32((uint16_t)(vpair[u] >> 16))
-                        : (float)__builtin_bit_cast(_Float16, (uint16_t)(vpair[u] >> 16));
+    const float scale = (float)a.scale;
     DKV_ALL_HEADS(h) {
-      const float w = ws[h * kDenseChunk + u];
-      pv0[h] = fmaf(w, v0, pv0[h]);
-      pv1[h] = fmaf(w, v1, pv1[h]);
+      const float lg = kt < nt ? (logit[h] + __shfl_xor(logit[h], 32, 64)) * scale : -INFINITY;
+      m[h] = wave_max(lg);
+      const float w = kt < nt ? expf(lg - m[h]) : 0.f;
+      if (khalf == 0) ws[kt * MG + h] = w;
+      l[h] = wave_sum(w) * 0.5f;  // every weight appears in two lanes
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- weighted values: channels 2 lane, 2 lane + 1, 4 steps of 8 tokens ----
+    DKV_ALL_HEADS(h) pv0[h] = pv1[h] = 0.f;
+#pragma unroll
+    for (int u0 = 0; u0 < kDenseChunk; u0 += 8) {
+      const int wo = after<MG>(u0 * MG, pv1);
+#pragma unroll
+      for (int u = u0; u < u0 + 8; ++u) {
+        const float v0 = dense_elem<BF>((uint16_t)vpair[u]);
+        const float v1 = dense_elem<BF>((uint16_t)(vpair[u] >> 16));
+        float w[MG];
+        lds_heads<MG>(ws + wo + (u - u0) * MG, w);
+        DKV_ALL_HEADS(h) {
+          pv0[h] = fmaf(w[h], v0, pv0[h]);
+          pv1[h] = fmaf(w[h], v1, pv1[h]);
+        }
+      }
+    }
+  } else {
+    DKV_ALL_HEADS(h) {
+      m[h] = -INFINITY;
+      l[h] = pv0[h] = pv1[h] = 0.f;
     }
   }
 
@@ -416,8 +438,8 @@ __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodePara
         wsp + (((int64_t)b * a.Hq + hq) * p.split_stride + p.split_offset + (int64_t)v * chunks + chunk) * (kDenseDim + 2);
     if (lane == 0) {
       // a segment this kernel cannot read poisons its record (NaN output)
-      rec[0] = ok ? (nt > 0 ? m[h] : -INFINITY) : NAN;
-      rec[1] = nt > 0 ? l[h] : 0.f;
+      rec[0] = ok ? m[h] : NAN;
+      rec[1] = l[h];
     }
     rec[2 + 2 * lane] = pv0[h];
     rec[3 + 2 * lane] = pv1[h];
@@ -562,10 +584,16 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
     const int64_t workers = a.B * a.Hkv * rest * chunks;
     const dim3 grid((unsigned)((workers + kDenseWaves - 1) / kDenseWaves)), block(64 * kDenseWaves);
     const int ch = (int)chunks;
-    if (mg == 1) hipLaunchKernelGGL(decode_dense_rest<1>, grid, block, 0, s, p, ch);
-    else if (mg == 2) hipLaunchKernelGGL(decode_dense_rest<2>, grid, block, 0, s, p, ch);
-    else if (mg == 4) hipLaunchKernelGGL(decode_dense_rest<4>, grid, block, 0, s, p, ch);
-    else hipLaunchKernelGGL(decode_dense_rest<8>, grid, block, 0, s, p, ch);
+#define DKV_DENSE_LAUNCH(MGV)                                                                  \
+  do {                                                                                         \
+    if (a.cache_dtype == dkv::kBF16) hipLaunchKernelGGL((decode_dense_rest<MGV, true>), grid, block, 0, s, p, ch); \
+    else hipLaunchKernelGGL((decode_dense_rest<MGV, false>), grid, block, 0, s, p, ch);      \
+  } while (0)
+    if (mg == 1) DKV_DENSE_LAUNCH(1);
+    else if (mg == 2) DKV_DENSE_LAUNCH(2);
+    else if (mg == 4) DKV_DENSE_LAUNCH(4);
+    else DKV_DENSE_LAUNCH(8);
+#undef DKV_DENSE_LAUNCH
     int rc = dkv_check_launch("dkv_decode_attention(dense)");
     if (rc) return rc;
   } else if (general_splits > 0) {
