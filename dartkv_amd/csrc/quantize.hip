@@ -76,13 +76,36 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_aligned(RowsParams p) 
   }
 }
 
+// Rounding to the source dtype with the hardware conversions (round to
+// nearest even): one v_cvt_pk_bf16_f32 / v_cvt_f16_f32 and its widening.
+template <int SRC>
+__device__ __forceinline__ float src_round(float x) {
+  if (SRC == kBF16) return (float)(__bf16)x;
+  if (SRC == kF16) return (float)(_Float16)x;
+  return x;
+}
+
+// fp32 a / b rounded to nearest, given y = RN(1 / b): q = RN(a y) is within
+// one ulp of a / b, the residual a - b q is exact with an fma, and
+// RN(q + (a - b q) y) is the correctly rounded quotient (Markstein's
+// theorem; no overflow or underflow for quotients of group-relative values).
+__device__ __forceinline__ float div_rn(float a, float b, float y) {
+  const float q = a * y;
+  const float r = __builtin_fmaf(-q, b, a);
+  return __builtin_fmaf(r, y, q);
+}
+
 // Contiguous rows, groups of 8 * L elements (L = 1..64 lanes, a power of two)
 // that tile the row exactly: every lane owns 8 consecutive elements (one
 // 16-byte load for 16-bit sources), the L lanes of a group reduce min/max with
 // cross-lane shuffles, and every lane stores its 8 codes packed (2, 4 or 8
-// bytes).  A wave's loads and stores are contiguous.
-template <int BITS>
-__global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int lanes_per_group) {
+// bytes).  A wave's loads and stores are contiguous.  The source dtype is a
+// template argument, so the per-element chain (subtract, round, divide,
+// round, rint, clamp) has no branches; the division is one reciprocal per
+// group and three operations per element.
+template <int BITS, int SRC>
+__global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int lanes_per_group, int row_shift) {
+  // row_shift = log2(lanes per row) when that is a power of two (no 64-bit division)
   const int64_t lanes_per_row = p.n / 8;
   const int64_t total = p.rows * lanes_per_row;
   const float qmax = (float)((1 << BITS) - 1);
@@ -91,10 +114,13 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int 
        v += (int64_t)gridDim.x * kThreads) {
     // whole waves stay in the loop so the shuffles see every lane of a group
     const bool active = v < total;
-    const int64_t r = active ? v / lanes_per_row : 0;
-    const int64_t i0 = active ? (v % lanes_per_row) * 8 : 0;
+    int64_t r = 0, i0 = 0;
+    if (active) {
+      r = row_shift >= 0 ? v >> row_shift : v / lanes_per_row;
+      i0 = (v - r * lanes_per_row) * 8;
+    }
     float x[8];
-    if (p.src_dtype == kF32) {
+    if (SRC == kF32) {
       const float4* src = (const float4*)((const float*)p.src + r * p.row_stride + i0);
       const float4 a = src[0], b = src[1];
       x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
@@ -105,7 +131,7 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int 
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const uint16_t bits = (uint16_t)(ww[j / 2] >> (16 * (j % 2)));
-        x[j] = p.src_dtype == kBF16 ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
+        x[j] = SRC == kBF16 ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
       }
     }
     float mn = x[0], mx = x[0];
@@ -119,19 +145,26 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int 
       mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     }
     if (!active) continue;
-    const float s = dev_group_scale(mn, mx, qmax, p.src_dtype);
+    const float s = dev_group_scale(mn, mx, qmax, SRC);
+    const float y = __fdiv_rn(1.0f, s);
     if (i0 % p.group == 0) {
       const int64_t g = i0 / p.group;
       dev_store_meta(p.scale, r * p.groups + g, s, p.meta_dtype);
       dev_store_meta(p.zero, r * p.groups + g, mn, p.meta_dtype);
     }
-    uint64_t packed = 0;
+    uint32_t packed[2] = {0u, 0u};  // codes 0..3 and 4..7 for 8-bit, else all in [0]
 #pragma unroll
-    for (int j = 0; j < 8; ++j) packed |= (uint64_t)dev_group_code(x[j], mn, s, qmax, p.src_dtype) << (j * BITS);
+    for (int j = 0; j < 8; ++j) {
+      const float diff = src_round<SRC>(x[j] - mn);
+      const float q = __builtin_rintf(src_round<SRC>(div_rn(diff, s, y)));
+      const uint32_t code = (uint32_t)fminf(fmaxf(q, 0.0f), qmax);
+      if (BITS == 8) packed[j / 4] |= code << (8 * (j % 4));
+      else packed[0] |= code << (j * BITS);
+    }
     uint8_t* out = p.values + r * p.packed_bytes + i0 * BITS / 8;
-    if (BITS == 2) *(uint16_t*)out = (uint16_t)packed;
-    else if (BITS == 4) *(uint32_t*)out = (uint32_t)packed;
-    else *(uint2*)out = make_uint2((uint32_t)packed, (uint32_t)(packed >> 32));
+    if (BITS == 2) *(uint16_t*)out = (uint16_t)packed[0];
+    else if (BITS == 4) *(uint32_t*)out = packed[0];
+    else *(uint2*)out = make_uint2(packed[0], packed[1]);
   }
 }
 
@@ -662,9 +695,21 @@ extern "C" int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, i
     const int64_t lanes = rows * (n / 8);
     const int64_t blocks = std::min<int64_t>((lanes + kThreads - 1) / kThreads, 1 << 20);
     const int lpg = (int)(group / 8);
-    if (bits == 2) hipLaunchKernelGGL(quantize_rows_vec<2>, dim3((unsigned)blocks), dim3(kThreads), 0, s, p, lpg);
-    else if (bits == 4) hipLaunchKernelGGL(quantize_rows_vec<4>, dim3((unsigned)blocks), dim3(kThreads), 0, s, p, lpg);
-    else hipLaunchKernelGGL(quantize_rows_vec<8>, dim3((unsigned)blocks), dim3(kThreads), 0, s, p, lpg);
+    const int64_t lpr = n / 8;
+    const int row_shift = (lpr & (lpr - 1)) == 0 ? __builtin_ctzll((unsigned long long)lpr) : -1;
+#define DKV_ROWS_LAUNCH(B, T) \
+  hipLaunchKernelGGL((quantize_rows_vec<B, T>), dim3((unsigned)blocks), dim3(kThreads), 0, s, p, lpg, row_shift)
+#define DKV_ROWS_BITS(T)                  \
+  do {                                    \
+    if (bits == 2) DKV_ROWS_LAUNCH(2, T); \
+    else if (bits == 4) DKV_ROWS_LAUNCH(4, T); \
+    else DKV_ROWS_LAUNCH(8, T);           \
+  } while (0)
+    if (src_dtype == kBF16) DKV_ROWS_BITS(kBF16);
+    else if (src_dtype == kF16) DKV_ROWS_BITS(kF16);
+    else DKV_ROWS_BITS(kF32);
+#undef DKV_ROWS_BITS
+#undef DKV_ROWS_LAUNCH
   } else if (group % p.per_byte == 0) {
     const int64_t items = rows * p.groups;
     hipLaunchKernelGGL(quantize_rows_aligned, dim3((unsigned)((items + kThreads - 1) / kThreads)), dim3(kThreads), 0,
