@@ -560,10 +560,13 @@ class DartKVCache:
                                  group=kg, promoted=K, selection=selection,
                                  given_idx=None if given is None else given[0].contiguous(), meta=meta,
                                  low=low, high=high, idx=idx, scale=scale, zero=zero)
-            return [MixedQuantizedKey(low_values=low[p], high_values=high[p], channel_indices=idx[p], scale=scale[p],
-                                      zero_point=zero[p], original_shape=(B, H, tokens, D), padded_tokens=G * kg,
-                                      group_size=kg, low_bits=2, promote_bits=c.promote_bits,
-                                      output_dtype=src.dtype) for p in range(n_pages)]
+            # per-page views from one unbind each (indexing page by page costs a
+            # Python-level tensor view per field per page)
+            return [MixedQuantizedKey(low_values=lo, high_values=hi, channel_indices=ix, scale=sc, zero_point=ze,
+                                      original_shape=(B, H, tokens, D), padded_tokens=G * kg, group_size=kg,
+                                      low_bits=2, promote_bits=c.promote_bits, output_dtype=src.dtype)
+                    for lo, hi, ix, sc, ze in zip(low.unbind(0), high.unbind(0), idx.unbind(0), scale.unbind(0),
+                                                  zero.unbind(0))]
         bits = c.resolved_key_bits
         per = 8 // bits
         padded = G * kg
@@ -574,9 +577,10 @@ class DartKVCache:
         launch_key_pages(src, page_tokens=tokens, n_pages=n_pages, key_mode=_lib.KEY_UNIFORM, bits=bits, group=kg,
                          promoted=0, selection=0, given_idx=None, meta=meta, low=values, high=None, idx=None,
                          scale=scale, zero=zero)
-        return [QuantizedTensor(values=values[p], scale=scale[p], zero_point=zero[p], original_shape=(B, H, tokens, D),
+        return [QuantizedTensor(values=va, scale=sc, zero_point=ze, original_shape=(B, H, tokens, D),
                                 original_dim=tokens, padded_dim=padded, packed_dim=packed_dim, group_size=kg,
-                                bits=bits, output_dtype=src.dtype, axis=2) for p in range(n_pages)]
+                                bits=bits, output_dtype=src.dtype, axis=2)
+                for va, sc, ze in zip(values.unbind(0), scale.unbind(0), zero.unbind(0))]
 
     def _quantize_value_chunks(self, value_states: torch.Tensor, chunk: int) -> List[QuantizedTensor]:
         """Value segments of ``chunk`` tokens (last may be shorter) quantized along head_dim.
@@ -603,12 +607,10 @@ class DartKVCache:
             scale = torch.empty(B, H, n, Gv, dtype=meta, device=dev)
             zero = torch.empty(B, H, n, Gv, dtype=meta, device=dev)
             _launch_value_rows(src, bits, vg, meta, values, scale, zero)
-            for i in range(count):
-                a, b = i * size, (i + 1) * size
-                out.append(QuantizedTensor(values=values[..., a:b, :], scale=scale[..., a:b, :],
-                                           zero_point=zero[..., a:b, :], original_shape=(B, H, size, D),
-                                           original_dim=D, padded_dim=padded, packed_dim=packed_dim, group_size=vg,
-                                           bits=bits, output_dtype=value_states.dtype, axis=3))
+            out.extend(QuantizedTensor(values=va, scale=sc, zero_point=ze, original_shape=(B, H, size, D),
+                                       original_dim=D, padded_dim=padded, packed_dim=packed_dim, group_size=vg,
+                                       bits=bits, output_dtype=value_states.dtype, axis=3)
+                       for va, sc, ze in zip(values.split(size, 2), scale.split(size, 2), zero.split(size, 2)))
         return out
 
     def _append_quantized_value_page(self, segment: QuantizedTensor) -> None:

@@ -41,7 +41,8 @@ DKV_HD inline bool sel_before(const SelItem& a, const SelItem& b) {
   return (an && !bn) || (a.v > b.v);
 }
 
-DKV_HD inline void sel_swap(SelItem* a, SelItem* b) {
+template <class It>
+DKV_HD inline void sel_swap(It a, SelItem* b) {
   SelItem t = *a;
   *a = *b;
   *b = t;
@@ -59,7 +60,8 @@ DKV_HD inline int sel_floor_log2(int n) {
 // ---- binary heap on [0, len) whose root is the element that ranks last ----
 
 // Move `value` up from `hole` while its parent ranks before it.
-DKV_HD inline void sel_heap_sift_up(SelItem* a, int hole, int top, SelItem value) {
+template <class It>
+DKV_HD inline void sel_heap_sift_up(It a, int hole, int top, SelItem value) {
   int parent = (hole - 1) / 2;
   while (hole > top && sel_before(a[parent], value)) {
     a[hole] = a[parent];
@@ -71,7 +73,8 @@ DKV_HD inline void sel_heap_sift_up(SelItem* a, int hole, int top, SelItem value
 
 // Fill the hole at `hole` by walking down along the child that ranks later,
 // then sift `value` up from the leaf that was reached.
-DKV_HD inline void sel_heap_adjust(SelItem* a, int hole, int len, SelItem value) {
+template <class It>
+DKV_HD inline void sel_heap_adjust(It a, int hole, int len, SelItem value) {
   const int top = hole;
   int child = hole;
   while (child < (len - 1) / 2) {
@@ -88,7 +91,8 @@ DKV_HD inline void sel_heap_adjust(SelItem* a, int hole, int len, SelItem value)
   sel_heap_sift_up(a, hole, top, value);
 }
 
-DKV_HD inline void sel_make_heap(SelItem* a, int len) {
+template <class It>
+DKV_HD inline void sel_make_heap(It a, int len) {
   if (len < 2) return;
   for (int parent = (len - 2) / 2;; --parent) {
     SelItem value = a[parent];
@@ -98,21 +102,24 @@ DKV_HD inline void sel_make_heap(SelItem* a, int len) {
 }
 
 // Move the root of heap [0, len) to `*out` and re-heap with the old `*out`.
-DKV_HD inline void sel_heap_pop_into(SelItem* a, int len, SelItem* out) {
+template <class It>
+DKV_HD inline void sel_heap_pop_into(It a, int len, SelItem* out) {
   SelItem value = *out;
   *out = a[0];
   sel_heap_adjust(a, 0, len, value);
 }
 
 // Keep the `middle` best-ranked of [0, last) in a heap on [0, middle).
-DKV_HD inline void sel_heap_select(SelItem* a, int middle, int last) {
+template <class It>
+DKV_HD inline void sel_heap_select(It a, int middle, int last) {
   sel_make_heap(a, middle);
   for (int i = middle; i < last; ++i) {
     if (sel_before(a[i], a[0])) sel_heap_pop_into(a, middle, &a[i]);
   }
 }
 
-DKV_HD inline void sel_sort_heap(SelItem* a, int len) {
+template <class It>
+DKV_HD inline void sel_sort_heap(It a, int len) {
   while (len > 1) {
     --len;
     sel_heap_pop_into(a, len, &a[len]);
@@ -121,7 +128,8 @@ DKV_HD inline void sel_sort_heap(SelItem* a, int len) {
 
 // ---- insertion sorts ----
 
-DKV_HD inline void sel_linear_insert_unguarded(SelItem* a, int pos) {
+template <class It>
+DKV_HD inline void sel_linear_insert_unguarded(It a, int pos) {
   SelItem value = a[pos];
   int prev = pos - 1;
   while (sel_before(value, a[prev])) {
@@ -132,7 +140,8 @@ DKV_HD inline void sel_linear_insert_unguarded(SelItem* a, int pos) {
   a[pos] = value;
 }
 
-DKV_HD inline void sel_insertion_sort(SelItem* a, int first, int last) {
+template <class It>
+DKV_HD inline void sel_insertion_sort(It a, int first, int last) {
   if (first == last) return;
   for (int i = first + 1; i < last; ++i) {
     if (sel_before(a[i], a[first])) {
@@ -148,7 +157,8 @@ DKV_HD inline void sel_insertion_sort(SelItem* a, int first, int last) {
 // ---- partitioning ----
 
 // Put the median (under sel_before) of a[x], a[y], a[z] into a[result].
-DKV_HD inline void sel_median_to(SelItem* a, int result, int x, int y, int z) {
+template <class It>
+DKV_HD inline void sel_median_to(It a, int result, int x, int y, int z) {
   if (sel_before(a[x], a[y])) {
     if (sel_before(a[y], a[z]))
       sel_swap(&a[result], &a[y]);
@@ -166,7 +176,8 @@ DKV_HD inline void sel_median_to(SelItem* a, int result, int x, int y, int z) {
 }
 
 // Hoare partition of [first, last) around a[pivot] (pivot lies outside the range).
-DKV_HD inline int sel_partition_unguarded(SelItem* a, int first, int last, int pivot) {
+template <class It>
+DKV_HD inline int sel_partition_unguarded(It a, int first, int last, int pivot) {
   for (;;) {
     while (sel_before(a[first], a[pivot])) ++first;
     --last;
@@ -177,7 +188,8 @@ DKV_HD inline int sel_partition_unguarded(SelItem* a, int first, int last, int p
   }
 }
 
-DKV_HD inline int sel_partition_pivot(SelItem* a, int first, int last) {
+template <class It>
+DKV_HD inline int sel_partition_pivot(It a, int first, int last) {
   const int mid = first + (last - first) / 2;
   sel_median_to(a, first, first + 1, mid, last - 1);
   return sel_partition_unguarded(a, first + 1, last, first);
@@ -185,7 +197,8 @@ DKV_HD inline int sel_partition_pivot(SelItem* a, int first, int last) {
 
 // ---- nth_element / sort / partial_sort ----
 
-DKV_HD inline void sel_nth_element(SelItem* a, int first, int nth, int last) {
+template <class It>
+DKV_HD inline void sel_nth_element(It a, int first, int nth, int last) {
   if (first == last || nth == last) return;
   int depth = 2 * sel_floor_log2(last - first);
   while (last - first > 3) {
@@ -204,12 +217,21 @@ DKV_HD inline void sel_nth_element(SelItem* a, int first, int nth, int last) {
   sel_insertion_sort(a, first, last);
 }
 
-DKV_HD inline void sel_sort(SelItem* a, int first, int last) {
+// Explicit stack for sel_sort's right-hand ranges: it never holds more than
+// 2 floor(log2(n)) + 1 entries (one per depth level).
+constexpr int kSelStack = 64;
+
+// `stack` holds 3 * cap ints (first, last, depth; an int pointer or any type
+// with `stack[j]` -> int& and `stack + j`); cap >= 2 floor(log2(last - first)) + 1.
+template <class It, class St>
+DKV_HD inline void sel_sort(It a, int first, int last, St stack, int cap) {
   if (first == last) return;
   constexpr int kThreshold = 16;
   // Explicit stack replaces the right-hand recursion; the ranges it holds are
   // disjoint, so the processing order does not change the result.
-  int st_first[64], st_last[64], st_depth[64];
+  St st_first = stack;
+  St st_last = stack + cap;
+  St st_depth = stack + 2 * cap;
   int top = 0;
   st_first[0] = first;
   st_last[0] = last;
@@ -241,25 +263,44 @@ DKV_HD inline void sel_sort(SelItem* a, int first, int last) {
   }
 }
 
-DKV_HD inline void sel_partial_sort(SelItem* a, int middle, int last) {
+template <class It>
+DKV_HD inline void sel_partial_sort(It a, int middle, int last) {
   sel_heap_select(a, middle, last);
   sel_sort_heap(a, middle);
 }
 
 // Indices of the `k` best-ranked scores, in torch.topk(sorted=True) order.
-// `work` holds n items of scratch.  Requires 0 < k <= n.
-DKV_HD inline void select_topk(const float* score, int n, int k, SelItem* work, int32_t* out_idx) {
-  for (int j = 0; j < n; ++j) {
-    work[j].v = score[j];
-    work[j].i = j;
-  }
+// `work` holds n items of scratch (a SelItem pointer, or any type with
+// `work[j]` -> SelItem& and `work + j`) and `stack` 3 * kSelStack ints (a
+// caller on the GPU passes LDS, so the kernel needs no private memory).
+// Requires 0 < k <= n.
+// select_topk on a work array the caller has already filled with
+// (score[j], j) for j < n.
+template <class It, class St>
+DKV_HD inline __attribute__((always_inline)) void select_topk_filled(int n, int k, It work, int32_t* out_idx,
+                                                                     St stack, int cap = kSelStack) {
   if ((int64_t)k * 64 <= (int64_t)n) {
     sel_partial_sort(work, k, n);
   } else {
     sel_nth_element(work, 0, k - 1, n);
-    sel_sort(work, 0, k - 1);
+    sel_sort(work, 0, k - 1, stack, cap);
   }
   for (int j = 0; j < k; ++j) out_idx[j] = work[j].i;
+}
+
+template <class It, class St>
+DKV_HD inline __attribute__((always_inline)) void select_topk(const float* score, int n, int k, It work,
+                                                              int32_t* out_idx, St stack, int cap = kSelStack) {
+  for (int j = 0; j < n; ++j) {
+    work[j].v = score[j];
+    work[j].i = j;
+  }
+  select_topk_filled(n, k, work, out_idx, stack, cap);
+}
+
+DKV_HD inline void select_topk(const float* score, int n, int k, SelItem* work, int32_t* out_idx) {
+  int stack[3 * kSelStack];
+  select_topk(score, n, k, work, out_idx, (int*)stack);
 }
 
 }  // namespace dkv

@@ -453,6 +453,7 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_tiled(KeyParams k
   // ---- stage the tile ----
   const uint16_t* src = (const uint16_t*)a.src + b * a.sb + h * a.sh + (int64_t)page * T * a.st;
   const int vecs = D / 8;
+#pragma unroll 8  // lets the loads of several rows issue before their LDS writes
   for (int i = threadIdx.x; i < T * vecs; i += kThreads) {
     const int t = i / vecs, c8 = i % vecs;
     const uint4 w = *(const uint4*)(src + (int64_t)t * a.st + 8 * c8);
@@ -575,25 +576,274 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_tiled(KeyParams k
   }
 }
 
-// Promoted-channel selection for many pages at once: one lane per
-// (batch * head, page) runs the exact top-k on the scores kKeyScores left in
-// the page's low-code region and writes the channel indices.  Each lane's
-// work array lives in its own slice of LDS (the selection is a chain of
-// dependent reads and writes, so LDS latency sets its speed).
-constexpr int kSelectLanes = 64;
-constexpr int kSelectMaxD = 128;
+// Single-pass key page kernel for the common shape: head_dim 128, at most 128
+// tokens per page, one key group per page, 16-bit source with unit channel
+// stride.  One workgroup per (batch * head, page), 256 threads:
+//   1. the page's [T][128] tile is staged in LDS with 16-byte loads;
+//   2. thread (channel c, half h) sums its channel's 16-token chunks of the
+//      half sequentially (and takes min / max); one thread per channel then
+//      adds the chunk sums in ATen's cascade order, so the mean is bit for bit
+//      the serial cascade's (channel_mean);
+//   3. selection: each channel's rank is the number of channels with a larger
+//      score; with all scores distinct, rank < K is the promoted set in
+//      torch.topk(sorted=True) order.  A page with equal (or NaN) scores needs
+//      the exact serial selection (select_topk).  Equal bf16 scores are the
+//      rule, not the exception (32 of 128 means in about one binade), so for
+//      many pages the launcher runs mode kKeyScores (steps 1-2, scores to the
+//      page's low-code region), key_select_pages (one lane per page) and mode
+//      kKeyCodes (steps 1, 4, 5 with the channels read back); mode kKeyAll
+//      does everything here (pages without a data-dependent selection, and the
+//      rank path with the one-lane fallback when few pages are quantized);
+//   4. scales, zero points and one reciprocal per channel;
+//   5. codes: thread (c, quarter) quantizes 32 tokens of channel c with the
+//      exact chain (div_rn) and stores its 8 (2-bit) code bytes directly.
+constexpr int kFastKeyD = 128, kFastKeyT = 128;
 
-__global__ void __launch_bounds__(kSelectLanes) key_select_pages(KeyParams k, int row_bytes) {
-  __shared__ SelItem work_all[kSelectLanes][kSelectMaxD];
+template <int SRC>
+__device__ __forceinline__ float tile_x(const uint16_t* tile, int t, int c) {
+  const uint16_t bits = tile[t * kFastKeyD + c];
+  return SRC == kBF16 ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
+}
+
+// Sum of f(x) over the 16 tokens tb .. tb + 15 of channel c, sequentially
+// (tokens at or past T add an exact zero).  The 16 reads are issued before
+// the first add.  mode 0: |x|; 1: rnd(rnd(x - m)^2); 2: x.  Also folds the
+// tokens into mn / mx when MINMAX (tokens past T repeat the last one, which
+// leaves min and max unchanged).
+template <int SRC, bool MINMAX>
+__device__ __forceinline__ float key_chunk_sum(const uint16_t* tile, int c, int tb, int T, int mode, float m,
+                                               float& mn, float& mx) {
+  float xs[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) xs[j] = tile_x<SRC>(tile, min(tb + j, T - 1), c);
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float x = xs[j];
+    if (MINMAX) {
+      mn = fminf(mn, x);
+      mx = fmaxf(mx, x);
+    }
+    float term = x;
+    if (mode == 0) term = fabsf(x);
+    if (mode == 1) {
+      const float d = src_round<SRC>(x - m);
+      term = src_round<SRC>(d * d);
+    }
+    acc = acc + (tb + j < T ? term : 0.f);
+  }
+  return acc;
+}
+
+// The cascade of channel_mean (level power 4: 16-term chunks, level-1
+// partials summed in order; pages of at most 128 tokens never reach level 2)
+// over the chunk sums csum[k][c], then one division and the rounding to the
+// source dtype.  A short last chunk is the cascade's remainder, added first.
+template <int SRC>
+__device__ __forceinline__ float key_cascade_mean(const float* csum, int c, int T) {
+  const int full = T >> 4;
+  float acc1 = 0.f;
+  for (int k = 0; k < full; ++k) acc1 = acc1 + csum[k * kFastKeyD + c];
+  float acc0 = (T & 15) ? csum[full * kFastKeyD + c] : 0.f;
+  acc0 = acc0 + acc1;
+  acc0 = acc0 + 0.f;  // levels 2 and 3 hold zero
+  acc0 = acc0 + 0.f;
+  return src_round<SRC>(__fdiv_rn(acc0, (float)T));
+}
+
+// BITS: code width of the low codes (2 for mixed keys, else the uniform width).
+template <int SRC, int BITS>
+__global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k, int mode) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[kFastKeyT * kFastKeyD];
+  __shared__ float csum[8 * kFastKeyD];
+  __shared__ float part_mn[2][kFastKeyD], part_mx[2][kFastKeyD];
+  __shared__ __attribute__((aligned(16))) float score[kFastKeyD];
+  __shared__ float ch_mn[kFastKeyD], ch_s[kFastKeyD], ch_y[kFastKeyD];
+  __shared__ int32_t slot[kFastKeyD], sel[kFastKeyD];
+  __shared__ SelItem work[kFastKeyD];
+  __shared__ int sel_stack[3 * kSelStack];
   const dkv_key_pages_args& a = k.a;
-  const int64_t item = (int64_t)blockIdx.x * kSelectLanes + threadIdx.x;
+  const int bh = blockIdx.x, page = blockIdx.y;
+  const int b = bh / (int)a.H, h = bh % (int)a.H;
+  const int T = (int)a.page_tokens, meta = (int)a.meta_dtype;
+  const bool mixed = a.key_mode == DKV_KEY_MIXED;
+  const int K = mixed ? (int)a.promoted : 0;
+  constexpr int row_bytes = kFastKeyT * BITS / 8;  // one group of up to 128 tokens per channel row
+  const int tid = threadIdx.x;
+
+  // ---- 1. stage the tile: every load is issued before the first LDS write
+  // (a loop that stored each load before issuing the next waited one memory
+  // round trip per row group) ----
+  const uint16_t* src = (const uint16_t*)a.src + b * a.sb + h * a.sh + (int64_t)page * T * a.st;
+  {
+    constexpr int kSteps = kFastKeyT * (kFastKeyD / 8) / kThreads;  // 8
+    uint4 w[kSteps];
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+      const int i = tid + j * kThreads, t = min(i >> 4, T - 1), c8 = i & 15;
+      w[j] = *(const uint4*)(src + (int64_t)t * a.st + 8 * c8);
+    }
+    // rows past T hold copies of row T - 1 (reads clamp to T - 1 anyway); an
+    // unconditional store keeps the compiler from sinking each load into a
+    // branch next to its store
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+      const int i = tid + j * kThreads;
+      *(uint4*)(tile + (i >> 4) * kFastKeyD + 8 * (i & 15)) = w[j];
+    }
+  }
+  if (tid < kFastKeyD) slot[tid] = -1;
+  __syncthreads();
+
+  // ---- 2. statistics: thread (channel c, half) covers tokens 64 half .. 64 half + 63 ----
+  const int c = tid & (kFastKeyD - 1), half = tid >> 7;
+  const bool select = mixed && K > 0 && K < kFastKeyD && a.selection != DKV_SELECT_GIVEN && mode != kKeyCodes;
+  const bool magnitude = a.selection == DKV_SELECT_MAGNITUDE;
+  {
+    float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int tb = 64 * half + 16 * q;
+      if (tb < T) {
+        const float sum = key_chunk_sum<SRC, true>(tile, c, tb, T, magnitude ? 0 : 2, 0.f, mn, mx);
+        if (select) csum[(tb >> 4) * kFastKeyD + c] = sum;
+      }
+    }
+    part_mn[half][c] = mn;
+    part_mx[half][c] = mx;
+  }
+  if (select) {
+    __syncthreads();
+    if (half == 0) score[c] = key_cascade_mean<SRC>(csum, c, T);  // magnitude score, or the variance's mean
+    if (!magnitude) {  // variance (mixed.py:158-162): mean squared deviation from that mean
+      __syncthreads();
+      const float m = score[c];
+      float mn = 0.f, mx = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int tb = 64 * half + 16 * q;
+        if (tb < T) csum[(tb >> 4) * kFastKeyD + c] = key_chunk_sum<SRC, false>(tile, c, tb, T, 1, m, mn, mx);
+      }
+      __syncthreads();
+      if (half == 0) score[c] = key_cascade_mean<SRC>(csum, c, T);
+    }
+  }
+  __syncthreads();
+  if (mode == kKeyScores) {
+    if (half == 0) ((float*)(a.low + page * a.low_page_stride + (int64_t)bh * kFastKeyD * row_bytes))[c] = score[c];
+    return;
+  }
+  if (half == 0) {
+    ch_mn[c] = fminf(part_mn[0][c], part_mn[1][c]);
+    ch_s[c] = fmaxf(part_mx[0][c], part_mx[1][c]);  // max for now
+  }
+
+  // ---- 3. channel selection ----
+  if (mixed && K > 0) {
+    if (mode == kKeyCodes && K < kFastKeyD && a.selection != DKV_SELECT_GIVEN) {
+      if (tid < K) sel[tid] = ((const int32_t*)((const char*)a.idx + page * a.idx_page_stride))[(int64_t)bh * K + tid];
+    } else if (select) {
+      bool tie = false;
+      int rank = 0;
+      if (half == 0) {
+        const float v = score[c];
+        tie = v != v;
+#pragma unroll 8
+        for (int j = 0; j < kFastKeyD; j += 4) {
+          const float4 u = *(const float4*)(score + j);
+          rank += (u.x > v) + (u.y > v) + (u.z > v) + (u.w > v);
+          tie |= ((u.x == v) & (j != c)) | ((u.y == v) & (j + 1 != c)) | ((u.z == v) & (j + 2 != c)) |
+                 ((u.w == v) & (j + 3 != c));
+        }
+      }
+      if (__syncthreads_or(tie)) {
+        if (tid == 0) select_topk(score, kFastKeyD, K, work, sel, sel_stack);
+      } else if (half == 0 && rank < K) {
+        sel[rank] = c;
+      }
+    } else if (tid < K) {
+      sel[tid] = (K == kFastKeyD) ? tid : a.given_idx[h * K + tid];
+    }
+    __syncthreads();
+    int32_t* idx_out = (int32_t*)((char*)a.idx + page * a.idx_page_stride) + (int64_t)bh * K;
+    if (tid < K) {
+      const int32_t ch = sel[tid];
+      if (ch >= 0 && ch < kFastKeyD) slot[ch] = tid;
+      idx_out[tid] = ch;
+    }
+  }
+  __syncthreads();
+
+  // ---- 4. scales and zero points (one group per channel) ----
+  if (half == 0) {
+    const float qmax = mixed ? (slot[c] >= 0 ? 15.0f : 3.0f) : (float)((1 << BITS) - 1);
+    const float mn = ch_mn[c];
+    const float s = dev_group_scale(mn, ch_s[c], qmax, SRC);
+    ch_s[c] = s;
+    ch_y[c] = __fdiv_rn(1.0f, s);
+    void* scale = (char*)a.scale + page * a.scale_page_stride;
+    void* zero = (char*)a.zero + page * a.zero_page_stride;
+    dev_store_meta(scale, (int64_t)bh * kFastKeyD + c, s, meta);
+    dev_store_meta(zero, (int64_t)bh * kFastKeyD + c, mn, meta);
+  }
+  __syncthreads();
+
+  // ---- 5. codes: thread (c, half) writes row bytes half * row_bytes / 2 .. ----
+  {
+    constexpr int per_byte = 8 / BITS, tpd = 4 * per_byte;  // tokens per code dword
+    constexpr int bpp = row_bytes / 2;
+    const int sl = slot[c];
+    const float qmax = mixed ? (sl >= 0 ? 15.0f : 3.0f) : (float)((1 << BITS) - 1);
+    const float mn = ch_mn[c], s = ch_s[c], y = ch_y[c];
+    uint8_t* low = a.low + page * a.low_page_stride + (int64_t)bh * kFastKeyD * row_bytes + c * row_bytes + half * bpp;
+    uint8_t* high = mixed && sl >= 0
+                        ? a.high + page * a.high_page_stride + (int64_t)bh * K * row_bytes + sl * row_bytes + half * bpp
+                        : nullptr;
+#pragma unroll 2
+    for (int w = 0; w < bpp; w += 4) {
+      const int tb = (half * bpp + w) * per_byte;
+      float xs[tpd];
+#pragma unroll
+      for (int j = 0; j < tpd; ++j) xs[j] = tile_x<SRC>(tile, min(tb + j, T - 1), c);  // padding repeats the last token
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int j = 0; j < tpd; ++j) {
+        const float diff = src_round<SRC>(xs[j] - mn);
+        const float q = __builtin_rintf(src_round<SRC>(div_rn(diff, s, y)));
+        const uint32_t code = (uint32_t)fminf(fmaxf(q, 0.0f), qmax);
+        lo |= (code & ((1u << BITS) - 1)) << (BITS * j);
+        if (BITS == 2) hi |= (code >> 2) << (2 * j);
+      }
+      *(uint32_t*)(low + w) = lo;
+      if (high) *(uint32_t*)(high + w) = hi;
+    }
+  }
+}
+
+// Promoted-channel selection for many pages at once: one wave per
+// (batch * head, page) runs the exact top-k on the scores kKeyScores left in
+// the page's low-code region and writes the channel indices.  The selection
+// is a serial chain of data-dependent LDS reads and writes; with one page per
+// lane the lanes' different branches serialized inside the wave (C3: 253 us),
+// so lane 0 runs it alone while the wave's lanes only load the scores, and the
+// small LDS footprint lets many such waves run side by side.
+constexpr int kSelectMaxD = 128;
+constexpr int kSelectStack = 16;  // >= 2 floor(log2(kSelectMaxD)) + 1
+
+__global__ void __launch_bounds__(64) key_select_pages(KeyParams k, int row_bytes) {
+  __shared__ SelItem work[kSelectMaxD];
+  __shared__ int stack[3 * kSelectStack];
+  const dkv_key_pages_args& a = k.a;
+  const int64_t item = blockIdx.x;
   const int64_t bhs = a.B * a.H;
-  if (item >= bhs * a.n_pages) return;
   const int64_t page = item / bhs, bh = item % bhs;
   const int D = (int)a.D, K = (int)a.promoted;
   const float* score = (const float*)(a.low + page * a.low_page_stride + bh * D * row_bytes);
+  for (int j = threadIdx.x; j < D; j += 64) work[j] = SelItem{score[j], j};
+  __syncthreads();
+  if (threadIdx.x != 0) return;
   int32_t* idx_out = (int32_t*)((char*)a.idx + page * a.idx_page_stride) + bh * K;
-  select_topk(score, D, K, work_all[threadIdx.x], idx_out);
+  select_topk_filled(D, K, (SelItem*)work, idx_out, (int*)stack, kSelectStack);
 }
 
 __host__ inline size_t key_tiled_smem(int D, int T, int G, int K, int row_bytes) {
@@ -758,6 +1008,44 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
                          ((int64_t)a.D * row_bytes) % 16 == 0 &&
                          (Kp == 0 || (((uintptr_t)a.high % 16) == 0 && (a.high_page_stride % 16) == 0 &&
                                       ((int64_t)Kp * row_bytes) % 16 == 0));
+  // the single-pass kernel: head_dim 128, one group of up to 128 tokens per page
+  const int fast_bits = a.key_mode == DKV_KEY_MIXED ? 2 : (int)a.bits;
+  const bool use_fast = use_tiled && a.D == kFastKeyD && a.page_tokens <= kFastKeyT && a.group >= kFastKeyT &&
+                        a.st % 8 == 0 && row_bytes == kFastKeyT * fast_bits / 8 && ((uintptr_t)a.low % 4) == 0 &&
+                        (a.low_page_stride % 4) == 0 && (Kp == 0 || (((uintptr_t)a.high % 4) == 0 &&
+                                                                       (a.high_page_stride % 4) == 0));
+  if (use_fast) {
+    const dim3 grid((unsigned)(a.B * a.H), (unsigned)a.n_pages);
+    hipStream_t s = (hipStream_t)stream;
+#define DKV_KEYF(T, B, M) hipLaunchKernelGGL((quantize_key_pages_fast<T, B>), grid, dim3(kThreads), 0, s, k, M)
+#define DKV_KEYF_BITS(T, M)                   \
+  do {                                        \
+    if (fast_bits == 2) DKV_KEYF(T, 2, M);    \
+    else if (fast_bits == 4) DKV_KEYF(T, 4, M); \
+    else DKV_KEYF(T, 8, M);                   \
+  } while (0)
+#define DKV_KEYF_RUN(M)                                \
+  do {                                                 \
+    if (a.src_dtype == kBF16) DKV_KEYF_BITS(kBF16, M); \
+    else DKV_KEYF_BITS(kF16, M);                       \
+  } while (0)
+    // a data-dependent selection over more than a few pages: scores, one
+    // lane per page selects, codes
+    const bool select = a.key_mode == DKV_KEY_MIXED && Kp > 0 && Kp < a.D && a.selection != DKV_SELECT_GIVEN;
+    if (select && a.B * a.H * a.n_pages > 256) {
+      DKV_KEYF_RUN(kKeyScores);
+      const int64_t items = a.B * a.H * a.n_pages;
+      DKV_CHECK(items <= 0x7fffffffLL, DKV_ERR_UNSUPPORTED, "too many pages for one launch");
+      hipLaunchKernelGGL(key_select_pages, dim3((unsigned)items), dim3(64), 0, s, k, row_bytes);
+      DKV_KEYF_RUN(kKeyCodes);
+    } else {
+      DKV_KEYF_RUN(kKeyAll);
+    }
+#undef DKV_KEYF_RUN
+#undef DKV_KEYF_BITS
+#undef DKV_KEYF
+    return dkv_check_launch("dkv_quantize_key_pages");
+  }
   if (use_tiled) {
     const dim3 grid((unsigned)(a.B * a.H), (unsigned)a.n_pages);
     hipStream_t s = (hipStream_t)stream;
@@ -766,8 +1054,8 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
       // scores -> one lane per page selects -> codes
       hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyScores);
       const int64_t items = a.B * a.H * a.n_pages;
-      hipLaunchKernelGGL(key_select_pages, dim3((unsigned)((items + kSelectLanes - 1) / kSelectLanes)),
-                         dim3(kSelectLanes), 0, s, k, row_bytes);
+      DKV_CHECK(items <= 0x7fffffffLL, DKV_ERR_UNSUPPORTED, "too many pages for one launch");
+      hipLaunchKernelGGL(key_select_pages, dim3((unsigned)items), dim3(64), 0, s, k, row_bytes);
       hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyCodes);
     } else {
       hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyAll);
