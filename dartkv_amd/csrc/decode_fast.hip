@@ -68,7 +68,8 @@ __host__ __device__ inline LdsMap lds_map(int np, int gv) {
   m.ks = o; o += 256;                      // key scale  [128] fp16
   m.kz = o; o += 256;                      // key zero   [128] fp16
   m.klut = o; o += 1024;                   // 2-bit key tables [128 ch][LO, HI] (zero for promoted channels)
-  m.klut16 = o; o += np * 32;              // 4-bit key tables [NP][LO 16 B, HI 16 B]
+  o = (o + 255) / 256 * 256;               // (the 4-bit tables are addressed by byte: 256-aligned)
+  m.klut16 = o; o += np * 32;              // 4-bit key tables [NP][16] fp16
   m.pidx = o; o += 64;                     // promoted channels [NP] uint8 (a copy: ki is refilled early)
   m.q16 = o; o += 1024;                    // query [4][128 ch] fp16
   // A-operand sources; row strides put the rows one read touches in distinct
@@ -83,7 +84,7 @@ __host__ __device__ inline LdsMap lds_map(int np, int gv) {
   m.vs = o; o += 256 * gv;                 // value scale [128 tok][Gv] fp16
   m.vz = o; o += 256 * gv;                 // value zero  [128 tok][Gv] fp16
   m.vlut = o; o += kVlutStride * gv;       // value tables [Gv][128 tok][LO, HI], padded rows
-  m.bytes = (o + 15) / 16 * 16;
+  m.bytes = (o + 255) / 256 * 256;         // keeps every wave's region 256-aligned
   return m;
 }
 
@@ -118,20 +119,23 @@ __device__ __forceinline__ half4 lookup4(uint32_t e, uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(half4, make_uint2(perm(h4, l4, 0x05010400u), perm(h4, l4, 0x07030602u)));
 }
 
-// B operand from 4-bit codes: el = low 2 bits per byte (values 0..3); wh =
-// the high-code dword, whose bits 8j + sh and 8j + sh + 1 are the high 2 bits
-// of byte j's entry; r2 = (sh - 2) & 31 and r1 = (sh - 1) & 31 rotate those
-// two bits to bit 2 of each byte.  L / H = low / high bytes of table entries
-// 0..15 (entry = low + 4 * high): the selector picks within an 8-entry half,
-// the blend takes the upper half's byte where the top bit is set.
-// m4 = 0x04040404 in a scalar register, ident = 0x03020100 in a vector register.
-__device__ __forceinline__ half4 lookup16(uint32_t el, uint32_t wh, uint32_t r2, uint32_t r1, const uint4& L,
-                                          const uint4& H, uint32_t m4, uint32_t ident) {
-  const uint32_t sel = (__builtin_amdgcn_alignbit(wh, wh, r2) & m4) | el;
-  const uint32_t blend = (__builtin_amdgcn_alignbit(wh, wh, r1) & m4) | ident;
-  const uint32_t l4 = perm(perm(L.w, L.z, sel), perm(L.y, L.x, sel), blend);
-  const uint32_t h4 = perm(perm(H.w, H.z, sel), perm(H.y, H.x, sel), blend);
-  return __builtin_bit_cast(half4, make_uint2(perm(h4, l4, 0x05010400u), perm(h4, l4, 0x07030602u)));
+// B operand from 4-bit codes by LDS gathers: wl / wh = the low / high code
+// dwords (bits 8j + sh, 8j + sh + 1 of byte j hold the lane's token of byte
+// j); rl = (sh - 1) & 31 and rh = (sh - 3) & 31 rotate them to 2 x low and
+// 8 x high, so byte j of sel = 2 code_j + 32 kq (kq32 = 32 kq in every byte)
+// is the byte offset of the entry in the lane's table (slot 4 pb + kq).  tab
+// is the LDS address of the block's tables with its low byte zero, so a byte
+// permute forms each element's address.  m6 = 0x06060606 and m18 = 0x18181818
+// in scalar registers.
+__device__ __forceinline__ half4 gather16(uint32_t wl, uint32_t wh, uint32_t rl, uint32_t rh, uint32_t kq32,
+                                          uint32_t tab, int off, uint32_t m6, uint32_t m18) {
+  typedef __attribute__((address_space(3))) const _Float16 lds_half;
+  const uint32_t x = (__builtin_amdgcn_alignbit(wl, wl, rl) & m6) | kq32;
+  const uint32_t sel = (__builtin_amdgcn_alignbit(wh, wh, rh) & m18) | x;
+  half4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r[j] = ((lds_half*)(uintptr_t)perm(tab, sel, 0x07060500u | j))[off / 2];
+  return r;
 }
 
 // Page data in three groups, each issued as soon as the previous page no
@@ -159,7 +163,7 @@ __host__ __device__ inline int n_small_loads(int np, int gv) {
 __host__ __device__ inline int n_key_loads(int np) { return 4 + (np * 32 + 1023) / 1024; }
 
 // 4-bit key tables of the NP promoted slots: lanes (2j, 2j+1) build entries
-// 0..7 / 8..15 of slot j (byte planes: low bytes at +0, high bytes at +16).
+// 0..7 / 8..15 of slot j (16 fp16 entries per slot).
 template <bool BF16, int NP>
 __device__ __forceinline__ void build_lut16_tables(const LdsMap& M, uint8_t* lds, const uint16_t* ks,
                                                    const uint16_t* kz, int lane) {
@@ -178,9 +182,7 @@ __device__ __forceinline__ void build_lut16_tables(const LdsMap& M, uint8_t* lds
       const uint32_t e3 = half ? 0x4b804b00u : 0x47004600u;  // (14, 15) | (6, 7)
       const uint32_t v0 = lut_pair<BF16>(e0, s2, z2), v1 = lut_pair<BF16>(e1, s2, z2);
       const uint32_t v2 = lut_pair<BF16>(e2, s2, z2), v3 = lut_pair<BF16>(e3, s2, z2);
-      uint8_t* t16 = lds + M.klut16 + 32 * j + 8 * half;
-      *(uint2*)t16 = make_uint2(perm(v1, v0, 0x06040200u), perm(v3, v2, 0x06040200u));
-      *(uint2*)(t16 + 16) = make_uint2(perm(v1, v0, 0x07050301u), perm(v3, v2, 0x07050301u));
+      *(uint4*)(lds + M.klut16 + 32 * j + 16 * half) = make_uint4(v0, v1, v2, v3);
     }
   }
 }
@@ -193,11 +195,11 @@ __device__ __forceinline__ void build_lut16_tables(const LdsMap& M, uint8_t* lds
 // scalar register, sel2 = 0x04000400 in a vector register.  All eight B
 // operands are formed before the MFMAs issue, so no MFMA waits on the VALU
 // result it reads.
-__device__ __forceinline__ void mma_lut_block(half4 a, const uint32_t x[4], const uint32_t lo[4], const uint32_t hi[4],
-                                              float4v acc[8], uint32_t m3, uint32_t sel2) {
+// wk[j]: the B operand of channel tile j (j < 8).
+__device__ __forceinline__ void lut_block_operands(const uint32_t x[4], const uint32_t lo[4], const uint32_t hi[4],
+                                                   uint2 wk[8], uint32_t m3, uint32_t sel2) {
   const uint32_t y0 = perm(x[1], x[0], 0x05010400u);
   const uint32_t y1 = perm(x[3], x[2], 0x05010400u);
-  uint2 wk[4], wk4[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const uint32_t e0 = ((y0 >> (2 * k)) & m3) | sel2;
@@ -205,13 +207,19 @@ __device__ __forceinline__ void mma_lut_block(half4 a, const uint32_t x[4], cons
     const uint32_t lp0 = perm(lo[1], lo[0], e0), hp0 = perm(hi[1], hi[0], e0);
     const uint32_t lp1 = perm(lo[3], lo[2], e1), hp1 = perm(hi[3], hi[2], e1);
     wk[k] = make_uint2(perm(hp0, lp0, 0x05010400u), perm(hp1, lp1, 0x05010400u));
-    wk4[k] = make_uint2(perm(hp0, lp0, 0x07030602u), perm(hp1, lp1, 0x07030602u));
+    wk[k + 4] = make_uint2(perm(hp0, lp0, 0x07030602u), perm(hp1, lp1, 0x07030602u));
   }
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    acc[k] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, __builtin_bit_cast(half4, wk[k]), acc[k], 0, 0, 0);
-    acc[k + 4] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, __builtin_bit_cast(half4, wk4[k]), acc[k + 4], 0, 0, 0);
-  }
+}
+
+// Two K = 16 blocks in one v_mfma_f32_16x16x32_f16: lane (n, kq) holds K
+// indices 8 kq .. 8 kq + 7, so concatenating each lane's operands of blocks
+// u and v gives K index 8 kq + i = block u's 4 kq + i for i < 4 and block v's
+// 4 kq + i - 4 otherwise; the product is the sum of the two blocks' products.
+__device__ __forceinline__ half8 cat8(half4 u, half4 v) {
+  return __builtin_shufflevector(u, v, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ float4v mma2(half4 a0, half4 a1, half4 b0, half4 b1, float4v acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(cat8(a0, a1), cat8(b0, b1), acc, 0, 0, 0);
 }
 
 // GQ: query heads per KV head; NP: promoted channels (16, 32, 48 or 64);
@@ -298,8 +306,12 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     issue_values(M, lds, a0, lane);
   }
   const float c2 = p.scale * kLog2e;
-  const uint32_t m3 = in_sgpr(0x03030303u), m4 = in_sgpr(0x04040404u);
-  const uint32_t sel2 = in_vgpr(0x04000400u), ident = in_vgpr(0x03020100u);
+  const uint32_t m3 = in_sgpr(0x03030303u);
+  const uint32_t sel2 = in_vgpr(0x04000400u);
+  // LDS address of the 4-bit tables; its low byte is zero (the map and every
+  // wave's region are 256-aligned and the dynamic LDS starts at 0).  Were it
+  // not, the split's records are poisoned (NaN) rather than wrong.
+  const uint32_t tab16 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.klut16));
 
 #pragma unroll 1
   for (int pg = page0; pg < page1; ++pg) {
@@ -350,13 +362,19 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
       };
 #pragma unroll
       for (int c = 0; c < kAhead; ++c) load_cb(c);
+      half4 pend0, pend1;  // even block's B operands, waiting for the odd one
 #pragma unroll
       for (int cb = 0; cb < kD / 4; ++cb) {
         if (cb + kAhead < kD / 4) load_cb(cb + kAhead);
-        S[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], lookup4((w0[cb] >> sh) & 0x03030303u, t[cb].x, t[cb].y),
-                                                     S[0], 0, 0, 0);
-        S[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], lookup4((w1[cb] >> sh) & 0x03030303u, t[cb].x, t[cb].y),
-                                                     S[1], 0, 0, 0);
+        const half4 b0 = lookup4((w0[cb] >> sh) & 0x03030303u, t[cb].x, t[cb].y);
+        const half4 b1 = lookup4((w1[cb] >> sh) & 0x03030303u, t[cb].x, t[cb].y);
+        if (cb & 1) {  // blocks cb - 1 and cb in one K = 32 MFMA per tile
+          S[0] = mma2(qa[cb - 1], qa[cb], pend0, b0, S[0]);
+          S[1] = mma2(qa[cb - 1], qa[cb], pend1, b1, S[1]);
+        } else {
+          pend0 = b0;
+          pend1 = b1;
+        }
         if (cb % 4 == 1 && cb / 4 < 4) {
           // value table k = cb / 4 of this lane: token lane + 64 (k & 1), group k >> 1
           // (groups beyond gv rebuild an existing table with identical contents)
@@ -388,9 +406,10 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     // promoted channels: 4-bit codes, slot j = 4pb + kq of the high codes;
     // block pb + 1's codes and tables are read before block pb is computed
     {
-      const uint32_t r2 = (uint32_t)(sh - 2) & 31u, r1 = (uint32_t)(sh - 1) & 31u;
+      const uint32_t rl = (uint32_t)(sh - 1) & 31u, rh = (uint32_t)(sh - 3) & 31u;
+      const uint32_t kq32 = 0x20202020u * (uint32_t)kq;
+      const uint32_t m6 = in_sgpr(0x06060606u), m18 = in_sgpr(0x18181818u);
       uint32_t wl0[np / 4], wl1[np / 4], wh0[np / 4], wh1[np / 4];
-      uint4 L[np / 4], H[np / 4];
       auto load_pb = [&](int pb) {
         const int j = 4 * pb + kq;
         const int row = M.kl + 32 * pidx[j] + qd;
@@ -399,18 +418,23 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
         const int hrow = M.kh + 32 * j + qd;
         wh0[pb] = lds_u32(lds, hrow);
         wh1[pb] = lds_u32(lds, hrow + 16);
-        L[pb] = *(const uint4*)(lds + M.klut16 + 32 * j);
-        H[pb] = *(const uint4*)(lds + M.klut16 + 32 * j + 16);
       };
       load_pb(0);
+      half4 pa, pend0, pend1;  // even block's operands, waiting for the odd one (np / 4 is even)
 #pragma unroll
       for (int pb = 0; pb < np / 4; ++pb) {
         if (pb + 1 < np / 4) load_pb(pb + 1);
         const half4 a = load_a(lds, aq, 8 * pb);
-        S[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(
-            a, lookup16((wl0[pb] >> sh) & 0x03030303u, wh0[pb], r2, r1, L[pb], H[pb], m4, ident), S[0], 0, 0, 0);
-        S[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(
-            a, lookup16((wl1[pb] >> sh) & 0x03030303u, wh1[pb], r2, r1, L[pb], H[pb], m4, ident), S[1], 0, 0, 0);
+        const half4 b0 = gather16(wl0[pb], wh0[pb], rl, rh, kq32, tab16, 128 * pb, m6, m18);
+        const half4 b1 = gather16(wl1[pb], wh1[pb], rl, rh, kq32, tab16, 128 * pb, m6, m18);
+        if (pb & 1) {
+          S[0] = mma2(pa, a, pend0, b0, S[0]);
+          S[1] = mma2(pa, a, pend1, b1, S[1]);
+        } else {
+          pa = a;
+          pend0 = b0;
+          pend1 = b1;
+        }
       }
     }
     lds_sync();
@@ -474,10 +498,21 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
         }
       };
       load_blk(0);
+      uint2 wprev[8];  // even block's B operands, waiting for the odd one
 #pragma unroll
       for (int blk = 0; blk < kPage / 16; ++blk) {
         if (blk + 1 < kPage / 16) load_blk(blk + 1);
-        mma_lut_block(a[blk], x[blk], lo[blk], hi[blk], O, m3, sel2);
+        uint2 wk[8];
+        lut_block_operands(x[blk], lo[blk], hi[blk], wk, m3, sel2);
+        if (blk & 1) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            O[j] = mma2(a[blk - 1], a[blk], __builtin_bit_cast(half4, wprev[j]), __builtin_bit_cast(half4, wk[j]),
+                        O[j]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) wprev[j] = wk[j];
+        }
       }
     }
     lds_sync();
@@ -491,7 +526,7 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     const int hq = kvh * GQ + i;
     float* rec = p.ws + (((int64_t)b * p.Hq + hq) * p.split_stride + split) * (kD + 2);
     if (lane == 0) {
-      rec[0] = m_run[i] * kLn2;
+      rec[0] = (tab16 & 255u) == 0 ? m_run[i] * kLn2 : NAN;
       rec[1] = l;
     }
     if (kq == 0) {
