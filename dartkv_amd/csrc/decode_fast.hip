@@ -18,7 +18,8 @@
 //      (low bytes of the entries in one dword, high bytes in another);
 //   3. orders channels so the NP promoted channels come first (the query is
 //      permuted the same way);
-//   4. computes S = Q K and O += P V with v_mfma_f32_16x16x16f16 in a "slot"
+//   4. computes S = Q K and O += P V with f16 MFMAs (16x16, K = 32: two
+//      16-deep blocks per instruction) in a "slot"
 //      layout: the 16 rows of a tile are 4 slots x 4 query heads.  For Q K the
 //      16 K values of one MFMA are 4 channels x 4 slots and a slot picks one
 //      of 4 tokens, so the B values a lane holds are 4 tokens of ONE channel
@@ -211,16 +212,6 @@ __device__ __forceinline__ void lut_block_operands(const uint32_t x[4], const ui
   }
 }
 
-// Two K = 16 blocks in one v_mfma_f32_16x16x32_f16: lane (n, kq) holds K
-// indices 8 kq .. 8 kq + 7, so concatenating each lane's operands of blocks
-// u and v gives K index 8 kq + i = block u's 4 kq + i for i < 4 and block v's
-// 4 kq + i - 4 otherwise; the product is the sum of the two blocks' products.
-__device__ __forceinline__ half8 cat8(half4 u, half4 v) {
-  return __builtin_shufflevector(u, v, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-__device__ __forceinline__ float4v mma2(half4 a0, half4 a1, half4 b0, half4 b1, float4v acc) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(cat8(a0, a1), cat8(b0, b1), acc, 0, 0, 0);
-}
 
 // GQ: query heads per KV head; NP: promoted channels (16, 32, 48 or 64);
 // BF16: cache dtype bf16 (else fp16).  All compile-time, so every block loop

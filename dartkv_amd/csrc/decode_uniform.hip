@@ -10,7 +10,7 @@
 // page's key codes (every channel) and key scales once, when the page starts
 // (for 8-bit keys, whose LDS would double, each half stages its own half of
 // every key row), and each half's value rows and scales; then per half page
-//   * S = Q K with v_mfma_f32_16x16x16f16 in the slot layout (rows = 4 slots x
+//   * S = Q K with MFMAs in the slot layout (rows = 4 slots x
 //     4 query heads; a lane's four B values are four tokens of one channel,
 //     A carries the query at the lane's slot); one tile covers the 64 tokens;
 //   * an online softmax in base 2 (running max moves only beyond 8);
@@ -248,11 +248,14 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
       };
 #pragma unroll
       for (int c = 0; c < kAhead; ++c) load_cb(c);
+      half4 pend;  // even block's B operand, waiting for the odd one
 #pragma unroll
       for (int cb = 0; cb < kD / 4; ++cb) {
         if (cb + kAhead < kD / 4) load_cb(cb + kAhead);
         const uint32_t e = (w[cb] >> kshift) & kmask;
-        S = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[cb], dequant4<KB, BF16>(e, sz[cb]), S, 0, 0, 0);
+        const half4 b = dequant4<KB, BF16>(e, sz[cb]);
+        if (cb & 1) S = mma2(qa[cb - 1], qa[cb], pend, b, S);  // blocks cb - 1, cb in one K = 32 MFMA
+        else pend = b;
       }
     }
     lds_sync();
@@ -306,13 +309,19 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
         sz1[tg] = *(const uint2*)(lds + M.vt + 8 * (t * gv + vg1));
       };
       load_tg(0);
+      half4 p0, p1;  // even group's B operands, waiting for the odd one
 #pragma unroll
       for (int tg = 0; tg < kHalfTok / 4; ++tg) {
         if (tg + 1 < kHalfTok / 4) load_tg(tg + 1);
         const half4 b0 = dequant4<VB, BF16>((w0[tg] >> vshift) & vmask, sz0[tg]);
         const half4 b1 = dequant4<VB, BF16>((w1[tg] >> vshift) & vmask, sz1[tg]);
-        O[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[tg], b0, O[0], 0, 0, 0);
-        O[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[tg], b1, O[1], 0, 0, 0);
+        if (tg & 1) {  // token groups tg - 1, tg in one K = 32 MFMA per tile
+          O[0] = mma2(a[tg - 1], a[tg], p0, b0, O[0]);
+          O[1] = mma2(a[tg - 1], a[tg], p1, b1, O[1]);
+        } else {
+          p0 = b0;
+          p1 = b1;
+        }
       }
     }
     lds_sync();

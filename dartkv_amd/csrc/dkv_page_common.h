@@ -99,6 +99,17 @@ __device__ __forceinline__ PageAddr page_addr(const_segment& s, int64_t bh) {
   return p;
 }
 
+// Two K = 16 blocks in one v_mfma_f32_16x16x32_f16: lane (n, kq) holds K
+// indices 8 kq .. 8 kq + 7, so concatenating each lane's operands of blocks
+// u and v gives K index 8 kq + i = block u's 4 kq + i for i < 4 and block v's
+// 4 kq + i - 4 otherwise; the product is the sum of the two blocks' products.
+__device__ __forceinline__ half8 cat8(half4 u, half4 v) {
+  return __builtin_shufflevector(u, v, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ float4v mma2(half4 a0, half4 a1, half4 b0, half4 b1, float4v acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(cat8(a0, a1), cat8(b0, b1), acc, 0, 0, 0);
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Copy `bytes` (a multiple of 16) from global `src` to LDS `dst` with
