@@ -28,6 +28,104 @@ from .quantization import QuantizedTensor
 
 Segment = Union[torch.Tensor, QuantizedTensor, MixedQuantizedKey]
 
+
+class _PageRun:
+    """Pages quantized by one launch: each field is one tensor with a page
+    dimension (`dim`; page p is `size` entries of it starting at p * size,
+    and dim 0 is dropped from the page's view), plus the fields every page
+    shares.  A prefill of 127 pages would otherwise create about a thousand
+    tensor views in Python before the first page is read."""
+
+    __slots__ = ("tensors", "dim", "size", "shared")
+
+    def __init__(self, tensors: dict, dim: int, size: int, shared: dict) -> None:
+        self.tensors, self.dim, self.size, self.shared = tensors, dim, size, shared
+
+    def view(self, name: str, page: int) -> torch.Tensor:
+        t = self.tensors[name]
+        return t[page] if self.dim == 0 else t.narrow(self.dim, page * self.size, self.size)
+
+    def block(self, name: str, page: int) -> Optional[Tuple[int, int]]:
+        """(address, (batch, head) stride) of the page's block as _bh_block gives it, or None when
+        _bh_block would need a copy (then the caller materializes the view)."""
+        t = self.tensors[name]
+        if t.numel() == 0:
+            return 0, 0
+        strides, shape = t.stride(), t.shape
+        if self.dim == 0:
+            strides, shape = strides[1:], shape[1:]
+        else:
+            shape = shape[:self.dim] + (self.size,) + shape[self.dim + 1:]
+        B, H = shape[0], shape[1]
+        inner = 1
+        for size, stride in zip(reversed(shape[2:]), reversed(strides[2:])):
+            if size != 1 and stride != inner:
+                return None
+            inner *= size
+        if H > 1:
+            bh = strides[1]
+            if not (B == 1 or strides[0] == H * bh):
+                return None
+        else:
+            bh = strides[0] if B > 1 else inner
+        offset = page * (t.stride(0) if self.dim == 0 else self.size * t.stride(self.dim))
+        return t.data_ptr() + offset * t.element_size(), bh
+
+
+class _RunField:
+    """A segment field read from the segment's page run: a tensor field becomes the page's view
+    on first access (then cached in the instance), a shared field is the run's value."""
+
+    def __init__(self, name: str, tensor: bool) -> None:
+        self.name, self.tensor = name, tensor
+
+    def __get__(self, obj, cls=None):
+        if obj is None:
+            return self
+        if not self.tensor:
+            return obj._run.shared[self.name]
+        v = obj._run.view(self.name, obj._page)
+        obj.__dict__[self.name] = v
+        return v
+
+
+class _PagedMixedKey(MixedQuantizedKey):
+    """One page of a `_PageRun` of mixed keys; behaves as a MixedQuantizedKey."""
+
+    low_values = _RunField("low_values", True)
+    high_values = _RunField("high_values", True)
+    channel_indices = _RunField("channel_indices", True)
+    scale = _RunField("scale", True)
+    zero_point = _RunField("zero_point", True)
+    original_shape = _RunField("original_shape", False)
+    padded_tokens = _RunField("padded_tokens", False)
+    group_size = _RunField("group_size", False)
+    low_bits = _RunField("low_bits", False)
+    promote_bits = _RunField("promote_bits", False)
+    output_dtype = _RunField("output_dtype", False)
+
+    def __init__(self, run: _PageRun, page: int) -> None:  # pylint: disable=super-init-not-called
+        self._run, self._page = run, page
+
+
+class _PagedQuantized(QuantizedTensor):
+    """One page of a `_PageRun` of uniform codes; behaves as a QuantizedTensor."""
+
+    values = _RunField("values", True)
+    scale = _RunField("scale", True)
+    zero_point = _RunField("zero_point", True)
+    original_shape = _RunField("original_shape", False)
+    original_dim = _RunField("original_dim", False)
+    padded_dim = _RunField("padded_dim", False)
+    packed_dim = _RunField("packed_dim", False)
+    group_size = _RunField("group_size", False)
+    bits = _RunField("bits", False)
+    output_dtype = _RunField("output_dtype", False)
+    axis = _RunField("axis", False)
+
+    def __init__(self, run: _PageRun, page: int) -> None:  # pylint: disable=super-init-not-called
+        self._run, self._page = run, page
+
 if TYPE_CHECKING:
     from .page_table import DartPageRun, DartPageTable
 
@@ -560,13 +658,10 @@ class DartKVCache:
                                  group=kg, promoted=K, selection=selection,
                                  given_idx=None if given is None else given[0].contiguous(), meta=meta,
                                  low=low, high=high, idx=idx, scale=scale, zero=zero)
-            # per-page views from one unbind each (indexing page by page costs a
-            # Python-level tensor view per field per page)
-            return [MixedQuantizedKey(low_values=lo, high_values=hi, channel_indices=ix, scale=sc, zero_point=ze,
-                                      original_shape=(B, H, tokens, D), padded_tokens=G * kg, group_size=kg,
-                                      low_bits=2, promote_bits=c.promote_bits, output_dtype=src.dtype)
-                    for lo, hi, ix, sc, ze in zip(low.unbind(0), high.unbind(0), idx.unbind(0), scale.unbind(0),
-                                                  zero.unbind(0))]
+            run = _PageRun(dict(low_values=low, high_values=high, channel_indices=idx, scale=scale, zero_point=zero),
+                           0, 1, dict(original_shape=(B, H, tokens, D), padded_tokens=G * kg, group_size=kg,
+                                      low_bits=2, promote_bits=c.promote_bits, output_dtype=src.dtype))
+            return [_PagedMixedKey(run, p) for p in range(n_pages)]
         bits = c.resolved_key_bits
         per = 8 // bits
         padded = G * kg
@@ -577,10 +672,10 @@ class DartKVCache:
         launch_key_pages(src, page_tokens=tokens, n_pages=n_pages, key_mode=_lib.KEY_UNIFORM, bits=bits, group=kg,
                          promoted=0, selection=0, given_idx=None, meta=meta, low=values, high=None, idx=None,
                          scale=scale, zero=zero)
-        return [QuantizedTensor(values=va, scale=sc, zero_point=ze, original_shape=(B, H, tokens, D),
-                                original_dim=tokens, padded_dim=padded, packed_dim=packed_dim, group_size=kg,
-                                bits=bits, output_dtype=src.dtype, axis=2)
-                for va, sc, ze in zip(values.unbind(0), scale.unbind(0), zero.unbind(0))]
+        run = _PageRun(dict(values=values, scale=scale, zero_point=zero), 0, 1,
+                       dict(original_shape=(B, H, tokens, D), original_dim=tokens, padded_dim=padded,
+                            packed_dim=packed_dim, group_size=kg, bits=bits, output_dtype=src.dtype, axis=2))
+        return [_PagedQuantized(run, p) for p in range(n_pages)]
 
     def _quantize_value_chunks(self, value_states: torch.Tensor, chunk: int) -> List[QuantizedTensor]:
         """Value segments of ``chunk`` tokens (last may be shorter) quantized along head_dim.
@@ -607,10 +702,11 @@ class DartKVCache:
             scale = torch.empty(B, H, n, Gv, dtype=meta, device=dev)
             zero = torch.empty(B, H, n, Gv, dtype=meta, device=dev)
             _launch_value_rows(src, bits, vg, meta, values, scale, zero)
-            out.extend(QuantizedTensor(values=va, scale=sc, zero_point=ze, original_shape=(B, H, size, D),
-                                       original_dim=D, padded_dim=padded, packed_dim=packed_dim, group_size=vg,
-                                       bits=bits, output_dtype=value_states.dtype, axis=3)
-                       for va, sc, ze in zip(values.split(size, 2), scale.split(size, 2), zero.split(size, 2)))
+            run = _PageRun(dict(values=values, scale=scale, zero_point=zero), 2, size,
+                           dict(original_shape=(B, H, size, D), original_dim=D, padded_dim=padded,
+                                packed_dim=packed_dim, group_size=vg, bits=bits, output_dtype=value_states.dtype,
+                                axis=3))
+            out.extend(_PagedQuantized(run, i) for i in range(count))
         return out
 
     def _append_quantized_value_page(self, segment: QuantizedTensor) -> None:
@@ -870,6 +966,20 @@ def _bh_block(t: torch.Tensor, keepalive: list) -> Tuple[int, int]:
     return c.data_ptr(), inner
 
 
+def _field_block(seg, name: str, keepalive: list) -> Tuple[int, int]:
+    """_bh_block of a segment field; a page of a run that has not materialized the field is read
+    from the run's tensor directly (no view); empty fields give (0, 0)."""
+    run = getattr(seg, "_run", None)
+    if run is not None and name not in seg.__dict__:
+        blk = run.block(name, seg._page)
+        if blk is not None:
+            return blk
+    t = getattr(seg, name)
+    if t.numel() == 0:
+        return 0, 0
+    return _bh_block(t, keepalive)
+
+
 def fill_segment(desc, kseg: Segment, vseg: Segment, keepalive: list) -> None:
     """Fill one dkv_segment descriptor from a (key, value) segment pair."""
     keepalive.append((kseg, vseg))
@@ -881,20 +991,17 @@ def fill_segment(desc, kseg: Segment, vseg: Segment, keepalive: list) -> None:
         desc.key_kind = _lib.KEY_MIXED
         desc.key_group = kseg.group_size
         desc.promoted = kseg.promoted_channels
-        for i, t in enumerate((kseg.low_values, kseg.high_values, kseg.channel_indices, kseg.scale, kseg.zero_point)):
-            if t.numel() == 0:
-                desc.key[i], desc.key_bh[i] = 0, 0
-            else:
-                desc.key[i], desc.key_bh[i] = _bh_block(t, keepalive)
+        for i, name in enumerate(("low_values", "high_values", "channel_indices", "scale", "zero_point")):
+            desc.key[i], desc.key_bh[i] = _field_block(kseg, name, keepalive)
     else:
         if kseg.axis != 2:
             raise ValueError("key pages must be quantized along the token axis")
         desc.key_kind = _lib.KEY_UNIFORM
         desc.key_bits = kseg.bits
         desc.key_group = kseg.group_size
-        desc.key[0], desc.key_bh[0] = _bh_block(kseg.values, keepalive)
-        desc.key[3], desc.key_bh[3] = _bh_block(kseg.scale, keepalive)
-        desc.key[4], desc.key_bh[4] = _bh_block(kseg.zero_point, keepalive)
+        desc.key[0], desc.key_bh[0] = _field_block(kseg, "values", keepalive)
+        desc.key[3], desc.key_bh[3] = _field_block(kseg, "scale", keepalive)
+        desc.key[4], desc.key_bh[4] = _field_block(kseg, "zero_point", keepalive)
     if isinstance(vseg, torch.Tensor):
         desc.value_kind = _lib.VALUE_DENSE
         desc.value[0], desc.value_bh[0] = _dense_block(vseg, keepalive)
@@ -904,9 +1011,9 @@ def fill_segment(desc, kseg: Segment, vseg: Segment, keepalive: list) -> None:
         desc.value_kind = _lib.VALUE_UNIFORM
         desc.value_bits = vseg.bits
         desc.value_group = vseg.group_size
-        desc.value[0], desc.value_bh[0] = _bh_block(vseg.values, keepalive)
-        desc.value[1], desc.value_bh[1] = _bh_block(vseg.scale, keepalive)
-        desc.value[2], desc.value_bh[2] = _bh_block(vseg.zero_point, keepalive)
+        desc.value[0], desc.value_bh[0] = _field_block(vseg, "values", keepalive)
+        desc.value[1], desc.value_bh[1] = _field_block(vseg, "scale", keepalive)
+        desc.value[2], desc.value_bh[2] = _field_block(vseg, "zero_point", keepalive)
 
 
 def _dense_block(t: torch.Tensor, keepalive: list) -> Tuple[int, int]:
