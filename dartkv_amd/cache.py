@@ -7,8 +7,9 @@ page merging and union-boundary segment iteration.  What differs is where
 the work happens:
 
 * every page of one append is quantized by one ``dkv_quantize_key_pages``
-  launch (keys along tokens) and one ``dkv_quantize_rows`` launch (values
-  along head_dim); page fields are views into page-major chunk tensors;
+  launch (keys along tokens) and one ``dkv_quantize_row_blocks`` launch
+  (values along head_dim, read in place from the appended tensor's token
+  slice); page fields are views into page-major chunk tensors;
 * the held partial page lives in a preallocated tail buffer, so a one-token
   decode append is a single device copy with no concatenation;
 * the decode kernel reads a device table of segment descriptors that is
@@ -861,16 +862,30 @@ class DartKVCache:
 
 def _launch_value_rows(src: torch.Tensor, bits: int, group: int, meta: torch.dtype, values: torch.Tensor,
                        scale: torch.Tensor, zero: torch.Tensor) -> None:
-    """Quantize [B,H,T,D] value rows along head_dim straight from strided storage."""
+    """Quantize [B,H,T,D] value rows along head_dim straight from strided storage.
+
+    A token slice of a [B,H,T',D] tensor is B*H blocks of T contiguous rows;
+    the kernel reads it in place.  Other layouts are copied first.
+    """
     B, H, T, D = src.shape
-    if not src.is_contiguous():
+    sb, sh, st, sd = src.stride()
+    row_stride = st if T > 1 else D
+    if sd != 1 or row_stride != D:
+        blocks = None
+    elif H == 1:
+        blocks, block_stride = B, sb
+    elif B == 1 or sb == H * sh:
+        blocks, block_stride = B * H, sh
+    else:
+        blocks = None
+    if blocks is None:
         src = src.contiguous()
-    rows = B * H * T
+        blocks, block_stride = B * H, T * D
     lib = _lib.load()
-    rc = lib.dkv_quantize_rows(src.data_ptr(), _lib.dtype_code(src.dtype), rows, D, D, 1, bits, group,
-                               values.data_ptr(), scale.data_ptr(), zero.data_ptr(), _lib.dtype_code(meta),
-                               _lib.stream_ptr(src.device))
-    _lib.check(rc, "dkv_quantize_rows")
+    rc = lib.dkv_quantize_row_blocks(src.data_ptr(), _lib.dtype_code(src.dtype), blocks, block_stride, T, D, D, bits,
+                                     group, values.data_ptr(), scale.data_ptr(), zero.data_ptr(),
+                                     _lib.dtype_code(meta), _lib.stream_ptr(src.device))
+    _lib.check(rc, "dkv_quantize_row_blocks")
 
 
 def _materialize(segment: Segment) -> torch.Tensor:

@@ -29,6 +29,9 @@ constexpr int kThreads = 256;
 struct RowsParams {
   const void* src;
   int64_t rows, n, row_stride, elem_stride;
+  // rows come in blocks of block_rows: row r = blk * block_rows + i starts at
+  // blk * block_stride + i * row_stride (one block: block_rows = rows)
+  int64_t blocks, block_rows, block_stride;
   int64_t group, groups, packed_bytes;
   int bits, per_byte, src_dtype, meta_dtype;
   uint8_t* values;
@@ -38,7 +41,8 @@ struct RowsParams {
 
 __device__ __forceinline__ float row_elem(const RowsParams& p, int64_t r, int64_t i) {
   if (i >= p.n) i = p.n - 1;  // replicate the last element (quantization.py:174-177)
-  return dev_load(p.src, r * p.row_stride + i * p.elem_stride, p.src_dtype);
+  const int64_t row = (r / p.block_rows) * p.block_stride + (r % p.block_rows) * p.row_stride;
+  return dev_load(p.src, row + i * p.elem_stride, p.src_dtype);
 }
 
 __device__ __forceinline__ void group_stats(const RowsParams& p, int64_t r, int64_t g, float qmax, float* mn_out,
@@ -102,31 +106,34 @@ __device__ __forceinline__ float div_rn(float a, float b, float y) {
 // bytes).  A wave's loads and stores are contiguous.  The source dtype is a
 // template argument, so the per-element chain (subtract, round, divide,
 // round, rint, clamp) has no branches; the division is one reciprocal per
-// group and three operations per element.
+// group and three operations per element.  The y grid dimension strides over
+// row blocks, the x dimension over the lanes of one block.
 template <int BITS, int SRC>
 __global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int lanes_per_group, int row_shift) {
   // row_shift = log2(lanes per row) when that is a power of two (no 64-bit division)
   const int64_t lanes_per_row = p.n / 8;
-  const int64_t total = p.rows * lanes_per_row;
+  const int64_t total = p.block_rows * lanes_per_row;
   const float qmax = (float)((1 << BITS) - 1);
   const int lane = threadIdx.x & 63;
+  for (int64_t blk = blockIdx.y; blk < p.blocks; blk += gridDim.y)
   for (int64_t v = (int64_t)blockIdx.x * kThreads + threadIdx.x; v - lane < total;
        v += (int64_t)gridDim.x * kThreads) {
     // whole waves stay in the loop so the shuffles see every lane of a group
     const bool active = v < total;
-    int64_t r = 0, i0 = 0;
+    int64_t r = 0, i0 = 0;  // row within the block, first element
     if (active) {
       r = row_shift >= 0 ? v >> row_shift : v / lanes_per_row;
       i0 = (v - r * lanes_per_row) * 8;
     }
+    const int64_t src_row = blk * p.block_stride + r * p.row_stride;
     float x[8];
     if (SRC == kF32) {
-      const float4* src = (const float4*)((const float*)p.src + r * p.row_stride + i0);
+      const float4* src = (const float4*)((const float*)p.src + src_row + i0);
       const float4 a = src[0], b = src[1];
       x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
       x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
     } else {
-      const uint4 w = *(const uint4*)((const uint16_t*)p.src + r * p.row_stride + i0);
+      const uint4 w = *(const uint4*)((const uint16_t*)p.src + src_row + i0);
       const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -145,6 +152,7 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int 
       mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     }
     if (!active) continue;
+    r += blk * p.block_rows;  // output row
     const float s = dev_group_scale(mn, mx, qmax, SRC);
     const float y = __fdiv_rn(1.0f, s);
     if (i0 % p.group == 0) {
@@ -909,9 +917,11 @@ bool valid_bits(int64_t b) { return b == 2 || b == 4 || b == 8; }
 
 }  // namespace
 
-extern "C" int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, int64_t n, int64_t row_stride,
-                                 int64_t elem_stride, int bits, int64_t group, uint8_t* values, void* scale,
-                                 void* zero, int meta_dtype, void* stream) {
+static int quantize_rows_impl(const void* src, int src_dtype, int64_t blocks, int64_t block_stride,
+                              int64_t block_rows, int64_t n, int64_t row_stride, int64_t elem_stride, int bits,
+                              int64_t group, uint8_t* values, void* scale, void* zero, int meta_dtype, void* stream,
+                              const char* name) {
+  const int64_t rows = blocks * block_rows;
   DKV_CHECK(valid_float_dtype(src_dtype), DKV_ERR_DTYPE, "quantize expects a floating-point tensor (f32/f16/bf16)");
   DKV_CHECK(valid_meta_dtype(meta_dtype), DKV_ERR_DTYPE, "metadata dtype must be floating point");
   DKV_CHECK(valid_bits(bits), DKV_ERR_INVALID, "bits must be one of (2, 4, 8), got %d", bits);
@@ -921,6 +931,9 @@ extern "C" int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, i
   RowsParams p;
   p.src = src;
   p.rows = rows;
+  p.blocks = blocks;
+  p.block_rows = block_rows;
+  p.block_stride = block_stride;
   p.n = n;
   p.row_stride = row_stride;
   p.elem_stride = elem_stride;
@@ -939,16 +952,21 @@ extern "C" int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, i
   const int esize = src_dtype == kF32 ? 4 : 2;
   const bool vec = elem_stride == 1 && n % 8 == 0 && group % 8 == 0 && group <= 512 && (group & (group - 1)) == 0 &&
                    n % group == 0 && ((uintptr_t)src % 16) == 0 && (row_stride * esize) % 16 == 0 &&
+                   (block_stride * esize) % 16 == 0 &&
                    (src_dtype == kF32 || src_dtype == kF16 || src_dtype == kBF16) && ((uintptr_t)values % 8) == 0 &&
                    (p.packed_bytes * bits) % 8 == 0 && (p.packed_bytes % 8) == 0;
   if (vec) {
-    const int64_t lanes = rows * (n / 8);
-    const int64_t blocks = std::min<int64_t>((lanes + kThreads - 1) / kThreads, 1 << 20);
+    // x: workgroups over one block's lanes; y: row blocks (the kernel strides
+    // over both, so the grid is capped at about 2^20 workgroups)
+    const int64_t lanes = block_rows * (n / 8);
+    const int64_t gy = std::min<int64_t>(blocks, 65535);
+    const int64_t gx = std::max<int64_t>(std::min<int64_t>((lanes + kThreads - 1) / kThreads, (1 << 20) / gy), 1);
     const int lpg = (int)(group / 8);
     const int64_t lpr = n / 8;
     const int row_shift = (lpr & (lpr - 1)) == 0 ? __builtin_ctzll((unsigned long long)lpr) : -1;
-#define DKV_ROWS_LAUNCH(B, T) \
-  hipLaunchKernelGGL((quantize_rows_vec<B, T>), dim3((unsigned)blocks), dim3(kThreads), 0, s, p, lpg, row_shift)
+#define DKV_ROWS_LAUNCH(B, T)                                                                                    \
+  hipLaunchKernelGGL((quantize_rows_vec<B, T>), dim3((unsigned)gx, (unsigned)gy), dim3(kThreads), 0, s, p, lpg, \
+                     row_shift)
 #define DKV_ROWS_BITS(T)                  \
   do {                                    \
     if (bits == 2) DKV_ROWS_LAUNCH(2, T); \
@@ -968,7 +986,24 @@ extern "C" int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, i
     hipLaunchKernelGGL(quantize_rows_serial, dim3((unsigned)((rows + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
                        p);
   }
-  return dkv_check_launch("dkv_quantize_rows");
+  return dkv_check_launch(name);
+}
+
+extern "C" int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, int64_t n, int64_t row_stride,
+                                 int64_t elem_stride, int bits, int64_t group, uint8_t* values, void* scale,
+                                 void* zero, int meta_dtype, void* stream) {
+  DKV_CHECK(rows >= 0, DKV_ERR_INVALID, "rows must be non-negative");
+  return quantize_rows_impl(src, src_dtype, 1, 0, rows, n, row_stride, elem_stride, bits, group, values, scale, zero,
+                            meta_dtype, stream, "dkv_quantize_rows");
+}
+
+extern "C" int dkv_quantize_row_blocks(const void* src, int src_dtype, int64_t blocks, int64_t block_stride,
+                                       int64_t block_rows, int64_t n, int64_t row_stride, int bits, int64_t group,
+                                       uint8_t* values, void* scale, void* zero, int meta_dtype, void* stream) {
+  DKV_CHECK(blocks >= 0 && block_rows >= 0, DKV_ERR_INVALID, "blocks and block_rows must be non-negative");
+  DKV_CHECK(block_rows == 0 || blocks <= INT64_MAX / block_rows, DKV_ERR_INVALID, "blocks * block_rows overflows");
+  return quantize_rows_impl(src, src_dtype, blocks, block_stride, block_rows, n, row_stride, 1, bits, group, values,
+                            scale, zero, meta_dtype, stream, "dkv_quantize_row_blocks");
 }
 
 extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stream) {

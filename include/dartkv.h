@@ -47,7 +47,7 @@ extern "C" {
 /* Thread-local description of the last error on this thread. */
 const char* dkv_last_error(void);
 
-/* ABI version (6); bumps when a struct below changes. */
+/* ABI version (7); bumps when a struct or an entry point below changes. */
 int dkv_abi_version(void);
 
 /*
@@ -66,6 +66,22 @@ int dkv_abi_version(void);
 int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, int64_t n,
                       int64_t row_stride, int64_t elem_stride, int bits, int64_t group,
                       uint8_t* values, void* scale, void* zero, int meta_dtype, void* stream);
+
+/*
+ * dkv_quantize_rows over `blocks` blocks of `block_rows` rows each, the form a
+ * token slice of a [B, H, T, D] tensor takes: row r = blk * block_rows + i
+ * (0 <= i < block_rows) starts at src[blk * block_stride + i * row_stride] and
+ * its elements are contiguous.  Outputs are laid out as for dkv_quantize_rows
+ * with rows = blocks * block_rows, so the result equals dkv_quantize_rows on
+ * the contiguous copy of the slice without making that copy.
+ *
+ * Replaces the same reference code as dkv_quantize_rows: the cache quantizes
+ * value pages cut out of the appended tensor along tokens
+ * (src/dart/cache.py:505-512, src/dart/quantization.py:134-204).
+ */
+int dkv_quantize_row_blocks(const void* src, int src_dtype, int64_t blocks, int64_t block_stride,
+                            int64_t block_rows, int64_t n, int64_t row_stride, int bits, int64_t group,
+                            uint8_t* values, void* scale, void* zero, int meta_dtype, void* stream);
 
 /*
  * Key quantization along tokens for `n_pages` pages of `page_tokens` tokens.

@@ -18,7 +18,7 @@ def declared_functions() -> set:
 
 def test_header_declares_the_entry_points():
     names = declared_functions()
-    assert {"dkv_quantize_rows", "dkv_quantize_key_pages", "dkv_dequantize_rows", "dkv_dequantize_mixed",
+    assert {"dkv_quantize_rows", "dkv_quantize_row_blocks", "dkv_quantize_key_pages", "dkv_dequantize_rows", "dkv_dequantize_mixed",
             "dkv_decode_attention", "dkv_decode_workspace_bytes", "dkv_last_error", "dkv_abi_version"} <= names
 
 
@@ -38,6 +38,9 @@ def test_library_loads_and_reports_errors_without_gpu():
     rc = lib.dkv_quantize_rows(None, 0, 1, 4, 4, 1, 3, 4, None, None, None, 0, None)
     assert rc == _lib.DKV_ERR_INVALID
     assert b"bits" in lib.dkv_last_error()
+    rc = lib.dkv_quantize_row_blocks(None, 0, 2, 64, -1, 4, 4, 2, 4, None, None, None, 0, None)
+    assert rc == _lib.DKV_ERR_INVALID
+    assert b"non-negative" in lib.dkv_last_error()
     assert lib.dkv_decode_workspace_bytes(2, 4, 8, 3) == 2 * 4 * 3 * 10 * 4
 
 

@@ -50,6 +50,35 @@ def test_uniform_quantize_bit_exact_vs_golden(golden):
         assert golden.matches(e["deq"], q.dequantize().cpu().contiguous()), e["tag"]
 
 
+@pytest.mark.parametrize("layout", ["token_slice", "batch1", "head1", "tokens_major", "one_token"])
+def test_value_rows_read_in_place_equal_the_contiguous_copy(layout):
+    """dkv_quantize_row_blocks on a strided token slice == dkv_quantize_rows on its copy, bit for bit."""
+    dart = _dkv()
+    from dartkv_amd.cache import _launch_value_rows
+    g = torch.Generator().manual_seed(7)
+    B, H, D = {"batch1": (1, 4), "head1": (3, 1)}.get(layout, (2, 3)) + (128,)
+    if layout == "tokens_major":
+        full = torch.randn(B, 200, H, D, generator=g).transpose(1, 2)  # [B, H, 200, D], not row blocks
+    else:
+        full = torch.randn(B, H, 200, D, generator=g)
+    t0, T = (37, 1) if layout == "one_token" else (37, 130)
+    for dtype in (torch.bfloat16, torch.float16, torch.float32):
+        src = full.to(dtype).to(DEV)[:, :, t0:t0 + T]
+        for bits, group, meta in ((2, 64, torch.float16), (4, 128, torch.bfloat16), (8, 32, torch.float32),
+                                  (2, 48, torch.float16)):
+            print("case", layout, dtype, bits, group, meta, flush=True)
+            G = -(-D // group)
+            values = torch.empty(B, H, T, -(-G * group // (8 // bits)), dtype=torch.uint8, device=DEV)
+            scale = torch.empty(B, H, T, G, dtype=meta, device=DEV)
+            zero = torch.empty_like(scale)
+            _launch_value_rows(src, bits, group, meta, values, scale, zero)
+            q = dart.quantize(src.contiguous(), bits=bits, group_size=group, metadata_dtype=meta, axis=-1)
+            torch.cuda.synchronize()
+            assert torch.equal(values, q.values.reshape(values.shape))
+            assert bits_equal(scale.cpu(), q.scale.reshape(scale.shape).cpu())
+            assert bits_equal(zero.cpu(), q.zero_point.reshape(zero.shape).cpu())
+
+
 def test_mixed_key_bit_exact_vs_golden_including_tie_order(golden):
     dart = _dkv()
     from tests.test_oracle_golden import _input
