@@ -68,7 +68,7 @@ __host__ __device__ inline LdsMap lds_map(int np, int gv) {
   m.ki = o; o += (np * 4 + 15) / 16 * 16;  // channel indices [NP] int32
   m.ks = o; o += 256;                      // key scale  [128] fp16
   m.kz = o; o += 256;                      // key zero   [128] fp16
-  m.klut = o; o += 1024;                   // 2-bit key tables [128 ch][LO, HI] (zero for promoted channels)
+  m.klut = o; o += 1024;                   // 2-bit key tables [128 ch][LO, HI] (zero for promoted channels), key_slot order
   o = (o + 255) / 256 * 256;               // (the 4-bit tables are addressed by byte: 256-aligned)
   m.klut16 = o; o += np * 32;              // 4-bit key tables [NP][16] fp16
   m.pidx = o; o += 64;                     // promoted channels [NP] uint8 (a copy: ki is refilled early)
@@ -84,10 +84,20 @@ __host__ __device__ inline LdsMap lds_map(int np, int gv) {
   o = (o + 15) / 16 * 16;
   m.vs = o; o += 256 * gv;                 // value scale [128 tok][Gv] fp16
   m.vz = o; o += 256 * gv;                 // value zero  [128 tok][Gv] fp16
-  m.vlut = o; o += kVlutStride * gv;       // value tables [Gv][128 tok][LO, HI], padded rows
+  m.vlut = o; o += kVlutStride * gv;       // value tables [Gv][128 tok][LO, HI] in K order (kpos), padded rows
   m.bytes = (o + 255) / 256 * 256;         // keeps every wave's region 256-aligned
   return m;
 }
+
+// Position of channel c's 2-bit key table: the tables of channels 8u + kq and
+// 8u + 4 + kq (channel blocks 2u and 2u + 1 of lane group kq) are adjacent, so
+// one 16-byte read serves a pair of blocks.
+__host__ __device__ inline int key_slot(int c) { return (c & ~7) | ((c & 3) << 1) | ((c >> 2) & 1); }
+
+// K position of token t in a P V block (block t / 16, K index 4 (t % 4) + (t / 4) % 4):
+// the softmax weights and the value tables are stored in this order, so a
+// lane's four tokens t, t + 4, t + 8, t + 12 are adjacent.
+__host__ __device__ inline int kpos(int t) { return (t & ~15) | ((t & 3) << 2) | ((t >> 2) & 3); }
 
 // Exact dequantized values for codes (c0, c1) of one (scale, zero) pair, as
 // an fp16 pair: fp16(fp16(code*s) + z), then bf16 precision if BF16.
@@ -239,7 +249,7 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
 
   // ---- per-lane constants ----
   const int sh = 2 * (n & 3);             // bit offset of this lane's codes in each byte
-  const int qd = 4 * (n >> 2);            // byte offset of this lane's code dword in a 16-byte run
+  const int qd = 8 * (n >> 2);            // byte offset of this lane's two code dwords in a 32-byte row
   const int slot = n >> 2, head = n & 3;  // slot-layout A row n = 4 * slot + head
   int aq[4];                              // promoted-query A sources (row at the lane's slot, else zeros)
 #pragma unroll
@@ -248,13 +258,14 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   // P V A source (heads in rows): weights of head n, or zeros
   const int apv = n < GQ ? M.pt + kPtStride * n + 8 * kq : M.zero + 8 * kq;
   // P V block blk, K index 4kq + m is token 16 blk + kq + 4m: the four lane
-  // groups then read code rows and tables in different banks; the weights are
-  // stored in that K order (wpos) so each A operand is one 8-byte read.
-  const int vtab = M.vlut + kVlutStride * ((8 * n) / p.vg) + 8 * kq;  // value tables of the lane's group
+  // groups then read code rows in different banks; the weights and the value
+  // tables are stored in that K order (kpos), so each A operand is one 8-byte
+  // read and a lane's four tables are one 32-byte run.
+  const int vtab = M.vlut + kVlutStride * ((8 * n) / p.vg) + 32 * kq;  // value tables of the lane's group
   const int vcode = M.vc + 32 * kq + 2 * n;                           // value codes of the lane's channels
 
   // ---- running state ----
-  // S (slot layout): lane (n, kq) holds heads 0..3 of tokens 64t + 16(n/4) + 4kq + n%4.
+  // S (slot layout): lane (n, kq) holds heads 0..3 of tokens 32(n/4) + 16t + 4kq + n%4.
   // O (heads in rows): lanes kq = 0 hold heads 0..3 of channels 8n + j in O[j].
   float m_run[4], l_part[4];
   float4v O[8];
@@ -324,57 +335,52 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
       pidx[lane] = (uint8_t)my_promoted;
     }
 #pragma unroll
-    for (int c = lane; c < kD; c += 64) *(uint2*)(lds + M.klut + 8 * c) = build_lut4<bf16>(ks[c], kz[c]);
+    for (int c = lane; c < kD; c += 64) *(uint2*)(lds + M.klut + 8 * key_slot(c)) = build_lut4<bf16>(ks[c], kz[c]);
     lds_sync();
     // promoted channels take the 4-bit pass: their 2-bit tables become zero
-    if (lane < np) *(uint2*)(lds + M.klut + 8 * my_promoted) = make_uint2(0u, 0u);
+    if (lane < np) *(uint2*)(lds + M.klut + 8 * key_slot(my_promoted)) = make_uint2(0u, 0u);
     lds_sync();
 
-    // ---- S = Q K; tile t covers tokens 64t + 16(n/4) + 4 slot + n%4 ----
+    // ---- S = Q K; tile t covers tokens 32(n/4) + 16t + 4 slot + n%4 ----
     float4v S[2];
     S[0] = S[1] = float4v{0.f, 0.f, 0.f, 0.f};
-    // 2-bit codes of every channel (promoted channels have zero tables);
-    // block cb + 1's codes and table are read before block cb is computed.
-    // The tables the later passes need (value tables, 4-bit key tables, the
-    // promoted channels' query) are built in between, so their LDS latency
-    // overlaps the lookups.
+    // 2-bit codes of every channel (promoted channels have zero tables), one
+    // pair of channel blocks (2u, 2u + 1) per step: each block's code dwords of
+    // both tiles are one 8-byte read and the pair's tables one 16-byte read;
+    // pair u + 1's are read before pair u is computed.  The tables the later
+    // passes need (value tables, 4-bit key tables, the promoted channels'
+    // query) are built in between, so their LDS latency overlaps the lookups.
     {
       const int row = M.kl + 32 * kq + qd;
-      const int tab = M.klut + 8 * kq;
+      const int tab = M.klut + 16 * kq;
       const uint16_t* vs = (const uint16_t*)(lds + M.vs);
       const uint16_t* vz = (const uint16_t*)(lds + M.vz);
-      constexpr int kAhead = 2;  // blocks whose codes and table are in flight
-      uint32_t w0[kD / 4], w1[kD / 4];
-      uint2 t[kD / 4];
-      auto load_cb = [&](int c) {
-        w0[c] = lds_u32(lds, row + 128 * c);
-        w1[c] = lds_u32(lds, row + 128 * c + 16);
-        t[c] = *(const uint2*)(lds + tab + 32 * c);
+      uint2 wc[kD / 4];
+      uint4 t[kD / 8];
+      auto load_pair = [&](int u) {
+        wc[2 * u] = *(const uint2*)(lds + row + 256 * u);
+        wc[2 * u + 1] = *(const uint2*)(lds + row + 256 * u + 128);
+        t[u] = *(const uint4*)(lds + tab + 64 * u);
       };
+      load_pair(0);
 #pragma unroll
-      for (int c = 0; c < kAhead; ++c) load_cb(c);
-      half4 pend0, pend1;  // even block's B operands, waiting for the odd one
-#pragma unroll
-      for (int cb = 0; cb < kD / 4; ++cb) {
-        if (cb + kAhead < kD / 4) load_cb(cb + kAhead);
-        const half4 b0 = lookup4((w0[cb] >> sh) & 0x03030303u, t[cb].x, t[cb].y);
-        const half4 b1 = lookup4((w1[cb] >> sh) & 0x03030303u, t[cb].x, t[cb].y);
-        if (cb & 1) {  // blocks cb - 1 and cb in one K = 32 MFMA per tile
-          S[0] = mma2(qa[cb - 1], qa[cb], pend0, b0, S[0]);
-          S[1] = mma2(qa[cb - 1], qa[cb], pend1, b1, S[1]);
-        } else {
-          pend0 = b0;
-          pend1 = b1;
-        }
-        if (cb % 4 == 1 && cb / 4 < 4) {
-          // value table k = cb / 4 of this lane: token lane + 64 (k & 1), group k >> 1
+      for (int u = 0; u < kD / 8; ++u) {
+        if (u + 1 < kD / 8) load_pair(u + 1);
+        const half4 b0e = lookup4((wc[2 * u].x >> sh) & 0x03030303u, t[u].x, t[u].y);
+        const half4 b1e = lookup4((wc[2 * u].y >> sh) & 0x03030303u, t[u].x, t[u].y);
+        const half4 b0o = lookup4((wc[2 * u + 1].x >> sh) & 0x03030303u, t[u].z, t[u].w);
+        const half4 b1o = lookup4((wc[2 * u + 1].y >> sh) & 0x03030303u, t[u].z, t[u].w);
+        S[0] = mma2(qa[2 * u], qa[2 * u + 1], b0e, b0o, S[0]);
+        S[1] = mma2(qa[2 * u], qa[2 * u + 1], b1e, b1o, S[1]);
+        if (u % 2 == 0 && u / 2 < 4) {
+          // value table k = u / 2 of this lane: token lane + 64 (k & 1), group k >> 1
           // (groups beyond gv rebuild an existing table with identical contents)
-          const int k = cb / 4;
+          const int k = u / 2;
           const int tt = lane + 64 * (k & 1), g = (k >> 1) % gv;
-          *(uint2*)(lds + M.vlut + kVlutStride * g + 8 * tt) = build_lut4<bf16>(vs[tt * gv + g], vz[tt * gv + g]);
+          *(uint2*)(lds + M.vlut + kVlutStride * g + 8 * kpos(tt)) = build_lut4<bf16>(vs[tt * gv + g], vz[tt * gv + g]);
         }
-        if (cb == 18) build_lut16_tables<bf16, np>(M, lds, ks, kz, lane);
-        if (cb == 26) {
+        if (u == 9) build_lut16_tables<bf16, np>(M, lds, ks, kz, lane);
+        if (u == 13) {
           const uint16_t* q16 = (const uint16_t*)(lds + M.q16);
           const uint8_t* pidx = lds + M.pidx;
           uint16_t* qp = (uint16_t*)(lds + M.qp);
@@ -391,7 +397,7 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
       const int g = i >> 7, tt = i & 127;
       const uint16_t* vs = (const uint16_t*)(lds + M.vs);
       const uint16_t* vz = (const uint16_t*)(lds + M.vz);
-      *(uint2*)(lds + M.vlut + kVlutStride * g + 8 * tt) = build_lut4<bf16>(vs[tt * gv + g], vz[tt * gv + g]);
+      *(uint2*)(lds + M.vlut + kVlutStride * g + 8 * kpos(tt)) = build_lut4<bf16>(vs[tt * gv + g], vz[tt * gv + g]);
     }
     lds_sync();
     // promoted channels: 4-bit codes, slot j = 4pb + kq of the high codes;
@@ -400,15 +406,11 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
       const uint32_t rl = (uint32_t)(sh - 1) & 31u, rh = (uint32_t)(sh - 3) & 31u;
       const uint32_t kq32 = 0x20202020u * (uint32_t)kq;
       const uint32_t m6 = in_sgpr(0x06060606u), m18 = in_sgpr(0x18181818u);
-      uint32_t wl0[np / 4], wl1[np / 4], wh0[np / 4], wh1[np / 4];
+      uint2 wl[np / 4], wh[np / 4];  // .x: tile 0, .y: tile 1
       auto load_pb = [&](int pb) {
         const int j = 4 * pb + kq;
-        const int row = M.kl + 32 * pidx[j] + qd;
-        wl0[pb] = lds_u32(lds, row);
-        wl1[pb] = lds_u32(lds, row + 16);
-        const int hrow = M.kh + 32 * j + qd;
-        wh0[pb] = lds_u32(lds, hrow);
-        wh1[pb] = lds_u32(lds, hrow + 16);
+        wl[pb] = *(const uint2*)(lds + M.kl + 32 * pidx[j] + qd);
+        wh[pb] = *(const uint2*)(lds + M.kh + 32 * j + qd);
       };
       load_pb(0);
       half4 pa, pend0, pend1;  // even block's operands, waiting for the odd one (np / 4 is even)
@@ -416,8 +418,8 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
       for (int pb = 0; pb < np / 4; ++pb) {
         if (pb + 1 < np / 4) load_pb(pb + 1);
         const half4 a = load_a(lds, aq, 8 * pb);
-        const half4 b0 = gather16(wl0[pb], wh0[pb], rl, rh, kq32, tab16, 128 * pb, m6, m18);
-        const half4 b1 = gather16(wl1[pb], wh1[pb], rl, rh, kq32, tab16, 128 * pb, m6, m18);
+        const half4 b0 = gather16(wl[pb].x, wh[pb].x, rl, rh, kq32, tab16, 128 * pb, m6, m18);
+        const half4 b1 = gather16(wl[pb].y, wh[pb].y, rl, rh, kq32, tab16, 128 * pb, m6, m18);
         if (pb & 1) {
           S[0] = mma2(pa, a, pend0, b0, S[0]);
           S[1] = mma2(pa, a, pend1, b1, S[1]);
@@ -456,15 +458,15 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
         }
       }
       uint16_t* pt = (uint16_t*)(lds + M.pt);
-      const int tok = 16 * (n >> 2) + 4 * kq + (n & 3);
-      const int wpos = (tok & ~15) | ((tok & 3) << 2) | ((tok >> 2) & 3);  // K position of token tok
+      const int tok = 32 * (n >> 2) + 4 * kq + (n & 3);  // tile 0; tile 1 is tok + 16
+      const int wpos = kpos(tok);
 #pragma unroll
       for (int i = 0; i < GQ; ++i) {
         const float p0 = __builtin_amdgcn_exp2f(x[0][i] - m_run[i]);
         const float p1 = __builtin_amdgcn_exp2f(x[1][i] - m_run[i]);
         l_part[i] += p0 + p1;
         pt[i * (kPtStride / 2) + wpos] = __builtin_bit_cast(uint16_t, (_Float16)p0);
-        pt[i * (kPtStride / 2) + wpos + 64] = __builtin_bit_cast(uint16_t, (_Float16)p1);
+        pt[i * (kPtStride / 2) + wpos + 16] = __builtin_bit_cast(uint16_t, (_Float16)p1);
       }
     }
     lds_sync();
@@ -481,12 +483,11 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
       auto load_blk = [&](int blk) {
         a[blk] = *(const half4*)(lds + apv + 32 * blk);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          x[blk][m] = *(const uint16_t*)(lds + vcode + 512 * blk + 128 * m);
-          const uint2 t = *(const uint2*)(lds + vtab + 128 * blk + 32 * m);
-          lo[blk][m] = t.x;
-          hi[blk][m] = t.y;
-        }
+        for (int m = 0; m < 4; ++m) x[blk][m] = *(const uint16_t*)(lds + vcode + 512 * blk + 128 * m);
+        const uint4 t01 = *(const uint4*)(lds + vtab + 128 * blk);
+        const uint4 t23 = *(const uint4*)(lds + vtab + 128 * blk + 16);
+        lo[blk][0] = t01.x; hi[blk][0] = t01.y; lo[blk][1] = t01.z; hi[blk][1] = t01.w;
+        lo[blk][2] = t23.x; hi[blk][2] = t23.y; lo[blk][3] = t23.z; hi[blk][3] = t23.w;
       };
       load_blk(0);
       uint2 wprev[8];  // even block's B operands, waiting for the odd one
