@@ -322,23 +322,15 @@ __device__ __forceinline__ void lds_heads(const float* src, float (&x)[MG]) {
   }
 }
 
+// Chunk `chunk` of rest segment v of (batch, kv head) bhi, by one wave; qs
+// and ws are the wave's LDS (kDenseDim * MG and kDenseChunk * MG floats).
 template <int MG, bool BF>
-__global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodeParams p, int chunks) {
-  __shared__ __attribute__((aligned(16))) float qsh[kDenseWaves][kDenseDim * MG];    // [c][MG]
-  __shared__ __attribute__((aligned(16))) float wsh[kDenseWaves][kDenseChunk * MG];  // [t][MG] weights
+__device__ __forceinline__ void dense_chunk(const DecodeParams& p, int chunks, int bhi, int v, int chunk, int lane,
+                                            float* qs, float* ws) {
   const dkv_decode_args& a = p.a;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int worker = blockIdx.x * kDenseWaves + wave;
-  const int per_bh = p.n_total * chunks;
-  if (worker >= (int)(a.B * a.Hkv) * per_bh) return;
-  const int v = (worker % per_bh) / chunks, chunk = worker % chunks;
-  const int bhi = worker / per_bh;
   const int b = bhi / (int)a.Hkv, kvh = bhi % (int)a.Hkv;
   const int64_t bh = (int64_t)bhi;
   const int G = p.group;
-  float* qs = qsh[wave];
-  float* ws = wsh[wave];
 
   const dkv_segment seg = general_segment(p, v);
   const bool ok = seg.key_kind == DKV_KEY_DENSE && seg.value_kind == DKV_VALUE_DENSE &&
@@ -446,43 +438,116 @@ __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodePara
   }
 }
 
-// One block per (batch, query head): combine the split records with the
-// log-sum-exp rule, then out = acc / max(sum, 1e-20) (attention.py:86).
-__global__ void __launch_bounds__(kThreads) decode_merge(DecodeParams p) {
-  extern __shared__ float wsh[];  // [S] weights, [S] sums
+template <int MG, bool BF>
+__global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodeParams p, int chunks) {
+  __shared__ __attribute__((aligned(16))) float qsh[kDenseWaves][kDenseDim * MG];    // [c][MG]
+  __shared__ __attribute__((aligned(16))) float wsh[kDenseWaves][kDenseChunk * MG];  // [t][MG] weights
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int worker = blockIdx.x * kDenseWaves + wave;
+  const int per_bh = p.n_total * chunks;
+  if (worker >= (int)(p.a.B * p.a.Hkv) * per_bh) return;
+  dense_chunk<MG, BF>(p, chunks, worker / per_bh, (worker % per_bh) / chunks, worker % chunks, lane, qsh[wave],
+                      wsh[wave]);
+}
+
+// Combine the split records of query heads kvh * G + h (h < G) of batch b with
+// the log-sum-exp rule, then out = acc / max(sum, 1e-20) (attention.py:86).
+// Same arithmetic and summation order for every thread count: per head, the
+// maximum and the sum run over the splits in order; each output channel sums
+// even and odd splits separately and adds the two.  wgt / lsum: G * S floats of
+// LDS each; mx / den: G floats.
+__device__ __forceinline__ void merge_heads(const DecodeParams& p, int b, int hq0, int G, float* wgt, float* lsum,
+                                            float* mx, float* den) {
   const dkv_decode_args& a = p.a;
-  const int bq = blockIdx.x;  // b * Hq + hq
-  const int b = bq / (int)a.Hq, hq = bq % (int)a.Hq;
   const int D = (int)a.D, S = p.split_stride;
-  const float* ws = (const float*)a.workspace + (int64_t)bq * S * (D + 2);
-  for (int s = threadIdx.x; s < S; s += blockDim.x) {
-    wsh[s] = ws[(int64_t)s * (D + 2)];
-    wsh[S + s] = ws[(int64_t)s * (D + 2) + 1];
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const float* ws = (const float*)a.workspace + ((int64_t)b * a.Hq + hq0) * S * (D + 2);
+  for (int i = tid; i < G * S; i += nt) {
+    wgt[i] = ws[(int64_t)i * (D + 2)];
+    lsum[i] = ws[(int64_t)i * (D + 2) + 1];
   }
   __syncthreads();
-  float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, wsh[s]);
-  __syncthreads();
-  for (int s = threadIdx.x; s < S; s += blockDim.x) {
-    const float ms = wsh[s];
-    wsh[s] = ms == -INFINITY ? 0.f : expf(ms - M);
+  if (tid < G) {
+    const float* w = wgt + tid * S;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, w[s]);
+    mx[tid] = M;
   }
   __syncthreads();
-  float L = 0.f;
-  for (int s = 0; s < S; ++s) L += wsh[S + s] * wsh[s];
-  const float denom = fmaxf(L, 1e-20f);
-  for (int c = threadIdx.x; c < D; c += blockDim.x) {
+  for (int i = tid; i < G * S; i += nt) {
+    const float ms = wgt[i];
+    wgt[i] = ms == -INFINITY ? 0.f : expf(ms - mx[i / S]);
+  }
+  __syncthreads();
+  if (tid < G) {
+    const float* w = wgt + tid * S;
+    const float* l = lsum + tid * S;
+    float L = 0.f;
+    for (int s = 0; s < S; ++s) L += l[s] * w[s];
+    den[tid] = fmaxf(L, 1e-20f);
+  }
+  __syncthreads();
+  for (int i = tid; i < G * D; i += nt) {
+    const int h = i / D, c = i % D;
+    const float* w = wgt + h * S;
+    const float* rec = ws + (int64_t)h * S * (D + 2) + 2 + c;
     float o0 = 0.f, o1 = 0.f;
     int s = 0;
-    for (; s + 1 < S; s += 2) {
-      o0 += ws[(int64_t)s * (D + 2) + 2 + c] * wsh[s];
-      o1 += ws[(int64_t)(s + 1) * (D + 2) + 2 + c] * wsh[s + 1];
+    for (; s + 8 <= S; s += 8) {  // eight records' loads in flight, then the same sums in order
+      float r[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r[j] = rec[(int64_t)(s + j) * (D + 2)];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        o0 += r[j] * w[s + j];
+        o1 += r[j + 1] * w[s + j + 1];
+      }
     }
-    if (s < S) o0 += ws[(int64_t)s * (D + 2) + 2 + c] * wsh[s];
-    const float o = (o0 + o1) / denom;
+    for (; s + 1 < S; s += 2) {
+      o0 += rec[(int64_t)s * (D + 2)] * w[s];
+      o1 += rec[(int64_t)(s + 1) * (D + 2)] * w[s + 1];
+    }
+    if (s < S) o0 += rec[(int64_t)s * (D + 2)] * w[s];
+    const float o = (o0 + o1) / den[h];
+    const int hq = hq0 + h;
     dev_store(a.out, (int64_t)b * a.out_sb + (int64_t)hq * a.out_sh + c, o, (int)a.q_dtype);
-    if (a.out_f32) a.out_f32[(int64_t)bq * D + c] = o;
+    if (a.out_f32) a.out_f32[((int64_t)b * a.Hq + hq) * D + c] = o;
   }
+}
+
+// The dense rest segments and the merge in one launch: one block per (batch,
+// kv head).  Its waves take the (segment, chunk) tasks of that pair in turn
+// and write their records; after a barrier the block merges every record of
+// the pair's query heads (the page kernel's were written by the launch
+// before).  Saves the merge launch and its wait.  Up to 4 heads per KV head it
+// keeps to 128 VGPRs, so two blocks share a CU.
+constexpr int kDenseMergeWaves = 8;
+
+template <int MG, bool BF>
+__global__ void __launch_bounds__(64 * kDenseMergeWaves, MG <= 4 ? 4 : 2) decode_dense_merge(DecodeParams p, int chunks) {
+  __shared__ __attribute__((aligned(16))) float qsh[kDenseMergeWaves][kDenseDim * MG];
+  __shared__ __attribute__((aligned(16))) float wsh[kDenseMergeWaves][kDenseChunk * MG];
+  __shared__ float mx[kDenseMaxGroup], den[kDenseMaxGroup];
+  extern __shared__ float dyn[];  // [G][S] weights, [G][S] sums
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int bhi = blockIdx.x;
+  const int tasks = p.n_total * chunks;
+  for (int t = wave; t < tasks; t += kDenseMergeWaves)
+    dense_chunk<MG, BF>(p, chunks, bhi, t / chunks, t % chunks, lane, qsh[wave], wsh[wave]);
+  __syncthreads();
+  const int G = p.group, S = p.split_stride;
+  const int b = bhi / (int)p.a.Hkv, kvh = bhi % (int)p.a.Hkv;
+  merge_heads(p, b, kvh * G, G, dyn, dyn + G * S, mx, den);
+}
+
+// One block per (batch, query head): the merge alone.
+__global__ void __launch_bounds__(kThreads) decode_merge(DecodeParams p) {
+  extern __shared__ float wsh[];  // [S] weights, [S] sums
+  __shared__ float mx[1], den[1];
+  const int bq = blockIdx.x;  // b * Hq + hq
+  merge_heads(p, bq / (int)p.a.Hq, bq % (int)p.a.Hq, 1, wsh, wsh + p.split_stride, mx, den);
 }
 
 }  // namespace
@@ -581,6 +646,24 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
     DKV_CHECK(a.D == kDenseDim && p.group <= kDenseMaxGroup, DKV_ERR_UNSUPPORTED,
               "rest_dense_tokens needs head_dim %d and at most %d query heads per KV head", kDenseDim, kDenseMaxGroup);
     const int mg = p.group <= 1 ? 1 : p.group <= 2 ? 2 : p.group <= 4 ? 4 : 8;
+    const size_t merge_lds = (size_t)2 * p.group * stride * sizeof(float);
+    if (merge_lds <= 64 * 1024) {
+      // dense chunks and the merge in one launch, one block per (batch, kv head)
+      const dim3 grid((unsigned)(a.B * a.Hkv)), block(64 * kDenseMergeWaves);
+      const int ch = (int)chunks;
+#define DKV_DM_LAUNCH(MGV)                                                                                    \
+  do {                                                                                                        \
+    if (a.cache_dtype == dkv::kBF16)                                                                          \
+      hipLaunchKernelGGL((decode_dense_merge<MGV, true>), grid, block, merge_lds, s, p, ch);                 \
+    else hipLaunchKernelGGL((decode_dense_merge<MGV, false>), grid, block, merge_lds, s, p, ch);             \
+  } while (0)
+      if (mg == 1) DKV_DM_LAUNCH(1);
+      else if (mg == 2) DKV_DM_LAUNCH(2);
+      else if (mg == 4) DKV_DM_LAUNCH(4);
+      else DKV_DM_LAUNCH(8);
+#undef DKV_DM_LAUNCH
+      return dkv_check_launch("dkv_decode_attention(dense + merge)");
+    }
     const int64_t workers = a.B * a.Hkv * rest * chunks;
     const dim3 grid((unsigned)((workers + kDenseWaves - 1) / kDenseWaves)), block(64 * kDenseWaves);
     const int ch = (int)chunks;
