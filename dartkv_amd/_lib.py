@@ -26,7 +26,7 @@ KEY_DENSE, KEY_UNIFORM, KEY_MIXED = 0, 1, 2
 VALUE_DENSE, VALUE_UNIFORM = 0, 1
 SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
@@ -36,6 +36,17 @@ def dtype_code(dtype: torch.dtype) -> int:
         return _DTYPE_CODES[dtype]
     except KeyError:
         raise TypeError(f"unsupported dtype {dtype}") from None
+
+
+class ValueRowsArgs(ctypes.Structure):
+    _fields_ = [
+        ("src", ctypes.c_void_p), ("src_dtype", ctypes.c_int64),
+        ("blocks", ctypes.c_int64), ("block_stride", ctypes.c_int64), ("block_rows", ctypes.c_int64),
+        ("n", ctypes.c_int64), ("row_stride", ctypes.c_int64),
+        ("bits", ctypes.c_int64), ("group", ctypes.c_int64),
+        ("values", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("zero", ctypes.c_void_p),
+        ("meta_dtype", ctypes.c_int64),
+    ]
 
 
 class KeyPagesArgs(ctypes.Structure):
@@ -52,6 +63,7 @@ class KeyPagesArgs(ctypes.Structure):
         ("idx", ctypes.c_void_p), ("idx_page_stride", ctypes.c_int64),
         ("scale", ctypes.c_void_p), ("scale_page_stride", ctypes.c_int64),
         ("zero", ctypes.c_void_p), ("zero_page_stride", ctypes.c_int64),
+        ("values", ctypes.c_void_p),  # const dkv_value_rows_args* (optional)
     ]
 
 

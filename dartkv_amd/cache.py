@@ -604,8 +604,9 @@ class DartKVCache:
         """Quantize consecutive pages; the last may be partial (reference cache.py:472-479)."""
         if key_states.shape[-2] != value_states.shape[-2]:
             raise RuntimeError("key/value page lengths diverged before quantization")
-        keys = self._quantize_key_chunks(key_states)
-        values = self._quantize_value_chunks(value_states, self.config.page_size)
+        jobs: list = []
+        values = self._quantize_value_chunks(value_states, self.config.page_size, jobs)
+        keys = self._quantize_key_chunks(key_states, jobs)
         for kseg, vseg in zip(keys, values):
             self._key_segments.append(kseg)
             self._append_quantized_value_page(vseg)
@@ -613,20 +614,37 @@ class DartKVCache:
     def _key_pages_only(self, key_states: torch.Tensor) -> None:
         self._key_segments.extend(self._quantize_key_chunks(key_states))
 
-    def _quantize_key_chunks(self, key_states: torch.Tensor) -> List[Segment]:
-        """Key pages of ``page_size`` tokens (last may be shorter), one launch per page size."""
+    def _quantize_key_chunks(self, key_states: torch.Tensor, value_jobs: Optional[list] = None) -> List[Segment]:
+        """Key pages of ``page_size`` tokens (last may be shorter), one launch per page size.
+
+        ``value_jobs`` from _quantize_value_chunks: each goes into the key
+        launch that covers the same tokens.
+        """
         c = self.config
         T = key_states.shape[-2]
         P = c.page_size
         full = T // P
+        jobs = {start: (n, job) for start, n, job, _ in (value_jobs or [])}
+
+        def job_for(start: int, n: int):
+            entry = jobs.pop(start, None)
+            if entry is None:
+                return None
+            if entry[0] != n:
+                raise RuntimeError("value rows and key pages cover different tokens")
+            return entry[1]
+
         out: List[Segment] = []
         if full:
-            out.extend(self._quantize_key_launch(key_states[..., : full * P, :], P, full))
+            out.extend(self._quantize_key_launch(key_states[..., : full * P, :], P, full, job_for(0, full * P)))
         if T - full * P:
-            out.extend(self._quantize_key_launch(key_states[..., full * P:, :], T - full * P, 1))
+            out.extend(self._quantize_key_launch(key_states[..., full * P:, :], T - full * P, 1,
+                                                 job_for(full * P, T - full * P)))
+        if jobs:
+            raise RuntimeError("value rows left without a key launch")
         return out
 
-    def _quantize_key_launch(self, src: torch.Tensor, tokens: int, n_pages: int) -> List[Segment]:
+    def _quantize_key_launch(self, src: torch.Tensor, tokens: int, n_pages: int, values=None) -> List[Segment]:
         c = self.config
         B, H, _, D = src.shape
         dev = src.device
@@ -653,12 +671,13 @@ class DartKVCache:
                     launch_key_pages(src[..., p * tokens:(p + 1) * tokens, :], page_tokens=tokens, n_pages=1,
                                      key_mode=_lib.KEY_MIXED, bits=2, group=kg, promoted=K, selection=selection,
                                      given_idx=given[p].contiguous(), meta=meta, low=low[p], high=high[p],
-                                     idx=idx[p], scale=scale[p], zero=zero[p])
+                                     idx=idx[p], scale=scale[p], zero=zero[p],
+                                     values=values if p == n_pages - 1 else None)
             else:
                 launch_key_pages(src, page_tokens=tokens, n_pages=n_pages, key_mode=_lib.KEY_MIXED, bits=2,
                                  group=kg, promoted=K, selection=selection,
                                  given_idx=None if given is None else given[0].contiguous(), meta=meta,
-                                 low=low, high=high, idx=idx, scale=scale, zero=zero)
+                                 low=low, high=high, idx=idx, scale=scale, zero=zero, values=values)
             run = _PageRun(dict(low_values=low, high_values=high, channel_indices=idx, scale=scale, zero_point=zero),
                            0, 1, dict(original_shape=(B, H, tokens, D), padded_tokens=G * kg, group_size=kg,
                                       low_bits=2, promote_bits=c.promote_bits, output_dtype=src.dtype))
@@ -667,22 +686,25 @@ class DartKVCache:
         per = 8 // bits
         padded = G * kg
         packed_dim = ((padded + per - 1) // per) * per
-        values = torch.empty(n_pages, B, H, D, packed_dim // per, dtype=torch.uint8, device=dev)
+        codes = torch.empty(n_pages, B, H, D, packed_dim // per, dtype=torch.uint8, device=dev)
         scale = torch.empty(n_pages, B, H, D, G, dtype=meta, device=dev)
         zero = torch.empty(n_pages, B, H, D, G, dtype=meta, device=dev)
         launch_key_pages(src, page_tokens=tokens, n_pages=n_pages, key_mode=_lib.KEY_UNIFORM, bits=bits, group=kg,
-                         promoted=0, selection=0, given_idx=None, meta=meta, low=values, high=None, idx=None,
-                         scale=scale, zero=zero)
-        run = _PageRun(dict(values=values, scale=scale, zero_point=zero), 0, 1,
+                         promoted=0, selection=0, given_idx=None, meta=meta, low=codes, high=None, idx=None,
+                         scale=scale, zero=zero, values=values)
+        run = _PageRun(dict(values=codes, scale=scale, zero_point=zero), 0, 1,
                        dict(original_shape=(B, H, tokens, D), original_dim=tokens, padded_dim=padded,
                             packed_dim=packed_dim, group_size=kg, bits=bits, output_dtype=src.dtype, axis=2))
         return [_PagedQuantized(run, p) for p in range(n_pages)]
 
-    def _quantize_value_chunks(self, value_states: torch.Tensor, chunk: int) -> List[QuantizedTensor]:
+    def _quantize_value_chunks(self, value_states: torch.Tensor, chunk: int,
+                               jobs: Optional[list] = None) -> List[QuantizedTensor]:
         """Value segments of ``chunk`` tokens (last may be shorter) quantized along head_dim.
 
         All full chunks share one launch and one [B,H,T,P] code tensor; each
-        segment is a token-range view of it.
+        segment is a token-range view of it.  With ``jobs`` (a list) nothing is
+        launched here: each launch's (token start, token count, job, keepalive)
+        is appended for the caller to hand to the key launch of the same tokens.
         """
         c = self.config
         B, H, T, D = value_states.shape
@@ -702,7 +724,11 @@ class DartKVCache:
             values = torch.empty(B, H, n, packed_dim // per, dtype=torch.uint8, device=dev)
             scale = torch.empty(B, H, n, Gv, dtype=meta, device=dev)
             zero = torch.empty(B, H, n, Gv, dtype=meta, device=dev)
-            _launch_value_rows(src, bits, vg, meta, values, scale, zero)
+            if jobs is None:
+                _launch_value_rows(src, bits, vg, meta, values, scale, zero)
+            else:
+                job, keep = _value_rows_job(src, bits, vg, meta, values, scale, zero)
+                jobs.append((start, n, job, keep))
             run = _PageRun(dict(values=values, scale=scale, zero_point=zero), 2, size,
                            dict(original_shape=(B, H, size, D), original_dim=D, padded_dim=padded,
                                 packed_dim=packed_dim, group_size=vg, bits=bits, output_dtype=value_states.dtype,
@@ -860,12 +886,13 @@ class DartKVCache:
 # helpers
 # ---------------------------------------------------------------------------
 
-def _launch_value_rows(src: torch.Tensor, bits: int, group: int, meta: torch.dtype, values: torch.Tensor,
-                       scale: torch.Tensor, zero: torch.Tensor) -> None:
-    """Quantize [B,H,T,D] value rows along head_dim straight from strided storage.
+def _value_rows_job(src: torch.Tensor, bits: int, group: int, meta: torch.dtype, values: torch.Tensor,
+                    scale: torch.Tensor, zero: torch.Tensor):
+    """The C description of quantizing [B,H,T,D] value rows along head_dim.
 
     A token slice of a [B,H,T',D] tensor is B*H blocks of T contiguous rows;
-    the kernel reads it in place.  Other layouts are copied first.
+    the kernel reads it in place.  Other layouts are copied first.  Returns
+    (``_lib.ValueRowsArgs``, the source tensor to keep alive until launch).
     """
     B, H, T, D = src.shape
     sb, sh, st, sd = src.stride()
@@ -881,10 +908,21 @@ def _launch_value_rows(src: torch.Tensor, bits: int, group: int, meta: torch.dty
     if blocks is None:
         src = src.contiguous()
         blocks, block_stride = B * H, T * D
+    job = _lib.ValueRowsArgs(src=src.data_ptr(), src_dtype=_lib.dtype_code(src.dtype), blocks=blocks,
+                             block_stride=block_stride, block_rows=T, n=D, row_stride=D, bits=bits, group=group,
+                             values=values.data_ptr(), scale=scale.data_ptr(), zero=zero.data_ptr(),
+                             meta_dtype=_lib.dtype_code(meta))
+    return job, src
+
+
+def _launch_value_rows(src: torch.Tensor, bits: int, group: int, meta: torch.dtype, values: torch.Tensor,
+                       scale: torch.Tensor, zero: torch.Tensor) -> None:
+    """Quantize [B,H,T,D] value rows along head_dim (dkv_quantize_row_blocks)."""
+    job, src = _value_rows_job(src, bits, group, meta, values, scale, zero)
     lib = _lib.load()
-    rc = lib.dkv_quantize_row_blocks(src.data_ptr(), _lib.dtype_code(src.dtype), blocks, block_stride, T, D, D, bits,
-                                     group, values.data_ptr(), scale.data_ptr(), zero.data_ptr(),
-                                     _lib.dtype_code(meta), _lib.stream_ptr(src.device))
+    rc = lib.dkv_quantize_row_blocks(job.src, job.src_dtype, job.blocks, job.block_stride, job.block_rows, job.n,
+                                     job.row_stride, job.bits, job.group, job.values, job.scale, job.zero,
+                                     job.meta_dtype, _lib.stream_ptr(src.device))
     _lib.check(rc, "dkv_quantize_row_blocks")
 
 

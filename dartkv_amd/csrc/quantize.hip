@@ -106,18 +106,18 @@ __device__ __forceinline__ float div_rn(float a, float b, float y) {
 // bytes).  A wave's loads and stores are contiguous.  The source dtype is a
 // template argument, so the per-element chain (subtract, round, divide,
 // round, rint, clamp) has no branches; the division is one reciprocal per
-// group and three operations per element.  The y grid dimension strides over
-// row blocks, the x dimension over the lanes of one block.
+// group and three operations per element.  Workgroup (bx, by) of a gx x gy
+// grid: y strides over row blocks, x over the lanes of one block.
 template <int BITS, int SRC>
-__global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int lanes_per_group, int row_shift) {
+__device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per_group, int row_shift, int64_t bx,
+                                              int64_t by, int64_t gx, int64_t gy) {
   // row_shift = log2(lanes per row) when that is a power of two (no 64-bit division)
   const int64_t lanes_per_row = p.n / 8;
   const int64_t total = p.block_rows * lanes_per_row;
   const float qmax = (float)((1 << BITS) - 1);
   const int lane = threadIdx.x & 63;
-  for (int64_t blk = blockIdx.y; blk < p.blocks; blk += gridDim.y)
-  for (int64_t v = (int64_t)blockIdx.x * kThreads + threadIdx.x; v - lane < total;
-       v += (int64_t)gridDim.x * kThreads) {
+  for (int64_t blk = by; blk < p.blocks; blk += gy)
+  for (int64_t v = bx * kThreads + threadIdx.x; v - lane < total; v += gx * kThreads) {
     // whole waves stay in the loop so the shuffles see every lane of a group
     const bool active = v < total;
     int64_t r = 0, i0 = 0;  // row within the block, first element
@@ -174,6 +174,11 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int 
     else if (BITS == 4) *(uint32_t*)out = packed[0];
     else *(uint2*)out = make_uint2(packed[0], packed[1]);
   }
+}
+
+template <int BITS, int SRC>
+__global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int lanes_per_group, int row_shift) {
+  rows_vec_body<BITS, SRC>(p, lanes_per_group, row_shift, blockIdx.x, blockIdx.y, gridDim.x, gridDim.y);
 }
 
 // Any group size: one thread per row walks the packed bytes in order.
@@ -838,20 +843,51 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
 constexpr int kSelectMaxD = 128;
 constexpr int kSelectStack = 16;  // >= 2 floor(log2(kSelectMaxD)) + 1
 
-__global__ void __launch_bounds__(64) key_select_pages(KeyParams k, int row_bytes) {
-  __shared__ SelItem work[kSelectMaxD];
-  __shared__ int stack[3 * kSelectStack];
+// Page `item` (page-major over (b, h)): the lanes of one wave stage its scores
+// in `work`, then lane 0 runs the exact selection and writes the indices.
+__device__ __forceinline__ void select_page(const KeyParams& k, int row_bytes, int64_t item, int lane, SelItem* work,
+                                            int* stack) {
   const dkv_key_pages_args& a = k.a;
-  const int64_t item = blockIdx.x;
   const int64_t bhs = a.B * a.H;
   const int64_t page = item / bhs, bh = item % bhs;
   const int D = (int)a.D, K = (int)a.promoted;
   const float* score = (const float*)(a.low + page * a.low_page_stride + bh * D * row_bytes);
-  for (int j = threadIdx.x; j < D; j += 64) work[j] = SelItem{score[j], j};
-  __syncthreads();
-  if (threadIdx.x != 0) return;
+  for (int j = lane; j < D; j += 64) work[j] = SelItem{score[j], j};
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane != 0) return;
   int32_t* idx_out = (int32_t*)((char*)a.idx + page * a.idx_page_stride) + bh * K;
-  select_topk_filled(D, K, (SelItem*)work, idx_out, (int*)stack, kSelectStack);
+  select_topk_filled(D, K, work, idx_out, stack, kSelectStack);
+}
+
+__global__ void __launch_bounds__(64) key_select_pages(KeyParams k, int row_bytes) {
+  __shared__ SelItem work[kSelectMaxD];
+  __shared__ int stack[3 * kSelectStack];
+  select_page(k, row_bytes, blockIdx.x, threadIdx.x, work, stack);
+}
+
+// The key path's channel selection and a value-row job in one launch.
+// Workgroups [0, sel_blocks) select (one wave per page, as key_select_pages);
+// the others quantize value rows (workgroup b - sel_blocks of the gx x gy grid
+// of quantize_rows_vec).  A selection keeps one lane busy and its wave waiting
+// on LDS; the value rows use the rest of each SIMD meanwhile.
+constexpr int kSelectWaves = kThreads / 64;
+
+template <int BITS, int SRC>
+__global__ void __launch_bounds__(kThreads) select_pages_and_rows(KeyParams k, int row_bytes, int64_t items,
+                                                                  int64_t sel_blocks, RowsParams p, int lpg,
+                                                                  int row_shift, int64_t gx, int64_t gy) {
+  __shared__ SelItem work[kSelectWaves][kSelectMaxD];
+  __shared__ int stack[kSelectWaves][3 * kSelectStack];
+  if ((int64_t)blockIdx.x < sel_blocks) {
+    const int wave = threadIdx.x >> 6;
+    const int64_t item = (int64_t)blockIdx.x * kSelectWaves + wave;
+    if (item < items) select_page(k, row_bytes, item, threadIdx.x & 63, work[wave], stack[wave]);
+    return;
+  }
+  const int64_t b = (int64_t)blockIdx.x - sel_blocks;
+  rows_vec_body<BITS, SRC>(p, lpg, row_shift, b % gx, b / gx, gx, gy);
 }
 
 __host__ inline size_t key_tiled_smem(int D, int T, int G, int K, int row_bytes) {
@@ -917,18 +953,27 @@ bool valid_bits(int64_t b) { return b == 2 || b == 4 || b == 8; }
 
 }  // namespace
 
-static int quantize_rows_impl(const void* src, int src_dtype, int64_t blocks, int64_t block_stride,
-                              int64_t block_rows, int64_t n, int64_t row_stride, int64_t elem_stride, int bits,
-                              int64_t group, uint8_t* values, void* scale, void* zero, int meta_dtype, void* stream,
-                              const char* name) {
+// A planned value-row launch: parameters, kernel choice and grid.
+struct RowsLaunch {
+  RowsParams p;
+  int64_t rows;
+  bool vec;                // quantize_rows_vec applies
+  int lpg, row_shift;      // its lanes per group and log2(lanes per row) (-1: not a power of two)
+  int64_t gx, gy;          // its grid
+  int bits, src_dtype;
+};
+
+// Validate a value-row job and plan its launch (nothing is launched).
+static int prepare_rows(const void* src, int src_dtype, int64_t blocks, int64_t block_stride, int64_t block_rows,
+                        int64_t n, int64_t row_stride, int64_t elem_stride, int bits, int64_t group, uint8_t* values,
+                        void* scale, void* zero, int meta_dtype, RowsLaunch& L) {
   const int64_t rows = blocks * block_rows;
   DKV_CHECK(valid_float_dtype(src_dtype), DKV_ERR_DTYPE, "quantize expects a floating-point tensor (f32/f16/bf16)");
   DKV_CHECK(valid_meta_dtype(meta_dtype), DKV_ERR_DTYPE, "metadata dtype must be floating point");
   DKV_CHECK(valid_bits(bits), DKV_ERR_INVALID, "bits must be one of (2, 4, 8), got %d", bits);
   DKV_CHECK(group > 0, DKV_ERR_INVALID, "group_size must be a positive integer, got %lld", (long long)group);
   DKV_CHECK(n > 0 && rows >= 0, DKV_ERR_INVALID, "quantize does not support an empty final dimension");
-  if (rows == 0) return DKV_OK;
-  RowsParams p;
+  RowsParams& p = L.p;
   p.src = src;
   p.rows = rows;
   p.blocks = blocks;
@@ -948,44 +993,64 @@ static int quantize_rows_impl(const void* src, int src_dtype, int64_t blocks, in
   p.values = values;
   p.scale = scale;
   p.zero = zero;
-  hipStream_t s = (hipStream_t)stream;
+  L.rows = rows;
+  L.bits = bits;
+  L.src_dtype = src_dtype;
   const int esize = src_dtype == kF32 ? 4 : 2;
-  const bool vec = elem_stride == 1 && n % 8 == 0 && group % 8 == 0 && group <= 512 && (group & (group - 1)) == 0 &&
-                   n % group == 0 && ((uintptr_t)src % 16) == 0 && (row_stride * esize) % 16 == 0 &&
-                   (block_stride * esize) % 16 == 0 &&
-                   (src_dtype == kF32 || src_dtype == kF16 || src_dtype == kBF16) && ((uintptr_t)values % 8) == 0 &&
-                   (p.packed_bytes * bits) % 8 == 0 && (p.packed_bytes % 8) == 0;
-  if (vec) {
-    // x: workgroups over one block's lanes; y: row blocks (the kernel strides
-    // over both, so the grid is capped at about 2^20 workgroups)
-    const int64_t lanes = block_rows * (n / 8);
-    const int64_t gy = std::min<int64_t>(blocks, 65535);
-    const int64_t gx = std::max<int64_t>(std::min<int64_t>((lanes + kThreads - 1) / kThreads, (1 << 20) / gy), 1);
-    const int lpg = (int)(group / 8);
-    const int64_t lpr = n / 8;
-    const int row_shift = (lpr & (lpr - 1)) == 0 ? __builtin_ctzll((unsigned long long)lpr) : -1;
-#define DKV_ROWS_LAUNCH(B, T)                                                                                    \
-  hipLaunchKernelGGL((quantize_rows_vec<B, T>), dim3((unsigned)gx, (unsigned)gy), dim3(kThreads), 0, s, p, lpg, \
-                     row_shift)
-#define DKV_ROWS_BITS(T)                  \
-  do {                                    \
-    if (bits == 2) DKV_ROWS_LAUNCH(2, T); \
-    else if (bits == 4) DKV_ROWS_LAUNCH(4, T); \
-    else DKV_ROWS_LAUNCH(8, T);           \
+  L.vec = elem_stride == 1 && n % 8 == 0 && group % 8 == 0 && group <= 512 && (group & (group - 1)) == 0 &&
+          n % group == 0 && ((uintptr_t)src % 16) == 0 && (row_stride * esize) % 16 == 0 &&
+          (block_stride * esize) % 16 == 0 &&
+          (src_dtype == kF32 || src_dtype == kF16 || src_dtype == kBF16) && ((uintptr_t)values % 8) == 0 &&
+          (p.packed_bytes * bits) % 8 == 0 && (p.packed_bytes % 8) == 0;
+  L.lpg = (int)(group / 8);
+  const int64_t lpr = n / 8;
+  L.row_shift = (lpr & (lpr - 1)) == 0 ? __builtin_ctzll((unsigned long long)lpr) : -1;
+  // x: workgroups over one block's lanes; y: row blocks (the kernel strides
+  // over both, so the grid is capped at about 2^20 workgroups)
+  const int64_t lanes = block_rows * (n / 8);
+  L.gy = std::max<int64_t>(std::min<int64_t>(blocks, 65535), 1);
+  L.gx = std::max<int64_t>(std::min<int64_t>((lanes + kThreads - 1) / kThreads, (1 << 20) / L.gy), 1);
+  return DKV_OK;
+}
+
+static void launch_rows(const RowsLaunch& L, hipStream_t s) {
+  if (L.rows == 0) return;
+  const RowsParams& p = L.p;
+  if (L.vec) {
+#define DKV_ROWS_LAUNCH(B, T)                                                                                     \
+  hipLaunchKernelGGL((quantize_rows_vec<B, T>), dim3((unsigned)L.gx, (unsigned)L.gy), dim3(kThreads), 0, s, p, L.lpg, \
+                     L.row_shift)
+#define DKV_ROWS_BITS(T)                    \
+  do {                                      \
+    if (L.bits == 2) DKV_ROWS_LAUNCH(2, T);   \
+    else if (L.bits == 4) DKV_ROWS_LAUNCH(4, T); \
+    else DKV_ROWS_LAUNCH(8, T);             \
   } while (0)
-    if (src_dtype == kBF16) DKV_ROWS_BITS(kBF16);
-    else if (src_dtype == kF16) DKV_ROWS_BITS(kF16);
+    if (L.src_dtype == kBF16) DKV_ROWS_BITS(kBF16);
+    else if (L.src_dtype == kF16) DKV_ROWS_BITS(kF16);
     else DKV_ROWS_BITS(kF32);
 #undef DKV_ROWS_BITS
 #undef DKV_ROWS_LAUNCH
-  } else if (group % p.per_byte == 0) {
-    const int64_t items = rows * p.groups;
+  } else if (p.group % p.per_byte == 0) {
+    const int64_t items = L.rows * p.groups;
     hipLaunchKernelGGL(quantize_rows_aligned, dim3((unsigned)((items + kThreads - 1) / kThreads)), dim3(kThreads), 0,
                        s, p);
   } else {
-    hipLaunchKernelGGL(quantize_rows_serial, dim3((unsigned)((rows + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
-                       p);
+    hipLaunchKernelGGL(quantize_rows_serial, dim3((unsigned)((L.rows + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                       s, p);
   }
+}
+
+static int quantize_rows_impl(const void* src, int src_dtype, int64_t blocks, int64_t block_stride,
+                              int64_t block_rows, int64_t n, int64_t row_stride, int64_t elem_stride, int bits,
+                              int64_t group, uint8_t* values, void* scale, void* zero, int meta_dtype, void* stream,
+                              const char* name) {
+  RowsLaunch L;
+  const int rc = prepare_rows(src, src_dtype, blocks, block_stride, block_rows, n, row_stride, elem_stride, bits,
+                              group, values, scale, zero, meta_dtype, L);
+  if (rc != DKV_OK) return rc;
+  if (L.rows == 0) return DKV_OK;
+  launch_rows(L, (hipStream_t)stream);
   return dkv_check_launch(name);
 }
 
@@ -1025,7 +1090,25 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
               DKV_ERR_INVALID, "given channel indices are required");
   }
   DKV_CHECK(a.B * a.H <= 0x7fffffffLL && a.n_pages <= 65535, DKV_ERR_UNSUPPORTED, "too many pages for one launch");
-  if (a.n_pages == 0) return DKV_OK;
+  DKV_CHECK(a.B * a.H * a.n_pages <= 0x7fffffffLL, DKV_ERR_UNSUPPORTED, "too many pages for one launch");
+  // the optional value rows: validated and planned before anything launches
+  RowsLaunch VL;
+  const bool with_values = a.values != nullptr;
+  bool values_done = false;
+  if (with_values) {
+    const dkv_value_rows_args& v = *a.values;
+    DKV_CHECK(v.blocks >= 0 && v.block_rows >= 0, DKV_ERR_INVALID, "value blocks and block_rows must be non-negative");
+    DKV_CHECK(v.block_rows == 0 || v.blocks <= INT64_MAX / v.block_rows, DKV_ERR_INVALID,
+              "value blocks * block_rows overflows");
+    const int rc = prepare_rows(v.src, (int)v.src_dtype, v.blocks, v.block_stride, v.block_rows, v.n, v.row_stride, 1,
+                                (int)v.bits, v.group, v.values, v.scale, v.zero, (int)v.meta_dtype, VL);
+    if (rc != DKV_OK) return rc;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (a.n_pages == 0) {
+    if (with_values) launch_rows(VL, s);
+    return dkv_check_launch("dkv_quantize_key_pages");
+  }
   KeyParams k;
   k.a = a;
   k.G = (a.page_tokens + a.group - 1) / a.group;
@@ -1051,7 +1134,6 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
                                                                        (a.high_page_stride % 4) == 0));
   if (use_fast) {
     const dim3 grid((unsigned)(a.B * a.H), (unsigned)a.n_pages);
-    hipStream_t s = (hipStream_t)stream;
 #define DKV_KEYF(T, B, M) hipLaunchKernelGGL((quantize_key_pages_fast<T, B>), grid, dim3(kThreads), 0, s, k, M)
 #define DKV_KEYF_BITS(T, M)                   \
   do {                                        \
@@ -1068,10 +1150,30 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
     // lane per page selects, codes
     const bool select = a.key_mode == DKV_KEY_MIXED && Kp > 0 && Kp < a.D && a.selection != DKV_SELECT_GIVEN;
     if (select && a.B * a.H * a.n_pages > 256) {
-      DKV_KEYF_RUN(kKeyScores);
       const int64_t items = a.B * a.H * a.n_pages;
-      DKV_CHECK(items <= 0x7fffffffLL, DKV_ERR_UNSUPPORTED, "too many pages for one launch");
-      hipLaunchKernelGGL(key_select_pages, dim3((unsigned)items), dim3(64), 0, s, k, row_bytes);
+      DKV_KEYF_RUN(kKeyScores);
+      if (with_values && VL.vec && VL.rows > 0 && (items + kSelectWaves - 1) / kSelectWaves + VL.gx * VL.gy <= 0x7fffffffLL) {
+        // the selection and the value rows share one launch
+        const int64_t sel_blocks = (items + kSelectWaves - 1) / kSelectWaves;
+        const dim3 sgrid((unsigned)(sel_blocks + VL.gx * VL.gy));
+#define DKV_SV(B, T)                                                                                                \
+  hipLaunchKernelGGL((select_pages_and_rows<B, T>), sgrid, dim3(kThreads), 0, s, k, row_bytes, items, sel_blocks, \
+                     VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy)
+#define DKV_SV_BITS(T)                    \
+  do {                                    \
+    if (VL.bits == 2) DKV_SV(2, T);       \
+    else if (VL.bits == 4) DKV_SV(4, T);  \
+    else DKV_SV(8, T);                    \
+  } while (0)
+        if (VL.src_dtype == kBF16) DKV_SV_BITS(kBF16);
+        else if (VL.src_dtype == kF16) DKV_SV_BITS(kF16);
+        else DKV_SV_BITS(kF32);
+#undef DKV_SV_BITS
+#undef DKV_SV
+        values_done = true;
+      } else {
+        hipLaunchKernelGGL(key_select_pages, dim3((unsigned)items), dim3(64), 0, s, k, row_bytes);
+      }
       DKV_KEYF_RUN(kKeyCodes);
     } else {
       DKV_KEYF_RUN(kKeyAll);
@@ -1079,28 +1181,29 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
 #undef DKV_KEYF_RUN
 #undef DKV_KEYF_BITS
 #undef DKV_KEYF
+    if (with_values && !values_done) launch_rows(VL, s);
     return dkv_check_launch("dkv_quantize_key_pages");
   }
   if (use_tiled) {
     const dim3 grid((unsigned)(a.B * a.H), (unsigned)a.n_pages);
-    hipStream_t s = (hipStream_t)stream;
     const bool select = a.key_mode == DKV_KEY_MIXED && Kp > 0 && Kp < a.D && a.selection != DKV_SELECT_GIVEN;
     if (select && row_bytes >= 4 && a.D <= kSelectMaxD) {
       // scores -> one lane per page selects -> codes
       hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyScores);
       const int64_t items = a.B * a.H * a.n_pages;
-      DKV_CHECK(items <= 0x7fffffffLL, DKV_ERR_UNSUPPORTED, "too many pages for one launch");
       hipLaunchKernelGGL(key_select_pages, dim3((unsigned)items), dim3(64), 0, s, k, row_bytes);
       hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyCodes);
     } else {
       hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyAll);
     }
+    if (with_values) launch_rows(VL, s);
     return dkv_check_launch("dkv_quantize_key_pages");
   }
   const size_t shmem = (size_t)a.D * (sizeof(float) + 2 * sizeof(int32_t) + sizeof(SelItem));
   DKV_CHECK(shmem <= 64 * 1024, DKV_ERR_UNSUPPORTED, "head_dim %lld is too large", (long long)a.D);
   hipLaunchKernelGGL(quantize_key_pages_kernel, dim3((unsigned)(a.B * a.H), (unsigned)a.n_pages), dim3(kThreads),
-                     shmem, (hipStream_t)stream, k);
+                     shmem, s, k);
+  if (with_values) launch_rows(VL, s);
   return dkv_check_launch("dkv_quantize_key_pages");
 }
 

@@ -9,6 +9,8 @@ Public surface and validation follow the reference ``dart.mixed``
 
 from __future__ import annotations
 
+import ctypes
+
 from dataclasses import dataclass
 from typing import Optional, Tuple
 
@@ -211,11 +213,13 @@ def quantize_key_mixed(
 def launch_key_pages(src: torch.Tensor, *, page_tokens: int, n_pages: int, key_mode: int, bits: int, group: int,
                      promoted: int, selection: int, given_idx: Optional[torch.Tensor], meta: torch.dtype,
                      low: torch.Tensor, high: Optional[torch.Tensor], idx: Optional[torch.Tensor],
-                     scale: torch.Tensor, zero: torch.Tensor) -> None:
+                     scale: torch.Tensor, zero: torch.Tensor, values=None) -> None:
     """Quantize ``n_pages`` pages of keys from ``src`` [B,H,T,D] into page-major outputs.
 
     Each output tensor has the page index as its leading dim when n_pages > 1
     (and may omit it when n_pages == 1); page strides are taken from dim 0.
+    ``values`` (a ``_lib.ValueRowsArgs``) adds the same tokens' value rows to
+    the call: the library quantizes them alongside the key path.
     """
     B, H, _, D = src.shape
 
@@ -239,6 +243,7 @@ def launch_key_pages(src: torch.Tensor, *, page_tokens: int, n_pages: int, key_m
     a.idx, a.idx_page_stride = _lib.ptr(idx), page_stride(idx)
     a.scale, a.scale_page_stride = scale.data_ptr(), page_stride(scale)
     a.zero, a.zero_page_stride = zero.data_ptr(), page_stride(zero)
+    a.values = 0 if values is None else ctypes.addressof(values)
     lib = _lib.load()
     _lib.check(lib.dkv_quantize_key_pages(a, _lib.stream_ptr(src.device)), "dkv_quantize_key_pages")
 

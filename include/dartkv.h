@@ -47,7 +47,7 @@ extern "C" {
 /* Thread-local description of the last error on this thread. */
 const char* dkv_last_error(void);
 
-/* ABI version (7); bumps when a struct or an entry point below changes. */
+/* ABI version (8); bumps when a struct or an entry point below changes. */
 int dkv_abi_version(void);
 
 /*
@@ -82,6 +82,24 @@ int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, int64_t n,
 int dkv_quantize_row_blocks(const void* src, int src_dtype, int64_t blocks, int64_t block_stride,
                             int64_t block_rows, int64_t n, int64_t row_stride, int bits, int64_t group,
                             uint8_t* values, void* scale, void* zero, int meta_dtype, void* stream);
+
+/*
+ * Value rows for dkv_quantize_key_pages to quantize in the same call, with the
+ * meaning of dkv_quantize_row_blocks's arguments: `blocks` blocks of
+ * `block_rows` rows of `n` contiguous elements, row r = blk * block_rows + i at
+ * src[blk * block_stride + i * row_stride]; outputs laid out as for
+ * dkv_quantize_rows.
+ */
+typedef struct dkv_value_rows_args {
+  const void* src;
+  int64_t src_dtype;
+  int64_t blocks, block_stride, block_rows, n, row_stride;
+  int64_t bits, group;
+  uint8_t* values;
+  void* scale;
+  void* zero;
+  int64_t meta_dtype;
+} dkv_value_rows_args;
 
 /*
  * Key quantization along tokens for `n_pages` pages of `page_tokens` tokens.
@@ -125,6 +143,11 @@ typedef struct dkv_key_pages_args {
   int64_t scale_page_stride;
   void* zero;
   int64_t zero_page_stride;
+  /* Optional (NULL: keys only): the value rows of the same tokens, quantized
+   * by this call too.  The reference quantizes a page's keys and its values
+   * one after the other (src/dart/cache.py:472-479); given both, the library
+   * runs the value kernel alongside the key path's serial channel selection. */
+  const dkv_value_rows_args* values;
 } dkv_key_pages_args;
 
 int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stream);

@@ -49,7 +49,7 @@ def test_ctypes_structs_match_the_header(tmp_path):
     import ctypes
     from dartkv_amd import _lib
     structs = {"dkv_segment": _lib.Segment, "dkv_decode_args": _lib.DecodeArgs,
-               "dkv_key_pages_args": _lib.KeyPagesArgs}
+               "dkv_key_pages_args": _lib.KeyPagesArgs, "dkv_value_rows_args": _lib.ValueRowsArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dartkv.h"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
