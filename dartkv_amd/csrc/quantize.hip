@@ -873,6 +873,10 @@ __global__ void __launch_bounds__(64) key_select_pages(KeyParams k, int row_byte
 // of quantize_rows_vec).  A selection keeps one lane busy and its wave waiting
 // on LDS; the value rows use the rest of each SIMD meanwhile.
 constexpr int kSelectWaves = kThreads / 64;
+// Shared launches pay off while every selection wave is resident at once (one
+// wave per page, 256 CUs x 32 waves); past that the selections queue in rounds
+// and the value rows wait behind them, so the two run as separate launches.
+constexpr int64_t kSelectFuseMaxPages = 8192;
 
 template <int BITS, int SRC>
 __global__ void __launch_bounds__(kThreads) select_pages_and_rows(KeyParams k, int row_bytes, int64_t items,
@@ -1152,7 +1156,8 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
     if (select && a.B * a.H * a.n_pages > 256) {
       const int64_t items = a.B * a.H * a.n_pages;
       DKV_KEYF_RUN(kKeyScores);
-      if (with_values && VL.vec && VL.rows > 0 && (items + kSelectWaves - 1) / kSelectWaves + VL.gx * VL.gy <= 0x7fffffffLL) {
+      if (with_values && VL.vec && VL.rows > 0 && items <= kSelectFuseMaxPages &&
+          (items + kSelectWaves - 1) / kSelectWaves + VL.gx * VL.gy <= 0x7fffffffLL) {
         // the selection and the value rows share one launch
         const int64_t sel_blocks = (items + kSelectWaves - 1) / kSelectWaves;
         const dim3 sgrid((unsigned)(sel_blocks + VL.gx * VL.gy));
