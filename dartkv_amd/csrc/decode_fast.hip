@@ -99,26 +99,36 @@ __host__ __device__ inline int key_slot(int c) { return (c & ~7) | ((c & 3) << 1
 // lane's four tokens t, t + 4, t + 8, t + 12 are adjacent.
 __host__ __device__ inline int kpos(int t) { return (t & ~15) | ((t & 3) << 2) | ((t >> 2) & 3); }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// fp16 scale or zero point (bits in the low half of x) in both halves; as an
+// operand of a packed op this is an op_sel broadcast, not an instruction.
+__device__ __forceinline__ half2v splat_h(uint32_t x) {
+  const _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)x);
+  return half2v{h, h};
+}
+
 // Exact dequantized values for codes (c0, c1) of one (scale, zero) pair, as
 // an fp16 pair: fp16(fp16(code*s) + z), then bf16 precision if BF16.
 template <bool BF16>
-__device__ __forceinline__ uint32_t lut_pair(uint32_t codes_h2, uint32_t s_h2, uint32_t z_h2) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  h2 c = __builtin_bit_cast(h2, codes_h2);
-  h2 s = __builtin_bit_cast(h2, s_h2);
-  h2 z = __builtin_bit_cast(h2, z_h2);
-  h2 prod = c * s;  // -ffp-contract=off keeps the multiply and the add separate
-  h2 sum = prod + z;
+__device__ __forceinline__ uint32_t lut_pair(uint32_t codes_h2, half2v s, half2v z) {
+  const half2v c = __builtin_bit_cast(half2v, codes_h2);
+  const half2v prod = c * s;  // -ffp-contract=off keeps the multiply and the add separate
+  const half2v sum = prod + z;
   uint32_t r = __builtin_bit_cast(uint32_t, sum);
   return BF16 ? round_pair_to_bf16_precision(r) : r;
 }
 
 // Byte-plane table of the 4 values for codes 0..3: x = low bytes, y = high bytes.
+// For codes 0 and 1 the products 0 * s and 1 * s are exact, so one fused
+// multiply-add rounds once, exactly as fp16(fp16(code * s) + z) does; codes 2
+// and 3 multiply and add separately.
 template <bool BF16>
 __device__ __forceinline__ uint2 build_lut4(uint32_t s, uint32_t z) {
-  const uint32_t s2 = s * 0x10001u, z2 = z * 0x10001u;
-  const uint32_t v01 = lut_pair<BF16>(0x3c000000u, s2, z2);  // codes (0, 1)
-  const uint32_t v23 = lut_pair<BF16>(0x42004000u, s2, z2);  // codes (2, 3)
+  const half2v sv = splat_h(s), zv = splat_h(z);
+  uint32_t v01 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(half2v{0.0f16, 1.0f16}, sv, zv));
+  if (BF16) v01 = round_pair_to_bf16_precision(v01);
+  const uint32_t v23 = lut_pair<BF16>(0x42004000u, sv, zv);  // codes (2, 3)
   return make_uint2(perm(v23, v01, 0x06040200u), perm(v23, v01, 0x07050301u));
 }
 
@@ -185,7 +195,7 @@ __device__ __forceinline__ void build_lut16_tables(const LdsMap& M, uint8_t* lds
     if (j < NP) {
       const int half = lane & 1;
       const int c = pidx[j];
-      const uint32_t s2 = (uint32_t)ks[c] * 0x10001u, z2 = (uint32_t)kz[c] * 0x10001u;
+      const half2v s2 = splat_h(ks[c]), z2 = splat_h(kz[c]);
       // fp16 code pairs (8 half + 2q, 8 half + 2q + 1), q = 0..3
       const uint32_t e0 = half ? 0x48804800u : 0x3c000000u;  // (8, 9)   | (0, 1)
       const uint32_t e1 = half ? 0x49804900u : 0x42004000u;  // (10, 11) | (2, 3)
