@@ -110,6 +110,32 @@ def _seg_fields(seg):
     return {"values": seg.values, "scale": seg.scale, "zero": seg.zero_point}
 
 
+@pytest.mark.parametrize("selection", ["magnitude", "variance"])
+def test_large_append_pages_bit_exact_vs_oracle(selection):
+    """An append of more than 256 key pages takes the separate selection pass
+    (scores, one wave per page, codes) with the value rows in the selection's
+    launch; every packed field, channel order included, equals the oracle's."""
+    dart = _dkv()
+    from dartkv_amd import synthetic
+    from oracle import dart_oracle as O
+    k, v, _ = synthetic.outlier_kv(2, 8, 3000, 128, query_heads=32, dtype=torch.bfloat16, seed=11)
+    cfg = dict(bits=2, page_size=128, key_group_size=128, value_group_size=64, promote_ratio=0.25, sink_tokens=32,
+               hold_partial_pages=True, metadata_dtype=torch.float16, channel_selection=selection)
+    print("case", selection, "pages", 2 * 8 * ((3000 - 32) // 128), flush=True)
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    cache.append(k.to(DEV), v.to(DEV))
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    oc.append(k, v)
+    torch.cuda.synchronize()
+    pairs = list(zip(cache.iter_segments(), oc.segments()))
+    assert len(pairs) == len(oc.segments())
+    for (ks, vs), (oks, ovs) in pairs:
+        for a, b in zip(_seg_fields(ks).values(), _seg_fields(oks).values()):
+            assert bits_equal(a.cpu(), b)
+        for a, b in zip(_seg_fields(vs).values(), _seg_fields(ovs).values()):
+            assert bits_equal(a.cpu(), b)
+
+
 @pytest.mark.parametrize("name", ["c2", "c1", "nonheld", "held_mixed", "kitty_local", "kitty_value_local",
                                   "uniform_mix_bits"])
 def test_cache_pages_and_decode_vs_golden(golden, name):
