@@ -164,30 +164,35 @@ def streamed_dart_attention(query: torch.Tensor, cache: DartKVCache, *, scale: O
     return _multi_token_attention(query, cache, scale=scale)
 
 
-def _multi_token_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None) -> torch.Tensor:
-    """Several query tokens: per-segment HIP dequantization + fp32 online softmax on the GPU."""
+def _multi_token_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,
+                           out_f32: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Several query tokens per head over the packed cache.
+
+    The reference attends every query token to every cached token, with no
+    mask (attention.py:67-87), so token i of query head h is one more query
+    row of h's KV group.  A [B, Hq, c, D] slice of the query read as a
+    [B, Hq * c, D] query keeps that grouping (row h * c + i belongs to KV head
+    h // G), and the single-token HIP decode path runs it unchanged: the MFMA
+    page kernel while G * c <= 4 rows per KV head, the general kernel up to 16.
+    ``out_f32`` ([B, Hq, Q, D] float32) receives the result before the cast.
+    """
     batch, kv_heads, head_dim = cache.shape[0], cache.shape[1], cache.shape[3]
-    Hq = query.shape[1]
+    Hq, Q = query.shape[1], query.shape[-2]
     groups = Hq // kv_heads
-    factor = scale if scale is not None else 1.0 / math.sqrt(head_dim)
-    q = query.float().reshape(batch, kv_heads, groups, query.shape[-2], head_dim)
-    m = torch.full(q.shape[:-1], -torch.inf, dtype=torch.float32, device=query.device)
-    l = torch.zeros_like(m)
-    acc = torch.zeros_like(q)
-    for kseg, vseg in cache.iter_segments():
-        keys = kseg if isinstance(kseg, torch.Tensor) else kseg.dequantize()
-        values = vseg if isinstance(vseg, torch.Tensor) else vseg.dequantize()
-        keys = keys.float().unsqueeze(2).contiguous()      # [B, Hkv, 1, T, D]
-        values = values.float().unsqueeze(2).contiguous()
-        logits = torch.matmul(q, keys.transpose(-1, -2).contiguous()) * factor
-        new_m = torch.maximum(m, logits.amax(dim=-1))
-        old_w = torch.exp(m - new_m)
-        w = torch.exp(logits - new_m.unsqueeze(-1))
-        acc = acc * old_w.unsqueeze(-1) + torch.matmul(w, values)
-        l = l * old_w + w.sum(dim=-1)
-        m = new_m
-    out = acc / l.clamp_min(1e-20).unsqueeze(-1)
-    return out.reshape(batch, Hq, query.shape[-2], head_dim).to(query.dtype)
+    chunk = max(1, 4 // groups) if groups <= 4 else max(1, 16 // groups)
+    if out_f32 is not None and (out_f32.shape != (batch, Hq, Q, head_dim) or out_f32.dtype != torch.float32):
+        raise ValueError("out_f32 must be a float32 [B, Hq, Q, D] tensor")
+    out = torch.empty(batch, Hq, Q, head_dim, dtype=query.dtype, device=query.device)
+    for start in range(0, Q, chunk):
+        c = min(chunk, Q - start)
+        rows = query[:, :, start:start + c].reshape(batch, Hq * c, head_dim)
+        o32 = None if out_f32 is None else torch.empty(batch, Hq * c, head_dim, dtype=torch.float32,
+                                                       device=query.device)
+        o = decode_attention(rows, cache, scale=scale, out_f32=o32)
+        out[:, :, start:start + c] = o.reshape(batch, Hq, c, head_dim)
+        if out_f32 is not None:
+            out_f32[:, :, start:start + c] = o32.reshape(batch, Hq, c, head_dim)
+    return out
 
 
 __all__ = ["dense_attention", "streamed_dart_attention", "decode_attention"]

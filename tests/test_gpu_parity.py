@@ -110,6 +110,39 @@ def _seg_fields(seg):
     return {"values": seg.values, "scale": seg.scale, "zero": seg.zero_point}
 
 
+@pytest.mark.parametrize("Hkv,Hq,Q,dtype", [
+    (8, 32, 3, torch.bfloat16),   # G 4: one token per launch (MFMA page kernel)
+    (4, 8, 5, torch.bfloat16),    # G 2: two tokens per launch
+    (4, 4, 4, torch.float16),     # G 1: four tokens per launch
+    (2, 6, 2, torch.bfloat16),    # G 3: general kernel
+])
+def test_multi_token_attention_vs_oracle(Hkv, Hq, Q, dtype):
+    """Several query tokens attend to every cached token (reference attention.py:67-87, no mask)."""
+    dart = _dkv()
+    from dartkv_amd.attention import _multi_token_attention
+    from oracle import dart_oracle as O
+    from dartkv_amd import synthetic
+    k, v, _ = synthetic.outlier_kv(2, Hkv, 900, 128, query_heads=Hq, dtype=dtype, seed=40 + Q)
+    cfg = dict(bits=2, page_size=128, key_group_size=128, value_group_size=64, promote_ratio=0.25, sink_tokens=32,
+               hold_partial_pages=True, metadata_dtype=torch.float16)
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    oc.append(k, v)
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    cache.append(k.to(DEV), v.to(DEV))
+    q = torch.randn(2, Hq, Q, 128, generator=torch.Generator().manual_seed(Q)).to(dtype)
+    _, ref32 = O.streamed_attention(q, oc, return_fp32=True)
+    print("case", Hkv, Hq, Q, dtype, flush=True)
+    qd = q.to(DEV)
+    out32 = torch.empty(2, Hq, Q, 128, dtype=torch.float32, device=DEV)
+    out = _multi_token_attention(qd, cache, out_f32=out32)
+    fused = dart.fused_dart_attention(qd, cache)
+    torch.cuda.synchronize()
+    err = rel_err(out32, ref32)
+    print("rel err", err, flush=True)
+    assert err <= tolerance(dtype)
+    assert out.shape == (2, Hq, Q, 128) and bits_equal(fused.cpu(), out.cpu())
+
+
 @pytest.mark.parametrize("selection", ["magnitude", "variance"])
 def test_large_append_pages_bit_exact_vs_oracle(selection):
     """An append of more than 256 key pages takes the separate selection pass
