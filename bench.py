@@ -151,6 +151,7 @@ def cpu_baseline(args, cfg, budget_s: float = 20.0) -> dict:
 def prefill_c3(torch, dart, synthetic, stream, cfg: dict) -> dict:
     """C3 prefill: one append of [8, 8, 16384, 128] bf16 K/V into a 2-bit + 25 % cache, then 256 one-token appends.
 
+    ``uniform_sweep`` times the same append into uniform 2-, 4- and 8-bit caches (no promotion).
     GB/s counts the K/V bytes read plus the packed bytes written (pages, metadata, dense sink and tail).
     ``append_us`` is the mean time per append of 256 one-token appends (HIP events around the loop;
     two of them seal a page).
@@ -164,17 +165,30 @@ def prefill_c3(torch, dart, synthetic, stream, cfg: dict) -> dict:
     for i in range(130):  # one-token appends through a page seal: first-use costs stay out of the timing
         warm.append(k[:, :, T + i % 256:T + i % 256 + 1], v[:, :, T + i % 256:T + i % 256 + 1])
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    times = []
-    for _ in range(3):
-        cache = dart.DartKVCache(dart.DartKVCacheConfig(**ccfg))
-        torch.cuda.synchronize()
-        e0.record(stream)
-        cache.append(kp, vp)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        times.append(e0.elapsed_time(e1))
-    ms = min(times)
+
+    def timed_append(config: dict):
+        """Best of three one-shot appends of the whole prefill into a fresh cache."""
+        times = []
+        for _ in range(3):
+            cache = dart.DartKVCache(dart.DartKVCacheConfig(**config))
+            torch.cuda.synchronize()
+            e0.record(stream)
+            cache.append(kp, vp)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        return min(times), cache
+
     read = 2 * B * H * T * D * 2
+    # the uniform 2/4/8-bit widths of the config's sweep (one append each, no promotion)
+    sweep = {}
+    for bits in (2, 4, 8):
+        ucfg = dict(ccfg, bits=bits, promote_ratio=0.0)
+        ums, ucache = timed_append(ucfg)
+        sweep[f"{bits}b"] = {"ms": round(ums, 3), "bytes_written": ucache.storage_bytes,
+                             "gbs": round((read + ucache.storage_bytes) / (ums * 1e-3) / 1e9, 2)}
+        del ucache
+    ms, cache = timed_append(ccfg)
     written = cache.storage_bytes
     e0.record(stream)
     for i in range(256):
@@ -184,7 +198,7 @@ def prefill_c3(torch, dart, synthetic, stream, cfg: dict) -> dict:
     return {"workload": "C3 prefill: batch 8, 8 KV heads, 16384 tokens, head_dim 128, bf16, 2-bit + 25 %",
             "ms": round(ms, 3), "bytes_read": read, "bytes_written": written,
             "gbs": round((read + written) / (ms * 1e-3) / 1e9, 2),
-            "append_us": round(e0.elapsed_time(e1) / 256 * 1e3, 2)}
+            "append_us": round(e0.elapsed_time(e1) / 256 * 1e3, 2), "uniform_sweep": sweep}
 
 
 def config2_latency_us(torch, dart, synthetic, stream) -> float:

@@ -801,34 +801,55 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
   }
   __syncthreads();
 
-  // ---- 5. codes: thread (c, half) writes row bytes half * row_bytes / 2 .. ----
+  // ---- 5. codes: thread (c, half) packs row bytes half * row_bytes / 2 ..
+  // of channel c into registers; once every tile read is done the packed rows
+  // go through the tile's LDS (rows kCodePitch bytes apart, so the lanes'
+  // 16-byte writes fall in different banks) and leave in 16-byte stores of
+  // consecutive addresses ----
   {
     constexpr int per_byte = 8 / BITS, tpd = 4 * per_byte;  // tokens per code dword
-    constexpr int bpp = row_bytes / 2;
+    constexpr int bpp = row_bytes / 2, nw = bpp / 4;        // bytes and dwords per thread
+    constexpr int kCodePitch = row_bytes + 16;
+    static_assert(kFastKeyD * (BITS == 2 ? 2 : 1) * kCodePitch <= (int)sizeof(tile), "packed rows must fit the tile");
     const int sl = slot[c];
     const float qmax = mixed ? (sl >= 0 ? 15.0f : 3.0f) : (float)((1 << BITS) - 1);
     const float mn = ch_mn[c], s = ch_s[c], y = ch_y[c];
-    uint8_t* low = a.low + page * a.low_page_stride + (int64_t)bh * kFastKeyD * row_bytes + c * row_bytes + half * bpp;
-    uint8_t* high = mixed && sl >= 0
-                        ? a.high + page * a.high_page_stride + (int64_t)bh * K * row_bytes + sl * row_bytes + half * bpp
-                        : nullptr;
-#pragma unroll 2
-    for (int w = 0; w < bpp; w += 4) {
-      const int tb = (half * bpp + w) * per_byte;
+    uint32_t lo[nw], hi[nw];
+#pragma unroll
+    for (int w = 0; w < nw; ++w) {
+      const int tb = (half * bpp + 4 * w) * per_byte;
       float xs[tpd];
 #pragma unroll
       for (int j = 0; j < tpd; ++j) xs[j] = tile_x<SRC>(tile, min(tb + j, T - 1), c);  // padding repeats the last token
-      uint32_t lo = 0, hi = 0;
+      lo[w] = 0;
+      hi[w] = 0;
 #pragma unroll
       for (int j = 0; j < tpd; ++j) {
         const float diff = src_round<SRC>(xs[j] - mn);
         const float q = __builtin_rintf(src_round<SRC>(div_rn(diff, s, y)));
         const uint32_t code = (uint32_t)fminf(fmaxf(q, 0.0f), qmax);
-        lo |= (code & ((1u << BITS) - 1)) << (BITS * j);
-        if (BITS == 2) hi |= (code >> 2) << (2 * j);
+        lo[w] |= (code & ((1u << BITS) - 1)) << (BITS * j);
+        if (BITS == 2) hi[w] |= (code >> 2) << (2 * j);
       }
-      *(uint32_t*)(low + w) = lo;
-      if (high) *(uint32_t*)(high + w) = hi;
+    }
+    __syncthreads();  // the tile is read for the last time above
+    uint8_t* lowb = (uint8_t*)tile;                      // [128][kCodePitch]: low codes
+    uint8_t* highb = lowb + kFastKeyD * kCodePitch;      // [K][kCodePitch]: high codes of the promoted slots
+#pragma unroll
+    for (int w = 0; w < nw; w += 4) {
+      *(uint4*)(lowb + c * kCodePitch + half * bpp + 4 * w) = make_uint4(lo[w], lo[w + 1], lo[w + 2], lo[w + 3]);
+      if (mixed && sl >= 0)
+        *(uint4*)(highb + sl * kCodePitch + half * bpp + 4 * w) = make_uint4(hi[w], hi[w + 1], hi[w + 2], hi[w + 3]);
+    }
+    __syncthreads();
+    constexpr int q_row = row_bytes / 16;  // 16-byte pieces per packed row
+    uint4* low = (uint4*)(a.low + page * a.low_page_stride + (int64_t)bh * kFastKeyD * row_bytes);
+    for (int i = tid; i < kFastKeyD * q_row; i += kThreads)
+      low[i] = *(const uint4*)(lowb + (i / q_row) * kCodePitch + 16 * (i % q_row));
+    if (mixed && K > 0) {
+      uint4* high = (uint4*)(a.high + page * a.high_page_stride + (int64_t)bh * K * row_bytes);
+      for (int i = tid; i < K * q_row; i += kThreads)
+        high[i] = *(const uint4*)(highb + (i / q_row) * kCodePitch + 16 * (i % q_row));
     }
   }
 }

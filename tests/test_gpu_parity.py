@@ -169,6 +169,32 @@ def test_large_append_pages_bit_exact_vs_oracle(selection):
             assert bits_equal(a.cpu(), b)
 
 
+@pytest.mark.parametrize("bits,dtype", [(2, torch.bfloat16), (4, torch.float16), (8, torch.bfloat16),
+                                        (8, torch.float16)])
+def test_uniform_append_pages_bit_exact_vs_oracle(bits, dtype):
+    """Uniform 2/4/8-bit pages of head_dim 128 (the single-pass key page kernel, packed rows staged in LDS),
+    with a partial held page and the value rows: every packed field equals the oracle's."""
+    dart = _dkv()
+    from dartkv_amd import synthetic
+    from oracle import dart_oracle as O
+    k, v, _ = synthetic.outlier_kv(2, 4, 1100, 128, query_heads=8, dtype=dtype, seed=5 + bits)
+    cfg = dict(bits=bits, page_size=128, key_group_size=128, value_group_size=64, promote_ratio=0.0, sink_tokens=32,
+               hold_partial_pages=False, metadata_dtype=torch.float16)
+    print("case uniform", bits, dtype, flush=True)
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    cache.append(k.to(DEV), v.to(DEV))
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    oc.append(k, v)
+    torch.cuda.synchronize()
+    pairs = list(zip(cache.iter_segments(), oc.segments()))
+    assert len(pairs) == len(oc.segments()) == 1 + -(-(1100 - 32) // 128)
+    for (ks, vs), (oks, ovs) in pairs:
+        for a, b in zip(_seg_fields(ks).values(), _seg_fields(oks).values()):
+            assert bits_equal(a.cpu(), b)
+        for a, b in zip(_seg_fields(vs).values(), _seg_fields(ovs).values()):
+            assert bits_equal(a.cpu(), b)
+
+
 @pytest.mark.parametrize("name", ["c2", "c1", "nonheld", "held_mixed", "kitty_local", "kitty_value_local",
                                   "uniform_mix_bits"])
 def test_cache_pages_and_decode_vs_golden(golden, name):
