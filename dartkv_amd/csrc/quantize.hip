@@ -99,6 +99,19 @@ __device__ __forceinline__ float div_rn(float a, float b, float y) {
   return __builtin_fmaf(r, y, q);
 }
 
+// The group scale of dev_group_scale (round(round(max - min) / qmax) in the
+// source dtype, range clamped below by eps) with the division by qmax as
+// div_rn against y = RN(1 / qmax).  For qmax 3, 15 and 255 that equals the
+// IEEE quotient for every positive finite fp32 range (checked exhaustively
+// on the host); an infinite range keeps the IEEE result, infinity.
+template <int SRC>
+__device__ __forceinline__ float rows_group_scale(float mn, float mx, float qmax, float inv_qmax) {
+  float range = src_round<SRC>(mx - mn);
+  if (!(range >= quant_eps(SRC))) range = quant_eps(SRC);
+  const float d = range == INFINITY ? INFINITY : div_rn(range, qmax, inv_qmax);
+  return src_round<SRC>(d);
+}
+
 // Contiguous rows, groups of 8 * L elements (L = 1..64 lanes, a power of two)
 // that tile the row exactly: every lane owns 8 consecutive elements (one
 // 16-byte load for 16-bit sources), the L lanes of a group reduce min/max with
@@ -115,16 +128,20 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
   const int64_t lanes_per_row = p.n / 8;
   const int64_t total = p.block_rows * lanes_per_row;
   const float qmax = (float)((1 << BITS) - 1);
+  constexpr float inv_qmax = 1.0f / (float)((1 << BITS) - 1);  // RN(1 / qmax), folded at compile time
+  const int group_shift = __builtin_ctz((unsigned)lanes_per_group);
   const int lane = threadIdx.x & 63;
   for (int64_t blk = by; blk < p.blocks; blk += gy)
   for (int64_t v = bx * kThreads + threadIdx.x; v - lane < total; v += gx * kThreads) {
     // whole waves stay in the loop so the shuffles see every lane of a group
     const bool active = v < total;
-    int64_t r = 0, i0 = 0;  // row within the block, first element
+    int64_t r = 0;  // row within the block
+    int li = 0;     // lane item within the row: elements 8 li .. 8 li + 7
     if (active) {
       r = row_shift >= 0 ? v >> row_shift : v / lanes_per_row;
-      i0 = (v - r * lanes_per_row) * 8;
+      li = (int)(v - r * lanes_per_row);
     }
+    const int64_t i0 = 8 * li;
     const int64_t src_row = blk * p.block_stride + r * p.row_stride;
     float x[8];
     if (SRC == kF32) {
@@ -153,10 +170,10 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
     }
     if (!active) continue;
     r += blk * p.block_rows;  // output row
-    const float s = dev_group_scale(mn, mx, qmax, SRC);
+    const float s = rows_group_scale<SRC>(mn, mx, qmax, inv_qmax);
     const float y = __fdiv_rn(1.0f, s);
-    if (i0 % p.group == 0) {
-      const int64_t g = i0 / p.group;
+    if ((li & (lanes_per_group - 1)) == 0) {  // the group's first lane (groups are power-of-two lanes)
+      const int64_t g = li >> group_shift;
       dev_store_meta(p.scale, r * p.groups + g, s, p.meta_dtype);
       dev_store_meta(p.zero, r * p.groups + g, mn, p.meta_dtype);
     }
