@@ -32,8 +32,7 @@
 #define DKV_HD
 #endif
 #endif
-// Every step is inlined into the caller, so on the GPU the lane arrays' words
-// stay in registers.
+// Every step is inlined into its caller (the GPU kernels run it on LDS arrays).
 #define DKV_SEL DKV_HD inline __attribute__((always_inline))
 
 namespace dkv {
@@ -313,16 +312,15 @@ DKV_SEL void sel_topk(int n, int k, A work, S stack, int cap) {
 // `work` holds n (score[j], j) items already filled in; `stack` 3 * cap ints.
 // (A caller on the GPU passes LDS, so the kernel needs no private memory.)
 template <class It, class St>
-DKV_SEL void select_topk_filled(int n, int k, It work, int32_t* out_idx,
-                                                                     St stack, int cap = kSelStack) {
+DKV_SEL void select_topk_filled(int n, int k, It work, int32_t* out_idx, St stack, int cap = kSelStack) {
   const PtrArray<SelItem> w{&work[0]};
   sel_topk(n, k, w, PtrArray<int>{&stack[0]}, cap);
   for (int j = 0; j < k; ++j) out_idx[j] = w.get(j).i;
 }
 
 template <class It, class St>
-DKV_SEL void select_topk(const float* score, int n, int k, It work,
-                                                              int32_t* out_idx, St stack, int cap = kSelStack) {
+DKV_SEL void select_topk(const float* score, int n, int k, It work, int32_t* out_idx, St stack,
+                         int cap = kSelStack) {
   for (int j = 0; j < n; ++j) {
     work[j].v = score[j];
     work[j].i = j;
