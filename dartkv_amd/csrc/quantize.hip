@@ -621,12 +621,13 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_tiled(KeyParams k
 //      rule, not the exception (32 of 128 means in about one binade), so for
 //      many pages the launcher runs mode kKeyScores (steps 1-2, scores to the
 //      page's low-code region), key_select_pages (one lane per page) and mode
-//      kKeyCodes (steps 1, 4, 5 with the channels read back); mode kKeyAll
-//      does everything here (pages without a data-dependent selection, and the
-//      rank path with the one-lane fallback when few pages are quantized);
+//      kKeyCodes (steps 1, 4, 5 with the channels and the channel ranges read
+//      back); mode kKeyAll does everything here (pages without a
+//      data-dependent selection, and the rank path with the one-lane fallback
+//      when few pages are quantized);
 //   4. scales, zero points and one reciprocal per channel;
-//   5. codes: thread (c, quarter) quantizes 32 tokens of channel c with the
-//      exact chain (div_rn) and stores its 8 (2-bit) code bytes directly.
+//   5. codes: thread (c, half) quantizes 64 tokens of channel c with the
+//      exact chain (div_rn); the packed rows leave through LDS.
 constexpr int kFastKeyD = 128, kFastKeyT = 128;
 
 template <int SRC>
@@ -729,7 +730,7 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
   const int c = tid & (kFastKeyD - 1), half = tid >> 7;
   const bool select = mixed && K > 0 && K < kFastKeyD && a.selection != DKV_SELECT_GIVEN && mode != kKeyCodes;
   const bool magnitude = a.selection == DKV_SELECT_MAGNITUDE;
-  {
+  if (mode != kKeyCodes) {  // the codes pass reads the channel min / max its scores pass stored
     float mn = INFINITY, mx = -INFINITY;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -759,13 +760,27 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
     }
   }
   __syncthreads();
+  // kKeyScores leaves [score | min | max] x 128 floats at the start of the
+  // page's low-code region (1.5 KiB of its 128 x row_bytes); kKeyCodes reads
+  // min and max back and overwrites the region with the codes
+  static_assert(3 * kFastKeyD * 4 <= kFastKeyD * row_bytes, "scores and ranges must fit the low-code region");
+  float* stash = (float*)(a.low + page * a.low_page_stride + (int64_t)bh * kFastKeyD * row_bytes);
   if (mode == kKeyScores) {
-    if (half == 0) ((float*)(a.low + page * a.low_page_stride + (int64_t)bh * kFastKeyD * row_bytes))[c] = score[c];
+    if (half == 0) {
+      stash[c] = score[c];
+      stash[kFastKeyD + c] = fminf(part_mn[0][c], part_mn[1][c]);
+      stash[2 * kFastKeyD + c] = fmaxf(part_mx[0][c], part_mx[1][c]);
+    }
     return;
   }
   if (half == 0) {
-    ch_mn[c] = fminf(part_mn[0][c], part_mn[1][c]);
-    ch_s[c] = fmaxf(part_mx[0][c], part_mx[1][c]);  // max for now
+    if (mode == kKeyCodes) {
+      ch_mn[c] = stash[kFastKeyD + c];
+      ch_s[c] = stash[2 * kFastKeyD + c];  // max for now
+    } else {
+      ch_mn[c] = fminf(part_mn[0][c], part_mn[1][c]);
+      ch_s[c] = fmaxf(part_mx[0][c], part_mx[1][c]);  // max for now
+    }
   }
 
   // ---- 3. channel selection ----
