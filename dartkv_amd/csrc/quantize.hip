@@ -897,27 +897,37 @@ constexpr int kSelectMaxD = 128;
 constexpr int kSelectStack = 16;  // >= 2 floor(log2(kSelectMaxD)) + 1
 
 // Page `item` (page-major over (b, h)): the lanes of one wave stage its scores
-// in `work`, then lane 0 runs the exact selection and writes the indices.
-__device__ __forceinline__ void select_page(const KeyParams& k, int row_bytes, int64_t item, int lane, SelItem* work,
-                                            int* stack) {
+// in `sc` and turn each into a packed (rank, index) word in `work` (the rank
+// orders and ties exactly like the score), then lane 0 runs the exact
+// selection on the words (one 4-byte LDS access and an integer compare per
+// step) and writes the indices.
+__device__ __forceinline__ void select_page(const KeyParams& k, int row_bytes, int64_t item, int lane,
+                                            PackedItem* work, float* sc, int* stack) {
   const dkv_key_pages_args& a = k.a;
   const int64_t bhs = a.B * a.H;
   const int64_t page = item / bhs, bh = item % bhs;
   const int D = (int)a.D, K = (int)a.promoted;
   const float* score = (const float*)(a.low + page * a.low_page_stride + bh * D * row_bytes);
-  for (int j = lane; j < D; j += 64) work[j] = SelItem{score[j], j};
+  for (int j = lane; j < D; j += 64) sc[j] = score[j];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (int j = lane; j < D; j += 64) work[j] = PackedItem{(sel_rank(sc[j], sc, D) << 7) | (uint32_t)j};
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (lane != 0) return;
   int32_t* idx_out = (int32_t*)((char*)a.idx + page * a.idx_page_stride) + bh * K;
-  select_topk_filled(D, K, work, idx_out, stack, kSelectStack);
+  const PtrArray<PackedItem> w{work};
+  sel_topk(D, K, w, PtrArray<int>{stack}, kSelectStack);
+  for (int j = 0; j < K; ++j) idx_out[j] = (int32_t)(w.get(j).k & 127u);
 }
 
 __global__ void __launch_bounds__(64) key_select_pages(KeyParams k, int row_bytes) {
-  __shared__ SelItem work[kSelectMaxD];
+  __shared__ PackedItem work[kSelectMaxD];
+  __shared__ float sc[kSelectMaxD];
   __shared__ int stack[3 * kSelectStack];
-  select_page(k, row_bytes, blockIdx.x, threadIdx.x, work, stack);
+  select_page(k, row_bytes, blockIdx.x, threadIdx.x, work, sc, stack);
 }
 
 // The key path's channel selection and a value-row job in one launch.
@@ -935,12 +945,13 @@ template <int BITS, int SRC>
 __global__ void __launch_bounds__(kThreads) select_pages_and_rows(KeyParams k, int row_bytes, int64_t items,
                                                                   int64_t sel_blocks, RowsParams p, int lpg,
                                                                   int row_shift, int64_t gx, int64_t gy) {
-  __shared__ SelItem work[kSelectWaves][kSelectMaxD];
+  __shared__ PackedItem work[kSelectWaves][kSelectMaxD];
+  __shared__ float sc[kSelectWaves][kSelectMaxD];
   __shared__ int stack[kSelectWaves][3 * kSelectStack];
   if ((int64_t)blockIdx.x < sel_blocks) {
     const int wave = threadIdx.x >> 6;
     const int64_t item = (int64_t)blockIdx.x * kSelectWaves + wave;
-    if (item < items) select_page(k, row_bytes, item, threadIdx.x & 63, work[wave], stack[wave]);
+    if (item < items) select_page(k, row_bytes, item, threadIdx.x & 63, work[wave], sc[wave], stack[wave]);
     return;
   }
   const int64_t b = (int64_t)blockIdx.x - sel_blocks;
