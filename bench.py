@@ -325,6 +325,7 @@ def main() -> int:
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="after timing, copy a MIB-MiB buffer 3 times (known bytes for PMC counter calibration)")
     p.add_argument("--no-c4", action="store_true", help="skip the C4 Qwen3-8B-shaped decode leg")
+    p.add_argument("--c3-only", action="store_true", help="run only the C3 prefill leg and print its JSON")
     p.add_argument("--c4-only", action="store_true", help="run only the C4 leg and print its JSON")
     p.add_argument("--c4-steps", type=int, default=128)
     p.add_argument("--c4-prompt", type=int, default=8192)
@@ -339,6 +340,12 @@ def main() -> int:
 
     import dartkv_amd as dart
     from dartkv_amd import synthetic
+
+    if args.c3_only:
+        c3cfg = config_for(args.bits)
+        c3cfg["metadata_dtype"] = torch.float16
+        print(json.dumps(prefill_c3(torch, dart, synthetic, torch.cuda.current_stream(), c3cfg)), flush=True)
+        return 0
 
     if args.c4_only:
         print(json.dumps(decode_c4(torch, dart, prompt=args.c4_prompt, steps=args.c4_steps, graph=not args.c4_eager)),
