@@ -26,7 +26,7 @@ KEY_DENSE, KEY_UNIFORM, KEY_MIXED = 0, 1, 2
 VALUE_DENSE, VALUE_UNIFORM = 0, 1
 SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
@@ -45,7 +45,7 @@ class ValueRowsArgs(ctypes.Structure):
         ("n", ctypes.c_int64), ("row_stride", ctypes.c_int64),
         ("bits", ctypes.c_int64), ("group", ctypes.c_int64),
         ("values", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("zero", ctypes.c_void_p),
-        ("meta_dtype", ctypes.c_int64),
+        ("meta_dtype", ctypes.c_int64), ("nonfinite", ctypes.c_void_p),
     ]
 
 
@@ -64,6 +64,7 @@ class KeyPagesArgs(ctypes.Structure):
         ("scale", ctypes.c_void_p), ("scale_page_stride", ctypes.c_int64),
         ("zero", ctypes.c_void_p), ("zero_page_stride", ctypes.c_int64),
         ("values", ctypes.c_void_p),  # const dkv_value_rows_args* (optional)
+        ("nonfinite", ctypes.c_void_p),  # uint32_t* (optional)
     ]
 
 
@@ -113,7 +114,8 @@ class DecodePrepArgs(ctypes.Structure):
 
 
 EXPORTED = (
-    "dkv_last_error", "dkv_abi_version", "dkv_quantize_rows", "dkv_quantize_row_blocks", "dkv_quantize_key_pages",
+    "dkv_last_error", "dkv_abi_version", "dkv_quantize_rows", "dkv_quantize_row_blocks", "dkv_quantize_value_rows",
+    "dkv_quantize_key_pages",
     "dkv_dequantize_rows",
     "dkv_dequantize_mixed", "dkv_decode_workspace_bytes", "dkv_decode_attention", "dkv_decode_prep",
 )
@@ -140,6 +142,7 @@ def load() -> ctypes.CDLL:
         lib.dkv_abi_version.restype = ctypes.c_int
         lib.dkv_quantize_rows.argtypes = [vp, i32, i64, i64, i64, i64, i32, i64, vp, vp, vp, i32, vp]
         lib.dkv_quantize_row_blocks.argtypes = [vp, i32, i64, i64, i64, i64, i64, i32, i64, vp, vp, vp, i32, vp]
+        lib.dkv_quantize_value_rows.argtypes = [ctypes.POINTER(ValueRowsArgs), vp]
         lib.dkv_quantize_key_pages.argtypes = [ctypes.POINTER(KeyPagesArgs), vp]
         lib.dkv_dequantize_rows.argtypes = [vp, vp, vp, i32, i64, i64, i32, i64, vp, i32, i64, vp]
         lib.dkv_dequantize_mixed.argtypes = [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, vp, i32, vp]
@@ -147,7 +150,8 @@ def load() -> ctypes.CDLL:
         lib.dkv_decode_workspace_bytes.restype = i64
         lib.dkv_decode_attention.argtypes = [ctypes.POINTER(DecodeArgs), vp]
         lib.dkv_decode_prep.argtypes = [ctypes.POINTER(DecodePrepArgs), vp]
-        for name in ("dkv_quantize_rows", "dkv_quantize_row_blocks", "dkv_quantize_key_pages", "dkv_dequantize_rows",
+        for name in ("dkv_quantize_rows", "dkv_quantize_row_blocks", "dkv_quantize_value_rows", "dkv_quantize_key_pages",
+                     "dkv_dequantize_rows",
                      "dkv_dequantize_mixed", "dkv_decode_attention", "dkv_decode_prep"):
             getattr(lib, name).restype = ctypes.c_int
         if lib.dkv_abi_version() != ABI_VERSION:

@@ -2,7 +2,8 @@
 
     python -m dartkv_amd.build
 
-Sources are compiled together by one hipcc invocation.  Flags:
+Each source is compiled to an object by its own hipcc process (in parallel),
+then the objects are linked into the shared library.  Flags:
 * ``-ffp-contract=off``: the quantizer and the dequantization chain must
   round after every multiply and add, like the reference's separate torch ops;
 * ``-Xclang -target-feature -Xclang -packed-fp32-ops``: no packed-fp32 VALU ops.
@@ -13,6 +14,8 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
@@ -28,26 +31,39 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def command(output: str = LIB) -> list[str]:
+def compile_flags() -> list[str]:
     return [
-        hipcc(), "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC", "-shared",
+        "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC",
         "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
         "-I", os.path.join(os.path.dirname(PKG), "include"),
-        *[os.path.join(CSRC, s) for s in SOURCES],
-        "-o", output,
     ]
 
 
-def build(verbose: bool = False) -> str:
-    tmp = LIB + ".tmp"
-    cmd = command(tmp)
+def command(output: str = LIB) -> list[str]:
+    """One hipcc line that compiles and links every source (the serial form of build())."""
+    return [hipcc(), *compile_flags(), "-shared", *[os.path.join(CSRC, s) for s in SOURCES], "-o", output]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
+        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}: {' '.join(cmd[-3:])}")
+
+
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    jobs = jobs or min(len(SOURCES), max(1, min(8, len(os.sched_getaffinity(0)))))
+    with tempfile.TemporaryDirectory(prefix="dkv_build_") as tmpdir:
+        objs = [os.path.join(tmpdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+        cmds = [[hipcc(), *compile_flags(), "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            for fut in [pool.submit(_run, c, verbose) for c in cmds]:
+                fut.result()
+        tmp = LIB + ".tmp"
+        _run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", *objs, "-o", tmp], verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -7,7 +7,7 @@ page merging and union-boundary segment iteration.  What differs is where
 the work happens:
 
 * every page of one append is quantized by one ``dkv_quantize_key_pages``
-  launch (keys along tokens) and one ``dkv_quantize_row_blocks`` launch
+  launch (keys along tokens) that also quantizes the values
   (values along head_dim, read in place from the appended tensor's token
   slice); page fields are views into page-major chunk tensors;
 * the held partial page lives in a preallocated tail buffer, so a one-token
@@ -18,6 +18,7 @@ the work happens:
 
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass
 from typing import TYPE_CHECKING, List, Optional, Tuple, Union
 
@@ -273,6 +274,9 @@ class DartKVCache:
         self._random_channels: Optional[torch.Tensor] = None
         # device copy of the held tail's length (replayable decode steps); None when off
         self._tail_count_dev: Optional[torch.Tensor] = None
+        # int32 [2] device flags (keys, values) the quantize kernels set on a NaN or an infinity
+        self._nonfinite: Optional[torch.Tensor] = None
+        self._nonfinite_ptrs: Tuple[int, int] = (0, 0)
 
     # ---- reference properties ----
     @property
@@ -594,25 +598,52 @@ class DartKVCache:
         if self._pending_value is not None:
             value_states = torch.cat((self._pending_value, value_states), dim=-2)
         quantized = max(0, value_states.shape[-2] - c.value_local_tokens)
-        for start in range(0, quantized, c.page_size):
-            stop = min(start + c.page_size, quantized)
-            for seg in self._quantize_value_chunks(value_states[..., start:stop, :], stop - start):
-                self._append_quantized_value_page(seg)
+        if quantized:
+            with self._finite_inputs():
+                for start in range(0, quantized, c.page_size):
+                    stop = min(start + c.page_size, quantized)
+                    for seg in self._quantize_value_chunks(value_states[..., start:stop, :], stop - start):
+                        self._append_quantized_value_page(seg)
         self._pending_value = value_states[..., quantized:, :].clone() if quantized < value_states.shape[-2] else None
+
+    @contextlib.contextmanager
+    def _finite_inputs(self):
+        """Quantize launches inside this scope report NaN or infinite inputs through device flags;
+        on exit the flags are read (one host synchronization) and such an input raises the reference's
+        ValueError (quantization.py:159-160, mixed.py:187-188) with the segment lists restored."""
+        flags = self._nonfinite
+        if flags is None or flags.device != self._device:
+            flags = self._nonfinite = torch.zeros(2, dtype=torch.int32, device=self._device)
+        else:
+            flags.zero_()
+        keys, values = list(self._key_segments), list(self._value_segments)
+        self._nonfinite_ptrs = (flags.data_ptr(), flags.data_ptr() + 4)
+        try:
+            yield
+        finally:
+            self._nonfinite_ptrs = (0, 0)
+        bad_keys, bad_values = flags.tolist()
+        if bad_keys or bad_values:
+            self._key_segments, self._value_segments = keys, values
+            if bad_keys and self.config.promote_ratio > 0.0:
+                raise ValueError("key_states must contain finite values")
+            raise ValueError("quantize expects all values to be finite")
 
     def _quantize_pages(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         """Quantize consecutive pages; the last may be partial (reference cache.py:472-479)."""
         if key_states.shape[-2] != value_states.shape[-2]:
             raise RuntimeError("key/value page lengths diverged before quantization")
-        jobs: list = []
-        values = self._quantize_value_chunks(value_states, self.config.page_size, jobs)
-        keys = self._quantize_key_chunks(key_states, jobs)
-        for kseg, vseg in zip(keys, values):
-            self._key_segments.append(kseg)
-            self._append_quantized_value_page(vseg)
+        with self._finite_inputs():
+            jobs: list = []
+            values = self._quantize_value_chunks(value_states, self.config.page_size, jobs)
+            keys = self._quantize_key_chunks(key_states, jobs)
+            for kseg, vseg in zip(keys, values):
+                self._key_segments.append(kseg)
+                self._append_quantized_value_page(vseg)
 
     def _key_pages_only(self, key_states: torch.Tensor) -> None:
-        self._key_segments.extend(self._quantize_key_chunks(key_states))
+        with self._finite_inputs():
+            self._key_segments.extend(self._quantize_key_chunks(key_states))
 
     def _quantize_key_chunks(self, key_states: torch.Tensor, value_jobs: Optional[list] = None) -> List[Segment]:
         """Key pages of ``page_size`` tokens (last may be shorter), one launch per page size.
@@ -672,12 +703,14 @@ class DartKVCache:
                                      key_mode=_lib.KEY_MIXED, bits=2, group=kg, promoted=K, selection=selection,
                                      given_idx=given[p].contiguous(), meta=meta, low=low[p], high=high[p],
                                      idx=idx[p], scale=scale[p], zero=zero[p],
-                                     values=values if p == n_pages - 1 else None)
+                                     values=values if p == n_pages - 1 else None,
+                                     nonfinite=self._nonfinite_ptrs[0])
             else:
                 launch_key_pages(src, page_tokens=tokens, n_pages=n_pages, key_mode=_lib.KEY_MIXED, bits=2,
                                  group=kg, promoted=K, selection=selection,
                                  given_idx=None if given is None else given[0].contiguous(), meta=meta,
-                                 low=low, high=high, idx=idx, scale=scale, zero=zero, values=values)
+                                 low=low, high=high, idx=idx, scale=scale, zero=zero, values=values,
+                                 nonfinite=self._nonfinite_ptrs[0])
             run = _PageRun(dict(low_values=low, high_values=high, channel_indices=idx, scale=scale, zero_point=zero),
                            0, 1, dict(original_shape=(B, H, tokens, D), padded_tokens=G * kg, group_size=kg,
                                       low_bits=2, promote_bits=c.promote_bits, output_dtype=src.dtype))
@@ -691,7 +724,7 @@ class DartKVCache:
         zero = torch.empty(n_pages, B, H, D, G, dtype=meta, device=dev)
         launch_key_pages(src, page_tokens=tokens, n_pages=n_pages, key_mode=_lib.KEY_UNIFORM, bits=bits, group=kg,
                          promoted=0, selection=0, given_idx=None, meta=meta, low=codes, high=None, idx=None,
-                         scale=scale, zero=zero, values=values)
+                         scale=scale, zero=zero, values=values, nonfinite=self._nonfinite_ptrs[0])
         run = _PageRun(dict(values=codes, scale=scale, zero_point=zero), 0, 1,
                        dict(original_shape=(B, H, tokens, D), original_dim=tokens, padded_dim=padded,
                             packed_dim=packed_dim, group_size=kg, bits=bits, output_dtype=src.dtype, axis=2))
@@ -725,9 +758,9 @@ class DartKVCache:
             scale = torch.empty(B, H, n, Gv, dtype=meta, device=dev)
             zero = torch.empty(B, H, n, Gv, dtype=meta, device=dev)
             if jobs is None:
-                _launch_value_rows(src, bits, vg, meta, values, scale, zero)
+                _launch_value_rows(src, bits, vg, meta, values, scale, zero, self._nonfinite_ptrs[1])
             else:
-                job, keep = _value_rows_job(src, bits, vg, meta, values, scale, zero)
+                job, keep = _value_rows_job(src, bits, vg, meta, values, scale, zero, self._nonfinite_ptrs[1])
                 jobs.append((start, n, job, keep))
             run = _PageRun(dict(values=values, scale=scale, zero_point=zero), 2, size,
                            dict(original_shape=(B, H, size, D), original_dim=D, padded_dim=padded,
@@ -887,12 +920,13 @@ class DartKVCache:
 # ---------------------------------------------------------------------------
 
 def _value_rows_job(src: torch.Tensor, bits: int, group: int, meta: torch.dtype, values: torch.Tensor,
-                    scale: torch.Tensor, zero: torch.Tensor):
+                    scale: torch.Tensor, zero: torch.Tensor, nonfinite: int = 0):
     """The C description of quantizing [B,H,T,D] value rows along head_dim.
 
     A token slice of a [B,H,T',D] tensor is B*H blocks of T contiguous rows;
     the kernel reads it in place.  Other layouts are copied first.  Returns
     (``_lib.ValueRowsArgs``, the source tensor to keep alive until launch).
+    ``nonfinite`` is the address of a device uint32 flag (0: no check).
     """
     B, H, T, D = src.shape
     sb, sh, st, sd = src.stride()
@@ -911,19 +945,16 @@ def _value_rows_job(src: torch.Tensor, bits: int, group: int, meta: torch.dtype,
     job = _lib.ValueRowsArgs(src=src.data_ptr(), src_dtype=_lib.dtype_code(src.dtype), blocks=blocks,
                              block_stride=block_stride, block_rows=T, n=D, row_stride=D, bits=bits, group=group,
                              values=values.data_ptr(), scale=scale.data_ptr(), zero=zero.data_ptr(),
-                             meta_dtype=_lib.dtype_code(meta))
+                             meta_dtype=_lib.dtype_code(meta), nonfinite=nonfinite or None)
     return job, src
 
 
 def _launch_value_rows(src: torch.Tensor, bits: int, group: int, meta: torch.dtype, values: torch.Tensor,
-                       scale: torch.Tensor, zero: torch.Tensor) -> None:
-    """Quantize [B,H,T,D] value rows along head_dim (dkv_quantize_row_blocks)."""
-    job, src = _value_rows_job(src, bits, group, meta, values, scale, zero)
+                       scale: torch.Tensor, zero: torch.Tensor, nonfinite: int = 0) -> None:
+    """Quantize [B,H,T,D] value rows along head_dim (dkv_quantize_value_rows)."""
+    job, src = _value_rows_job(src, bits, group, meta, values, scale, zero, nonfinite)
     lib = _lib.load()
-    rc = lib.dkv_quantize_row_blocks(job.src, job.src_dtype, job.blocks, job.block_stride, job.block_rows, job.n,
-                                     job.row_stride, job.bits, job.group, job.values, job.scale, job.zero,
-                                     job.meta_dtype, _lib.stream_ptr(src.device))
-    _lib.check(rc, "dkv_quantize_row_blocks")
+    _lib.check(lib.dkv_quantize_value_rows(job, _lib.stream_ptr(src.device)), "dkv_quantize_value_rows")
 
 
 def _materialize(segment: Segment) -> torch.Tensor:

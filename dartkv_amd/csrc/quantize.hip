@@ -22,6 +22,20 @@ namespace {
 
 constexpr int kThreads = 256;
 
+// Group minimum / maximum that propagate NaN (v_minimum3_f32 / v_maximum3_f32
+// on gfx950; on finite values they equal fminf / fmaxf).  A group holding a
+// NaN or an infinity therefore ends with a non-finite min or max, and
+// flag_nonfinite reports it: the reference rejects such inputs
+// (quantization.py:159-160, mixed.py:187-188).
+__device__ __forceinline__ float nmin(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ float nmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// flag (may be NULL) := 1 when a group's min or max is not finite.  Every
+// writer stores the same value, with a vector store.
+__device__ __forceinline__ void flag_nonfinite(uint32_t* flag, float mn, float mx) {
+  if (flag != nullptr && !(__builtin_isfinite(mn) && __builtin_isfinite(mx))) *flag = 1u;
+}
+
 // ---------------------------------------------------------------------------
 // rows
 // ---------------------------------------------------------------------------
@@ -37,6 +51,7 @@ struct RowsParams {
   uint8_t* values;
   void* scale;
   void* zero;
+  uint32_t* nonfinite;  // optional flag, set when a group holds a non-finite value
 };
 
 __device__ __forceinline__ float row_elem(const RowsParams& p, int64_t r, int64_t i) {
@@ -50,9 +65,10 @@ __device__ __forceinline__ void group_stats(const RowsParams& p, int64_t r, int6
   float mn = row_elem(p, r, g * p.group), mx = mn;
   for (int64_t j = 1; j < p.group; ++j) {
     const float x = row_elem(p, r, g * p.group + j);
-    mn = fminf(mn, x);
-    mx = fmaxf(mx, x);
+    mn = nmin(mn, x);
+    mx = nmax(mx, x);
   }
+  flag_nonfinite(p.nonfinite, mn, mx);
   const float s = dev_group_scale(mn, mx, qmax, p.src_dtype);
   dev_store_meta(p.scale, r * p.groups + g, s, p.meta_dtype);
   dev_store_meta(p.zero, r * p.groups + g, mn, p.meta_dtype);
@@ -161,12 +177,12 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
     float mn = x[0], mx = x[0];
 #pragma unroll
     for (int j = 1; j < 8; ++j) {
-      mn = fminf(mn, x[j]);
-      mx = fmaxf(mx, x[j]);
+      mn = nmin(mn, x[j]);
+      mx = nmax(mx, x[j]);
     }
     for (int off = 1; off < lanes_per_group; off <<= 1) {
-      mn = fminf(mn, __shfl_xor(mn, off, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      mn = nmin(mn, __shfl_xor(mn, off, 64));
+      mx = nmax(mx, __shfl_xor(mx, off, 64));
     }
     if (!active) continue;
     r += blk * p.block_rows;  // output row
@@ -176,6 +192,7 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
       const int64_t g = li >> group_shift;
       dev_store_meta(p.scale, r * p.groups + g, s, p.meta_dtype);
       dev_store_meta(p.zero, r * p.groups + g, mn, p.meta_dtype);
+      flag_nonfinite(p.nonfinite, mn, mx);
     }
     uint32_t packed[2] = {0u, 0u};  // codes 0..3 and 4..7 for 8-bit, else all in [0]
 #pragma unroll
@@ -356,9 +373,10 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_kernel(KeyParams 
         float mx = mn;
         for (int64_t j = 1; j < group; ++j) {
           const float x = key_elem(k, b, h, page, g * group + j, c);
-          mn = fminf(mn, x);
-          mx = fmaxf(mx, x);
+          mn = nmin(mn, x);
+          mx = nmax(mx, x);
         }
+        flag_nonfinite(a.nonfinite, mn, mx);
         s = dev_group_scale(mn, mx, qmax, dt);
         dev_store_meta(scale, meta_base + g, s, meta);
         dev_store_meta(zero, meta_base + g, mn, meta);
@@ -390,9 +408,10 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_kernel(KeyParams 
             float mx = mn;
             for (int64_t q = 1; q < group; ++q) {
               const float x = key_elem(k, b, h, page, g * group + q, c);
-              mn = fminf(mn, x);
-              mx = fmaxf(mx, x);
+              mn = nmin(mn, x);
+              mx = nmax(mx, x);
             }
+            flag_nonfinite(a.nonfinite, mn, mx);
             s = dev_group_scale(mn, mx, qmax, dt);
             dev_store_meta(scale, meta_base + g, s, meta);
             dev_store_meta(zero, meta_base + g, mn, meta);
@@ -502,9 +521,10 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_tiled(KeyParams k
       float mn = tile_elem(tile, rs, T, g * group, c, dt), mx = mn;
       for (int j = 1; j < group; ++j) {
         const float x = tile_elem(tile, rs, T, g * group + j, c, dt);
-        mn = fminf(mn, x);
-        mx = fmaxf(mx, x);
+        mn = nmin(mn, x);
+        mx = nmax(mx, x);
       }
+      if (mode != kKeyCodes) flag_nonfinite(a.nonfinite, mn, mx);
       mn_s[c * G + g] = mn;
       sc_s[c * G + g] = mx;  // max for now; the scale needs qmax, known after selection
     }
@@ -652,8 +672,8 @@ __device__ __forceinline__ float key_chunk_sum(const uint16_t* tile, int c, int 
   for (int j = 0; j < 16; ++j) {
     const float x = xs[j];
     if (MINMAX) {
-      mn = fminf(mn, x);
-      mx = fmaxf(mx, x);
+      mn = nmin(mn, x);
+      mx = nmax(mx, x);
     }
     float term = x;
     if (mode == 0) term = fabsf(x);
@@ -767,9 +787,11 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
   float* stash = (float*)(a.low + page * a.low_page_stride + (int64_t)bh * kFastKeyD * row_bytes);
   if (mode == kKeyScores) {
     if (half == 0) {
+      const float mn = nmin(part_mn[0][c], part_mn[1][c]), mx = nmax(part_mx[0][c], part_mx[1][c]);
       stash[c] = score[c];
-      stash[kFastKeyD + c] = fminf(part_mn[0][c], part_mn[1][c]);
-      stash[2 * kFastKeyD + c] = fmaxf(part_mx[0][c], part_mx[1][c]);
+      stash[kFastKeyD + c] = mn;
+      stash[2 * kFastKeyD + c] = mx;
+      flag_nonfinite(a.nonfinite, mn, mx);
     }
     return;
   }
@@ -778,8 +800,9 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
       ch_mn[c] = stash[kFastKeyD + c];
       ch_s[c] = stash[2 * kFastKeyD + c];  // max for now
     } else {
-      ch_mn[c] = fminf(part_mn[0][c], part_mn[1][c]);
-      ch_s[c] = fmaxf(part_mx[0][c], part_mx[1][c]);  // max for now
+      ch_mn[c] = nmin(part_mn[0][c], part_mn[1][c]);
+      ch_s[c] = nmax(part_mx[0][c], part_mx[1][c]);  // max for now
+      flag_nonfinite(a.nonfinite, ch_mn[c], ch_s[c]);
     }
   }
 
@@ -1034,7 +1057,7 @@ struct RowsLaunch {
 // Validate a value-row job and plan its launch (nothing is launched).
 static int prepare_rows(const void* src, int src_dtype, int64_t blocks, int64_t block_stride, int64_t block_rows,
                         int64_t n, int64_t row_stride, int64_t elem_stride, int bits, int64_t group, uint8_t* values,
-                        void* scale, void* zero, int meta_dtype, RowsLaunch& L) {
+                        void* scale, void* zero, int meta_dtype, uint32_t* nonfinite, RowsLaunch& L) {
   const int64_t rows = blocks * block_rows;
   DKV_CHECK(valid_float_dtype(src_dtype), DKV_ERR_DTYPE, "quantize expects a floating-point tensor (f32/f16/bf16)");
   DKV_CHECK(valid_meta_dtype(meta_dtype), DKV_ERR_DTYPE, "metadata dtype must be floating point");
@@ -1061,6 +1084,7 @@ static int prepare_rows(const void* src, int src_dtype, int64_t blocks, int64_t 
   p.values = values;
   p.scale = scale;
   p.zero = zero;
+  p.nonfinite = nonfinite;
   L.rows = rows;
   L.bits = bits;
   L.src_dtype = src_dtype;
@@ -1111,11 +1135,11 @@ static void launch_rows(const RowsLaunch& L, hipStream_t s) {
 
 static int quantize_rows_impl(const void* src, int src_dtype, int64_t blocks, int64_t block_stride,
                               int64_t block_rows, int64_t n, int64_t row_stride, int64_t elem_stride, int bits,
-                              int64_t group, uint8_t* values, void* scale, void* zero, int meta_dtype, void* stream,
-                              const char* name) {
+                              int64_t group, uint8_t* values, void* scale, void* zero, int meta_dtype,
+                              uint32_t* nonfinite, void* stream, const char* name) {
   RowsLaunch L;
   const int rc = prepare_rows(src, src_dtype, blocks, block_stride, block_rows, n, row_stride, elem_stride, bits,
-                              group, values, scale, zero, meta_dtype, L);
+                              group, values, scale, zero, meta_dtype, nonfinite, L);
   if (rc != DKV_OK) return rc;
   if (L.rows == 0) return DKV_OK;
   launch_rows(L, (hipStream_t)stream);
@@ -1127,7 +1151,7 @@ extern "C" int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, i
                                  void* zero, int meta_dtype, void* stream) {
   DKV_CHECK(rows >= 0, DKV_ERR_INVALID, "rows must be non-negative");
   return quantize_rows_impl(src, src_dtype, 1, 0, rows, n, row_stride, elem_stride, bits, group, values, scale, zero,
-                            meta_dtype, stream, "dkv_quantize_rows");
+                            meta_dtype, nullptr, stream, "dkv_quantize_rows");
 }
 
 extern "C" int dkv_quantize_row_blocks(const void* src, int src_dtype, int64_t blocks, int64_t block_stride,
@@ -1136,7 +1160,17 @@ extern "C" int dkv_quantize_row_blocks(const void* src, int src_dtype, int64_t b
   DKV_CHECK(blocks >= 0 && block_rows >= 0, DKV_ERR_INVALID, "blocks and block_rows must be non-negative");
   DKV_CHECK(block_rows == 0 || blocks <= INT64_MAX / block_rows, DKV_ERR_INVALID, "blocks * block_rows overflows");
   return quantize_rows_impl(src, src_dtype, blocks, block_stride, block_rows, n, row_stride, 1, bits, group, values,
-                            scale, zero, meta_dtype, stream, "dkv_quantize_row_blocks");
+                            scale, zero, meta_dtype, nullptr, stream, "dkv_quantize_row_blocks");
+}
+
+extern "C" int dkv_quantize_value_rows(const dkv_value_rows_args* args, void* stream) {
+  DKV_CHECK(args != nullptr, DKV_ERR_INVALID, "args is NULL");
+  const dkv_value_rows_args& v = *args;
+  DKV_CHECK(v.blocks >= 0 && v.block_rows >= 0, DKV_ERR_INVALID, "blocks and block_rows must be non-negative");
+  DKV_CHECK(v.block_rows == 0 || v.blocks <= INT64_MAX / v.block_rows, DKV_ERR_INVALID, "blocks * block_rows overflows");
+  return quantize_rows_impl(v.src, (int)v.src_dtype, v.blocks, v.block_stride, v.block_rows, v.n, v.row_stride, 1,
+                            (int)v.bits, v.group, v.values, v.scale, v.zero, (int)v.meta_dtype, v.nonfinite, stream,
+                            "dkv_quantize_value_rows");
 }
 
 extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stream) {
@@ -1169,7 +1203,7 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
     DKV_CHECK(v.block_rows == 0 || v.blocks <= INT64_MAX / v.block_rows, DKV_ERR_INVALID,
               "value blocks * block_rows overflows");
     const int rc = prepare_rows(v.src, (int)v.src_dtype, v.blocks, v.block_stride, v.block_rows, v.n, v.row_stride, 1,
-                                (int)v.bits, v.group, v.values, v.scale, v.zero, (int)v.meta_dtype, VL);
+                                (int)v.bits, v.group, v.values, v.scale, v.zero, (int)v.meta_dtype, v.nonfinite, VL);
     if (rc != DKV_OK) return rc;
   }
   hipStream_t s = (hipStream_t)stream;

@@ -82,6 +82,10 @@ class MixedQuantizedKey:
     def dequantize(self, *, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
         """Materialize [B,H,T,D] on the device (reference mixed.py:72-94 semantics)."""
         out_dtype = dtype or self.output_dtype
+        if self.low_values.device.type == "cpu":
+            # host-resident pages (a cache moved with .to("cpu")): dequantized on the current GPU
+            gpu = torch.device("cuda", torch.cuda.current_device())
+            return self.to(gpu).dequantize(dtype=dtype).cpu()
         _lib.require_device(self.low_values)
         B, H, T, D = self.original_shape
         kernel_dtype = out_dtype if out_dtype in (torch.float32, torch.float16, torch.bfloat16) else torch.float32
@@ -213,13 +217,14 @@ def quantize_key_mixed(
 def launch_key_pages(src: torch.Tensor, *, page_tokens: int, n_pages: int, key_mode: int, bits: int, group: int,
                      promoted: int, selection: int, given_idx: Optional[torch.Tensor], meta: torch.dtype,
                      low: torch.Tensor, high: Optional[torch.Tensor], idx: Optional[torch.Tensor],
-                     scale: torch.Tensor, zero: torch.Tensor, values=None) -> None:
+                     scale: torch.Tensor, zero: torch.Tensor, values=None, nonfinite: int = 0) -> None:
     """Quantize ``n_pages`` pages of keys from ``src`` [B,H,T,D] into page-major outputs.
 
     Each output tensor has the page index as its leading dim when n_pages > 1
     (and may omit it when n_pages == 1); page strides are taken from dim 0.
     ``values`` (a ``_lib.ValueRowsArgs``) adds the same tokens' value rows to
-    the call: the library quantizes them alongside the key path.
+    the call: the library quantizes them alongside the key path.  ``nonfinite`` is
+    the address of a device uint32 the kernels set on a NaN or an infinity (0: no check).
     """
     B, H, _, D = src.shape
 
@@ -244,6 +249,7 @@ def launch_key_pages(src: torch.Tensor, *, page_tokens: int, n_pages: int, key_m
     a.scale, a.scale_page_stride = scale.data_ptr(), page_stride(scale)
     a.zero, a.zero_page_stride = zero.data_ptr(), page_stride(zero)
     a.values = 0 if values is None else ctypes.addressof(values)
+    a.nonfinite = nonfinite or None
     lib = _lib.load()
     _lib.check(lib.dkv_quantize_key_pages(a, _lib.stream_ptr(src.device)), "dkv_quantize_key_pages")
 

@@ -81,6 +81,10 @@ class QuantizedTensor:
     def dequantize(self, *, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
         """Materialize on the device (reference quantization.py:96-109 semantics)."""
         out_dtype = dtype or self.output_dtype
+        if self.values.device.type == "cpu":
+            # host-resident pages (a cache moved with .to("cpu")): dequantized on the current GPU
+            gpu = torch.device("cuda", torch.cuda.current_device())
+            return self.to(gpu).dequantize(dtype=dtype).cpu()
         _lib.require_device(self.values)
         ndim = len(self.original_shape)
         axis = self.axis if self.axis >= 0 else ndim + self.axis

@@ -47,7 +47,7 @@ extern "C" {
 /* Thread-local description of the last error on this thread. */
 const char* dkv_last_error(void);
 
-/* ABI version (8); bumps when a struct or an entry point below changes. */
+/* ABI version (9); bumps when a struct or an entry point below changes. */
 int dkv_abi_version(void);
 
 /*
@@ -99,7 +99,19 @@ typedef struct dkv_value_rows_args {
   void* scale;
   void* zero;
   int64_t meta_dtype;
+  /* Optional (NULL: no check): a device uint32 set to 1 when a group holds a
+   * NaN or an infinity (the reference raises ValueError for such inputs,
+   * src/dart/quantization.py:159-160); never cleared by the library. */
+  uint32_t* nonfinite;
 } dkv_value_rows_args;
+
+/*
+ * dkv_quantize_row_blocks described by a dkv_value_rows_args, with its
+ * optional non-finite flag: the form the cache uses for value pages that are
+ * quantized without keys (reference src/dart/cache.py:457-470 and :505-512,
+ * quantize at src/dart/quantization.py:134-204).
+ */
+int dkv_quantize_value_rows(const dkv_value_rows_args* args, void* stream);
 
 /*
  * Key quantization along tokens for `n_pages` pages of `page_tokens` tokens.
@@ -148,6 +160,10 @@ typedef struct dkv_key_pages_args {
    * one after the other (src/dart/cache.py:472-479); given both, the library
    * runs the value kernel alongside the key path's serial channel selection. */
   const dkv_value_rows_args* values;
+  /* Optional (NULL: no check): a device uint32 set to 1 when a key group holds
+   * a NaN or an infinity (reference src/dart/mixed.py:187-188 and
+   * src/dart/quantization.py:159-160 raise ValueError); never cleared. */
+  uint32_t* nonfinite;
 } dkv_key_pages_args;
 
 int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stream);

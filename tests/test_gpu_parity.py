@@ -160,8 +160,8 @@ def test_large_append_pages_bit_exact_vs_oracle(selection):
     oc = O.OracleCache(O.OracleConfig(**cfg))
     oc.append(k, v)
     torch.cuda.synchronize()
+    assert len(cache.iter_segments()) == len(oc.segments())
     pairs = list(zip(cache.iter_segments(), oc.segments()))
-    assert len(pairs) == len(oc.segments())
     for (ks, vs), (oks, ovs) in pairs:
         for a, b in zip(_seg_fields(ks).values(), _seg_fields(oks).values()):
             assert bits_equal(a.cpu(), b)
@@ -186,8 +186,8 @@ def test_uniform_append_pages_bit_exact_vs_oracle(bits, dtype):
     oc = O.OracleCache(O.OracleConfig(**cfg))
     oc.append(k, v)
     torch.cuda.synchronize()
+    assert len(cache.iter_segments()) == len(oc.segments()) == 1 + -(-(1100 - 32) // 128)
     pairs = list(zip(cache.iter_segments(), oc.segments()))
-    assert len(pairs) == len(oc.segments()) == 1 + -(-(1100 - 32) // 128)
     for (ks, vs), (oks, ovs) in pairs:
         for a, b in zip(_seg_fields(ks).values(), _seg_fields(oks).values()):
             assert bits_equal(a.cpu(), b)
@@ -257,6 +257,7 @@ def test_config2_decode_vs_oracle(seed, dtype):
     print("config2", seed, dtype, "rel err", err, flush=True)
     assert err <= 2e-3
     # every packed page matches the oracle bit for bit
+    assert len(cache.iter_segments()) == len(oc.segments())
     for (ks, vs), (oks, ovs) in zip(cache.iter_segments(), oc.segments()):
         for a, b in zip(_seg_fields(ks).values(), _seg_fields(oks).values()):
             assert bits_equal(a.cpu(), b)
