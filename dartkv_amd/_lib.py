@@ -117,7 +117,8 @@ EXPORTED = (
     "dkv_last_error", "dkv_abi_version", "dkv_quantize_rows", "dkv_quantize_row_blocks", "dkv_quantize_value_rows",
     "dkv_quantize_key_pages",
     "dkv_dequantize_rows",
-    "dkv_dequantize_mixed", "dkv_decode_workspace_bytes", "dkv_decode_attention", "dkv_decode_prep",
+    "dkv_dequantize_mixed", "dkv_decode_workspace_bytes", "dkv_decode_attention", "dkv_decode_attention_noalloc",
+    "dkv_decode_scratch_bytes", "dkv_decode_prep",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -149,10 +150,14 @@ def load() -> ctypes.CDLL:
         lib.dkv_decode_workspace_bytes.argtypes = [i64, i64, i64, i64]
         lib.dkv_decode_workspace_bytes.restype = i64
         lib.dkv_decode_attention.argtypes = [ctypes.POINTER(DecodeArgs), vp]
+        lib.dkv_decode_attention_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), vp]
+        lib.dkv_decode_scratch_bytes.argtypes = []
+        lib.dkv_decode_scratch_bytes.restype = i64
         lib.dkv_decode_prep.argtypes = [ctypes.POINTER(DecodePrepArgs), vp]
         for name in ("dkv_quantize_rows", "dkv_quantize_row_blocks", "dkv_quantize_value_rows", "dkv_quantize_key_pages",
                      "dkv_dequantize_rows",
-                     "dkv_dequantize_mixed", "dkv_decode_attention", "dkv_decode_prep"):
+                     "dkv_dequantize_mixed", "dkv_decode_attention", "dkv_decode_attention_noalloc",
+                     "dkv_decode_prep"):
             getattr(lib, name).restype = ctypes.c_int
         if lib.dkv_abi_version() != ABI_VERSION:
             raise RuntimeError("libdartkv_hip.so ABI version mismatch; rebuild it")

@@ -68,7 +68,8 @@ def _fast_enabled() -> bool:
 
 def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,
                      n_splits: Optional[int] = None, out_f32: Optional[torch.Tensor] = None,
-                     fast: Optional[bool] = None, fast_events=None) -> torch.Tensor:
+                     fast: Optional[bool] = None, fast_events=None, out: Optional[torch.Tensor] = None,
+                     static_scratch: bool = False) -> torch.Tensor:
     """Single-token decode over the packed cache with the HIP split-K kernel.
 
     ``query`` is [B, Hq, 1, D] (or [B, Hq, D]) on the cache's device.  Returns
@@ -78,7 +79,11 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     environment sets DKV_FORCE_GENERAL=1); ``n_splits`` overrides the split
     count of the page kernel (or of the general kernel when it does all work).
     ``fast_events`` (two recorded ``torch.cuda.Event`` objects) are recorded
-    again right before and after the page kernel, to time it alone.
+    again right before and after the page kernel, to time it alone.  ``out``
+    ([B, Hq, 1, D] in ``query.dtype``) receives the result instead of a new
+    tensor.  ``static_scratch`` keeps the split records in the library's static
+    device scratch (``dkv_decode_attention_noalloc``) instead of a workspace
+    tensor, so with ``out`` given the call allocates nothing.
     """
     _lib.require_device(query)
     batch, kv_heads, head_dim = _check_query(query, cache)
@@ -110,10 +115,14 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
         splits = n_splits or default_splits(batch, kv_heads, rest)
         splits = max(1, min(splits, max(1, rest)))
     Hq = q3.shape[1]
-    out = torch.empty(batch, Hq, 1, head_dim, dtype=query.dtype, device=query.device)
+    if out is None:
+        out = torch.empty(batch, Hq, 1, head_dim, dtype=query.dtype, device=query.device)
+    elif out.shape != (batch, Hq, 1, head_dim) or out.dtype != query.dtype or out.device != query.device \
+            or out.stride(-1) != 1:
+        raise ValueError("out must be a [B, Hq, 1, D] tensor of the query's dtype and device, unit stride in D")
     lib = _lib.load()
     ws_bytes = lib.dkv_decode_workspace_bytes(batch, Hq, head_dim, splits + fast_splits)
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+    workspace = None if static_scratch else torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
     a = _lib.DecodeArgs()
     a.query = q3.data_ptr()
     a.q_dtype = _lib.dtype_code(q3.dtype)
@@ -133,7 +142,7 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     a.meta_dtype = _lib.dtype_code(meta)
     a.scale = float(factor)
     a.n_splits = splits
-    a.workspace = workspace.data_ptr()
+    a.workspace = _lib.ptr(workspace)
     a.workspace_bytes = ws_bytes
     if fast_count:
         a.fast_first, a.fast_count = plan.fast_first, fast_count
@@ -144,7 +153,10 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
         a.tail_tokens_dev = cache.device_tail.data_ptr()
     if fast_events is not None:
         a.fast_events[0], a.fast_events[1] = fast_events[0].cuda_event, fast_events[1].cuda_event
-    _lib.check(lib.dkv_decode_attention(a, _lib.stream_ptr(query.device)), "dkv_decode_attention")
+    if static_scratch:
+        _lib.check(lib.dkv_decode_attention_noalloc(a, _lib.stream_ptr(query.device)), "dkv_decode_attention_noalloc")
+    else:
+        _lib.check(lib.dkv_decode_attention(a, _lib.stream_ptr(query.device)), "dkv_decode_attention")
     return out
 
 

@@ -13,6 +13,8 @@
 // so the values attended to are exactly those the reference's streamed
 // attention sees (attention.py:74-77).
 #include <hip/hip_runtime.h>
+
+#include <mutex>
 #include <math.h>
 
 #include "dkv_capi_util.h"
@@ -558,6 +560,64 @@ static int record_event(void* ev, hipStream_t s) {
   const hipError_t e = hipEventRecord((hipEvent_t)ev, s);
   DKV_CHECK(e == hipSuccess, DKV_ERR_HIP, "dkv_decode_attention: hipEventRecord failed: %s", hipGetErrorString(e));
   return DKV_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Static scratch for dkv_decode_attention_noalloc: the split records live in a
+// file-scope device array instead of a caller workspace.  Every GPU the
+// library runs on holds its own copy until the process ends.  In host code
+// `scratch` only names the array; its device address on the current GPU comes
+// from hipGetSymbolAddress, fetched once per device and kept in
+// g_scratch_ptr.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int64_t kScratchBytes = (int64_t)32 << 20;
+constexpr int kScratchMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device, with that device current).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  DKV_CHECK(e == hipSuccess, DKV_ERR_HIP, "dkv_decode_attention_noalloc: hipGetDevice failed: %s",
+            hipGetErrorString(e));
+  DKV_CHECK(dev >= 0 && dev < kScratchMaxDevices, DKV_ERR_UNSUPPORTED,
+            "dkv_decode_attention_noalloc: device %d is beyond the %d devices it supports", dev, kScratchMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    DKV_CHECK(e == hipSuccess && ptr != nullptr, DKV_ERR_HIP,
+              "dkv_decode_attention_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return DKV_OK;
+}
+}  // namespace
+
+extern "C" int64_t dkv_decode_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int dkv_decode_attention_noalloc(const dkv_decode_args* args, void* stream) {
+  DKV_CHECK(args != nullptr, DKV_ERR_INVALID, "args is NULL");
+  dkv_decode_args a = *args;
+  const bool fast = a.fast_count > 0;
+  const int64_t rest = a.n_segments - (fast ? a.fast_count : 0) + (a.tail.tokens > 0 ? 1 : 0);
+  const int64_t splits = (fast ? a.fast_splits : 0) + (rest > 0 ? a.n_splits : 0);
+  const int64_t need = dkv_decode_workspace_bytes(a.B, a.Hq, a.D, splits);
+  DKV_CHECK(need <= kScratchBytes, DKV_ERR_INVALID,
+            "dkv_decode_attention_noalloc: the split records need %lld bytes, more than the %lld bytes of static "
+            "scratch; use fewer splits or dkv_decode_attention with a workspace",
+            (long long)need, (long long)kScratchBytes);
+  void* ptr = nullptr;
+  const int rc = scratch_address(&ptr);
+  if (rc != DKV_OK) return rc;
+  a.workspace = ptr;
+  a.workspace_bytes = kScratchBytes;
+  return dkv_decode_attention(&a, stream);
 }
 
 extern "C" int64_t dkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t n_splits) {

@@ -321,6 +321,24 @@ int64_t dkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t n_s
 
 int dkv_decode_attention(const dkv_decode_args* args, void* stream);
 
+/*
+ * dkv_decode_attention without a caller workspace and without any device
+ * allocation: the split records go to a static device array of
+ * dkv_decode_scratch_bytes() bytes (32 MiB) that the library holds on each
+ * GPU it runs on until the process ends.  args->workspace and
+ * args->workspace_bytes are ignored; every other argument means what it means
+ * for dkv_decode_attention.  A call whose records
+ * (dkv_decode_workspace_bytes of its splits) exceed the scratch returns
+ * DKV_ERR_INVALID.  Calls that overlap on one GPU (several streams or host
+ * threads) share the array and race; callers serialize them.
+ *
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).
+ */
+int dkv_decode_attention_noalloc(const dkv_decode_args* args, void* stream);
+int64_t dkv_decode_scratch_bytes(void);
+
 #ifdef __cplusplus
 }
 #endif
