@@ -26,7 +26,7 @@ KEY_DENSE, KEY_UNIFORM, KEY_MIXED = 0, 1, 2
 VALUE_DENSE, VALUE_UNIFORM = 0, 1
 SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
@@ -46,6 +46,7 @@ class ValueRowsArgs(ctypes.Structure):
         ("bits", ctypes.c_int64), ("group", ctypes.c_int64),
         ("values", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("zero", ctypes.c_void_p),
         ("meta_dtype", ctypes.c_int64), ("nonfinite", ctypes.c_void_p),
+        ("out_block_rows", ctypes.c_int64), ("out_row0", ctypes.c_int64),
     ]
 
 

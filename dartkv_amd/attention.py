@@ -19,7 +19,11 @@ from typing import Optional
 import torch
 
 from . import _lib
-from .cache import DartKVCache, _dense16_ok, tail_segment
+from .cache import DartKVCache, _dense16_ok, _materialize, tail_segment
+
+# The HIP decode kernels take at most this many query heads per KV head and this head_dim
+# (decode.hip kMaxGroup / kMaxDim); larger shapes run segment_attention.
+MAX_GROUP, MAX_HEAD_DIM = 16, 512
 
 
 def dense_attention(query: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, *,
@@ -171,9 +175,42 @@ def streamed_dart_attention(query: torch.Tensor, cache: DartKVCache, *, scale: O
         raise ValueError("cache is empty")
     batch, kv_heads, head_dim = _check_query(query, cache)
     _lib.require_device(query)
+    if query.shape[1] // kv_heads > MAX_GROUP or head_dim > MAX_HEAD_DIM:
+        return segment_attention(query, cache, scale=scale)
     if query.shape[-2] == 1:
         return decode_attention(query, cache, scale=scale)
     return _multi_token_attention(query, cache, scale=scale)
+
+
+def segment_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,
+                      out_f32: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention over the cache one segment at a time, for shapes the HIP decode kernels do not take
+    (more than MAX_GROUP query heads per KV head, head_dim above MAX_HEAD_DIM): each segment is
+    dequantized by the HIP dequantize kernels and attended with fp32 logits and an online softmax on
+    the GPU, the reference's streamed algorithm (attention.py:32-87).  ``out_f32`` ([B, Hq, Q, D]
+    float32) receives the result before the final cast."""
+    batch, kv_heads, head_dim = _check_query(query, cache)
+    group = query.shape[1] // kv_heads
+    factor = scale if scale is not None else 1.0 / math.sqrt(head_dim)
+    q = query.float()
+    shape = (*query.shape[:3], 1)
+    m = torch.full(shape, float("-inf"), device=query.device)
+    l = torch.zeros(shape, device=query.device)
+    acc = torch.zeros(query.shape, dtype=torch.float32, device=query.device)
+    for kseg, vseg in cache.iter_segments():
+        k = _materialize(kseg).float().repeat_interleave(group, dim=1)
+        v = _materialize(vseg).float().repeat_interleave(group, dim=1)
+        logits = torch.matmul(q, k.transpose(-1, -2).contiguous()) * factor
+        m_new = torch.maximum(m, logits.amax(dim=-1, keepdim=True))
+        p = torch.exp(logits - m_new)
+        correction = torch.exp(m - m_new)
+        l = l * correction + p.sum(dim=-1, keepdim=True)
+        acc = acc * correction + torch.matmul(p, v)
+        m = m_new
+    out = acc / l.clamp_min(1e-20)
+    if out_f32 is not None:
+        out_f32.copy_(out)
+    return out.to(query.dtype)
 
 
 def _multi_token_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,

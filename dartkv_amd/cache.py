@@ -1,135 +1,43 @@
-"""Append-only compressed KV cache whose pages are produced by HIP kernels.
+"""Append-only compressed KV cache whose pages live in a device page pool.
 
-Lifecycle semantics follow the reference ``DartKVCache``
-(reference src/dart/cache.py:45-661): dense sink prefix, page-sized
-quantization, held partial pages, Kitty local / value-local buffers, value
-page merging and union-boundary segment iteration.  What differs is where
-the work happens:
+The observable lifecycle is the reference ``DartKVCache``'s (reference
+src/dart/cache.py:45-661): a dense sink prefix, page-sized quantization,
+held partial pages, Kitty local / value-local windows, value pages that grow
+token-wise up to a page, and segments cut at the union of the key and value
+boundaries.  How it is stored is this build's own:
 
-* every page of one append is quantized by one ``dkv_quantize_key_pages``
-  launch (keys along tokens) that also quantizes the values
-  (values along head_dim, read in place from the appended tensor's token
-  slice); page fields are views into page-major chunk tensors;
+* packed pages live in two growable device pools (``pool.PagePool``): key
+  pages page-major, one slot per page; value pages token-major, one row per
+  token.  Every page of one append is quantized by one key launch that also
+  quantizes the values, straight into the pools; a value page that grows
+  token-wise is a run of consecutive pool rows, filled in place;
 * the held partial page lives in a preallocated tail buffer, so a one-token
-  decode append is a single device copy with no concatenation;
-* the decode kernel reads a device table of segment descriptors that is
-  rebuilt only when a page is sealed, never on a plain tail append.
+  decode append is one device copy;
+* the (key, value) segment list is rebuilt only when a page is sealed, and the
+  device descriptor table the decode kernels read (with the page directory
+  ``page_table()`` views) is built once per sealed layout;
+* batch reordering (beam search) gathers the packed bytes along the batch
+  axis; nothing is quantized again.
 """
 
 from __future__ import annotations
 
 import contextlib
 from dataclasses import dataclass
+from itertools import accumulate
 from typing import TYPE_CHECKING, List, Optional, Tuple, Union
 
 import torch
 
 from . import _lib
 from .mixed import MixedQuantizedKey, launch_key_pages, promoted_count, random_channels
+from .pool import PagePool, PoolKeys, PoolMixedKey, PoolValues
 from .quantization import QuantizedTensor
 
-Segment = Union[torch.Tensor, QuantizedTensor, MixedQuantizedKey]
-
-
-class _PageRun:
-    """Pages quantized by one launch: each field is one tensor with a page
-    dimension (`dim`; page p is `size` entries of it starting at p * size,
-    and dim 0 is dropped from the page's view), plus the fields every page
-    shares.  A prefill of 127 pages would otherwise create about a thousand
-    tensor views in Python before the first page is read."""
-
-    __slots__ = ("tensors", "dim", "size", "shared")
-
-    def __init__(self, tensors: dict, dim: int, size: int, shared: dict) -> None:
-        self.tensors, self.dim, self.size, self.shared = tensors, dim, size, shared
-
-    def view(self, name: str, page: int) -> torch.Tensor:
-        t = self.tensors[name]
-        return t[page] if self.dim == 0 else t.narrow(self.dim, page * self.size, self.size)
-
-    def block(self, name: str, page: int) -> Optional[Tuple[int, int]]:
-        """(address, (batch, head) stride) of the page's block as _bh_block gives it, or None when
-        _bh_block would need a copy (then the caller materializes the view)."""
-        t = self.tensors[name]
-        if t.numel() == 0:
-            return 0, 0
-        strides, shape = t.stride(), t.shape
-        if self.dim == 0:
-            strides, shape = strides[1:], shape[1:]
-        else:
-            shape = shape[:self.dim] + (self.size,) + shape[self.dim + 1:]
-        B, H = shape[0], shape[1]
-        inner = 1
-        for size, stride in zip(reversed(shape[2:]), reversed(strides[2:])):
-            if size != 1 and stride != inner:
-                return None
-            inner *= size
-        if H > 1:
-            bh = strides[1]
-            if not (B == 1 or strides[0] == H * bh):
-                return None
-        else:
-            bh = strides[0] if B > 1 else inner
-        offset = page * (t.stride(0) if self.dim == 0 else self.size * t.stride(self.dim))
-        return t.data_ptr() + offset * t.element_size(), bh
-
-
-class _RunField:
-    """A segment field read from the segment's page run: a tensor field becomes the page's view
-    on first access (then cached in the instance), a shared field is the run's value."""
-
-    def __init__(self, name: str, tensor: bool) -> None:
-        self.name, self.tensor = name, tensor
-
-    def __get__(self, obj, cls=None):
-        if obj is None:
-            return self
-        if not self.tensor:
-            return obj._run.shared[self.name]
-        v = obj._run.view(self.name, obj._page)
-        obj.__dict__[self.name] = v
-        return v
-
-
-class _PagedMixedKey(MixedQuantizedKey):
-    """One page of a `_PageRun` of mixed keys; behaves as a MixedQuantizedKey."""
-
-    low_values = _RunField("low_values", True)
-    high_values = _RunField("high_values", True)
-    channel_indices = _RunField("channel_indices", True)
-    scale = _RunField("scale", True)
-    zero_point = _RunField("zero_point", True)
-    original_shape = _RunField("original_shape", False)
-    padded_tokens = _RunField("padded_tokens", False)
-    group_size = _RunField("group_size", False)
-    low_bits = _RunField("low_bits", False)
-    promote_bits = _RunField("promote_bits", False)
-    output_dtype = _RunField("output_dtype", False)
-
-    def __init__(self, run: _PageRun, page: int) -> None:  # pylint: disable=super-init-not-called
-        self._run, self._page = run, page
-
-
-class _PagedQuantized(QuantizedTensor):
-    """One page of a `_PageRun` of uniform codes; behaves as a QuantizedTensor."""
-
-    values = _RunField("values", True)
-    scale = _RunField("scale", True)
-    zero_point = _RunField("zero_point", True)
-    original_shape = _RunField("original_shape", False)
-    original_dim = _RunField("original_dim", False)
-    padded_dim = _RunField("padded_dim", False)
-    packed_dim = _RunField("packed_dim", False)
-    group_size = _RunField("group_size", False)
-    bits = _RunField("bits", False)
-    output_dtype = _RunField("output_dtype", False)
-    axis = _RunField("axis", False)
-
-    def __init__(self, run: _PageRun, page: int) -> None:  # pylint: disable=super-init-not-called
-        self._run, self._page = run, page
-
 if TYPE_CHECKING:
-    from .page_table import DartPageRun, DartPageTable
+    from .page_table import DartPageTable
+
+Segment = Union[torch.Tensor, QuantizedTensor, MixedQuantizedKey]
 
 
 @dataclass(frozen=True)
@@ -254,8 +162,9 @@ class DartKVCache:
 
     def __init__(self, config: Optional[DartKVCacheConfig] = None) -> None:
         self.config = config or DartKVCacheConfig()
-        self._key_segments: List[Segment] = []
-        self._value_segments: List[Segment] = []
+        # the key and the value track: segments in sequence order (dense tensors or pool views)
+        self._keys: List[Segment] = []
+        self._values: List[Segment] = []
         self._pending_key: Optional[torch.Tensor] = None
         self._pending_value: Optional[torch.Tensor] = None
         self._shape: Optional[Tuple[int, int, int]] = None
@@ -263,20 +172,21 @@ class DartKVCache:
         self._device: Optional[torch.device] = None
         self._seen_tokens = 0
         self._layout_version = 0
-        self._page_table_cache: dict = {}
-        self._page_run_cache: dict = {}
-        # Sealed-structure version: bumps when any segment other than the
-        # held tail changes; the decode table is rebuilt only then.
+        # bumps when anything but the held tail changes; segment lists and descriptors follow it
         self._sealed_version = 0
+        self._key_pool: Optional[PagePool] = None
+        self._value_pool: Optional[PagePool] = None
+        self._value_job = None  # a value-row launch waiting for the key launch of the same tokens
         self._tail_key: Optional[torch.Tensor] = None
         self._tail_value: Optional[torch.Tensor] = None
-        self._decode_plan_cache: Optional[_DecodePlan] = None
-        self._random_channels: Optional[torch.Tensor] = None
-        # device copy of the held tail's length (replayable decode steps); None when off
-        self._tail_count_dev: Optional[torch.Tensor] = None
-        # int32 [2] device flags (keys, values) the quantize kernels set on a NaN or an infinity
-        self._nonfinite: Optional[torch.Tensor] = None
+        self._tail_count_dev: Optional[torch.Tensor] = None  # held tail length on the device (graph replay)
+        self._nonfinite: Optional[torch.Tensor] = None  # int32 [2] flags (keys, values) set by the quantizers
         self._nonfinite_ptrs: Tuple[int, int] = (0, 0)
+        self._sealed_pairs_cache: Optional[Tuple[int, list]] = None
+        self._directory_cache: dict = {}
+        self._decode_plan_cache: Optional[_DecodePlan] = None
+        self._page_table_cache: dict = {}
+        self._page_run_cache: dict = {}
 
     # ---- reference properties ----
     @property
@@ -325,17 +235,17 @@ class DartKVCache:
         if value_states.stride(-1) != 1:
             value_states = value_states.contiguous()
         chunk = key_states.shape[-2]
-        sink_remaining = max(0, self.config.sink_tokens - self._seen_tokens)
-        sink = min(sink_remaining, chunk)
+        sink = min(max(0, self.config.sink_tokens - self._seen_tokens), chunk)
         if sink:
-            self._key_segments.append(key_states[..., :sink, :].clone())
-            self._value_segments.append(value_states[..., :sink, :].clone())
+            self._keys.append(key_states[..., :sink, :].clone())
+            self._values.append(value_states[..., :sink, :].clone())
             self._sealed_version += 1
         if sink < chunk:
-            if not self._device_tail_append(key_states[..., sink:, :], value_states[..., sink:, :]):
+            keys, values = key_states[..., sink:, :], value_states[..., sink:, :]
+            if not self._device_tail_append(keys, values):
                 if self._tail_count_dev is not None and torch.cuda.is_current_stream_capturing():
                     raise RuntimeError("a captured append may only extend the held tail by one token")
-                self._append_remainder(key_states[..., sink:, :], value_states[..., sink:, :])
+                self._append_tokens(keys, values)
                 self._sync_device_tail()
         self._seen_tokens += chunk
         self._layout_version += 1
@@ -344,8 +254,8 @@ class DartKVCache:
     def get(self) -> Tuple[torch.Tensor, torch.Tensor]:
         if self._seen_tokens == 0:
             raise RuntimeError("DartKVCache is empty; call update() before get()")
-        keys = [_materialize(s) for s in self._key_segments]
-        values = [_materialize(s) for s in self._value_segments]
+        keys = [_materialize(s) for s in self._keys]
+        values = [_materialize(s) for s in self._values]
         if self._pending_key is not None:
             keys.append(self._pending_key)
         if self._pending_value is not None:
@@ -362,12 +272,8 @@ class DartKVCache:
 
     @property
     def storage_bytes(self) -> int:
-        pending = 0
-        if self._pending_key is not None:
-            pending += self._pending_key.numel() * self._pending_key.element_size()
-        if self._pending_value is not None:
-            pending += self._pending_value.numel() * self._pending_value.element_size()
-        return sum(_segment_nbytes(s) for s in (*self._key_segments, *self._value_segments)) + pending
+        pending = sum(t.numel() * t.element_size() for t in (self._pending_key, self._pending_value) if t is not None)
+        return sum(_segment_nbytes(s) for s in (*self._keys, *self._values)) + pending
 
     @property
     def dense_bytes(self) -> int:
@@ -380,54 +286,79 @@ class DartKVCache:
     def compression_ratio(self) -> float:
         return self.dense_bytes / self.storage_bytes if self.storage_bytes else 1.0
 
+    # ---- segments and descriptors ----
+    def _tail_resident(self) -> bool:
+        """The pending tokens sit in the tail buffer and are described per call, not in the sealed layout."""
+        return self.config.value_local_tokens == 0 and self._pending_in_tail()
+
+    def _sealed_pairs(self) -> list:
+        """(key, value) segments of everything but a tail-resident pending tail, cut at the union of the two
+        tracks' boundaries; built once per sealed layout."""
+        cached = self._sealed_pairs_cache
+        if cached is not None and cached[0] == self._sealed_version:
+            return cached[1]
+        keys, values = list(self._keys), list(self._values)
+        if not self._tail_resident():
+            if self._pending_key is not None:
+                if self._pending_value is None:
+                    raise RuntimeError("DartKVCache has a pending key without a pending value")
+                keys.append(self._pending_key)
+            if self._pending_value is not None:
+                values.append(self._pending_value)
+        pairs = _union_pairs(keys, values)
+        self._sealed_pairs_cache = (self._sealed_version, pairs)
+        return pairs
+
     def iter_segments(self) -> list:
-        """K/V segments in sequence order over the union of their boundaries (reference cache.py:229-274)."""
-        key_segments = list(self._key_segments)
-        value_segments = list(self._value_segments)
-        if self._pending_key is not None:
-            if self._pending_value is None:
-                raise RuntimeError("DartKVCache has a pending key without a pending value")
-            key_segments.append(self._pending_key)
-            value_segments.append(self._pending_value)
-        if not key_segments or not value_segments:
-            return []
-        pairs = []
-        ki = vi = ko = vo = 0
-        while ki < len(key_segments) and vi < len(value_segments):
-            kseg, vseg = key_segments[ki], value_segments[vi]
-            klen, vlen = _segment_tokens(kseg), _segment_tokens(vseg)
-            take = min(klen - ko, vlen - vo)
-            if take <= 0:
-                raise RuntimeError("DartKVCache contains an empty logical segment")
-            pairs.append((_slice_segment(kseg, ko, ko + take), _slice_segment(vseg, vo, vo + take)))
-            ko += take
-            vo += take
-            if ko == klen:
-                ki, ko = ki + 1, 0
-            if vo == vlen:
-                vi, vo = vi + 1, 0
-        if ki != len(key_segments) or vi != len(value_segments):
-            raise RuntimeError("DartKVCache key/value logical lengths diverged")
+        """K/V segments in sequence order over the union of their boundaries (reference cache.py:229-274).
+
+        Where a union piece covers only part of a packed segment, that part is returned dequantized."""
+        pairs = list(self._sealed_pairs())
+        if self._tail_resident():
+            pairs.append((self._pending_key, self._pending_value))
         return pairs
 
     def page_metadata(self) -> list:
         """Page order, logical lengths, shapes and element strides (reference cache.py:276-300)."""
-        metadata = []
-        start = 0
+        out, start = [], 0
         for index, (kseg, vseg) in enumerate(self.iter_segments()):
-            klay, vlay = _segment_layout(kseg), _segment_layout(vseg)
-            ktok, vtok = klay.logical_shape[-2], vlay.logical_shape[-2]
-            if ktok != vtok:
+            n = _segment_tokens(kseg)
+            if _segment_tokens(vseg) != n:
                 raise RuntimeError("DartKVCache key/value page lengths diverged")
-            metadata.append(DartPageMetadata(index=index, sequence_start=start, token_count=ktok, key=klay,
-                                             value=vlay))
-            start += ktok
+            out.append(DartPageMetadata(index=index, sequence_start=start, token_count=n, key=_segment_layout(kseg),
+                                        value=_segment_layout(vseg)))
+            start += n
         if start != self._seen_tokens:
             raise RuntimeError(f"page metadata covers {start} tokens, expected {self._seen_tokens}")
-        return metadata
+        return out
+
+    def _directory(self, device: torch.device) -> torch.Tensor:
+        """int32 [N, 4] page directory on ``device``: (sequence start, tokens, key mode, value mode) per
+        segment of ``iter_segments()``.  The sealed rows are built once per sealed layout; the held tail's
+        row is added per call."""
+        cached = self._directory_cache.get(device)
+        if cached is None or cached[0] != self._sealed_version:
+            rows, start = [], 0
+            for kseg, vseg in self._sealed_pairs():
+                n = _segment_tokens(kseg)
+                rows.append((start, n, _page_mode(kseg), _page_mode(vseg)))
+                start += n
+            table = torch.tensor(rows, dtype=torch.int32).reshape(len(rows), 4).to(device)
+            cached = (self._sealed_version, table, start)
+            self._directory_cache = {device: cached}
+        _, table, start = cached
+        if self._tail_resident():
+            tail = torch.tensor([[start, self._pending_key.shape[-2], 0, 0]], dtype=torch.int32).to(device)
+            table = torch.cat((table, tail))
+            start += self._pending_key.shape[-2]
+        if start != self._seen_tokens:
+            raise RuntimeError(f"page table covers {start} tokens, expected {self._seen_tokens}")
+        return table
 
     def page_table(self, *, device=None, rebuild: bool = False) -> "DartPageTable":
-        """Cached page descriptors, invalidated on append/clear/move (reference cache.py:302-323)."""
+        """Page descriptors, one object per layout version and device (reference cache.py:302-323).
+
+        The table's arrays are views of the cache's page directory."""
         from .page_table import DartPageTable
 
         target = _descriptor_device(device, self._device)
@@ -439,7 +370,10 @@ class DartKVCache:
         return table
 
     def page_runs(self, *, device=None, page_table=None, rebuild: bool = False) -> tuple:
-        """Cached page-major uniform runs (reference cache.py:325-352)."""
+        """Runs of consecutive full uniform pages, page-major (reference cache.py:325-352).
+
+        Runs are slices of the page pool; a run is stacked (copied) only where its pages are not
+        consecutive pool slots."""
         target = _descriptor_device(device, self._device)
         if page_table is None:
             cached = self._page_run_cache.get(target)
@@ -455,27 +389,61 @@ class DartKVCache:
             self._page_run_cache[target] = (self._layout_version, runs)
         return runs
 
+    def uniform_page_runs(self, table: "DartPageTable") -> tuple:
+        """The ``DartPageRun``s ``table`` describes over this cache's pages (``DartPageTable.uniform_quantized_runs``)."""
+        from .page_table import DartPageRun
+
+        pairs = self.iter_segments()
+        if len(pairs) != table.page_count or self._seen_tokens != table.seen_tokens:
+            raise ValueError("cache and page_table describe different page lifecycles")
+        page = self.config.page_size
+        full = [_full_uniform(k, v, page) for k, v in pairs]
+        runs, i = [], 0
+        while i < len(pairs):
+            if not full[i]:
+                i += 1
+                continue
+            j = i + 1
+            while j < len(pairs) and full[j] and _same_run_layout(pairs[i], pairs[j]):
+                j += 1
+            keys, values = [p[0] for p in pairs[i:j]], [p[1] for p in pairs[i:j]]
+            kf = _run_fields(keys, ("values", "scale", "zero_point"), page_major=True)
+            vf = _run_fields(values, ("values", "scale", "zero_point"), page_major=False)
+            dev = kf[0].device
+            runs.append(DartPageRun(
+                first_page_index=i, page_indices=table.page_ids[0, i:j].to(dev),
+                sequence_starts=table.sequence_starts[i:j].to(dev), token_counts=table.token_counts[i:j].to(dev),
+                key_values=kf[0], key_scale=kf[1], key_zero_point=kf[2],
+                value_values=vf[0], value_scale=vf[1], value_zero_point=vf[2],
+                key_bits=keys[0].bits, value_bits=values[0].bits, key_group_size=keys[0].group_size,
+                value_group_size=values[0].group_size, page_size=page).validate())
+            i = j
+        return tuple(runs)
+
     def to(self, device) -> "DartKVCache":
         """Move backing tensors to ``device`` (reference cache.py:354-366)."""
-        self._key_segments = [s.to(device) for s in self._key_segments]
-        self._value_segments = [s.to(device) for s in self._value_segments]
+        target = _descriptor_device(device, self._device)
+        for pool in self._pools():
+            pool.to(target)
+        self._keys = [s.to(target) if isinstance(s, torch.Tensor) else s for s in self._keys]
+        self._values = [s.to(target) if isinstance(s, torch.Tensor) else s for s in self._values]
         if self._pending_key is not None:
-            self._pending_key = self._pending_key.to(device)
+            self._pending_key = self._pending_key.to(target)
         if self._pending_value is not None:
-            self._pending_value = self._pending_value.to(device)
+            self._pending_value = self._pending_value.to(target)
         self._tail_key = self._tail_value = None
         self._tail_count_dev = None
-        self._device = _descriptor_device(device, self._device)
+        self._nonfinite = None
+        self._device = target
         self._layout_version += 1
         self._sealed_version += 1
         self._invalidate_page_descriptors()
         return self
 
     def clear(self) -> None:
-        self._key_segments.clear()
-        self._value_segments.clear()
-        self._pending_key = None
-        self._pending_value = None
+        self._keys, self._values = [], []
+        self._pending_key = self._pending_value = None
+        self._key_pool = self._value_pool = None
         self._tail_key = self._tail_value = None
         self._shape = None
         self._dtype = None
@@ -484,8 +452,59 @@ class DartKVCache:
         self._layout_version += 1
         self._sealed_version += 1
         self._decode_plan_cache = None
+        self._directory_cache = {}
         self._tail_count_dev = None
         self._invalidate_page_descriptors()
+
+    def reorder_batch(self, indices) -> None:
+        """Keep batch rows ``indices`` in that order (beam reordering, batch selection, repeats).
+
+        Every packed and dense tensor is gathered along its batch axis: the packed bytes are unchanged
+        and nothing is quantized again (the reference re-quantizes dequantized rows,
+        integrations/huggingface.py:117-127).  With the batch size unchanged the pools and the tail
+        buffer are gathered in place, so descriptors and captured decode graphs stay valid."""
+        if self._shape is None:
+            return
+        index = torch.as_tensor(indices, device=self._device)
+        if index.dtype == torch.bool:
+            index = index.nonzero().flatten()
+        index = index.to(torch.long).flatten()
+        batch = self._shape[0]
+        if index.numel() and bool(((index < 0) | (index >= batch)).any()):
+            raise IndexError("batch indices contain an invalid batch row")
+        same = index.numel() == batch
+        for pool in self._pools():
+            pool.select_batch(index)
+        self._keys = [s.index_select(0, index) if isinstance(s, torch.Tensor) else s for s in self._keys]
+        self._values = [s.index_select(0, index) if isinstance(s, torch.Tensor) else s for s in self._values]
+        in_tail = self._pending_in_tail()
+        if self._tail_key is not None:
+            if same:
+                self._tail_key.copy_(self._tail_key.index_select(0, index))
+                self._tail_value.copy_(self._tail_value.index_select(0, index))
+            else:
+                self._tail_key = self._tail_key.index_select(0, index)
+                self._tail_value = self._tail_value.index_select(0, index)
+        if in_tail:
+            n = self._pending_key.shape[-2]
+            self._pending_key, self._pending_value = self._tail_key[..., :n, :], self._tail_value[..., :n, :]
+        else:
+            if self._pending_key is not None:
+                self._pending_key = self._pending_key.index_select(0, index)
+            if self._pending_value is not None:
+                self._pending_value = self._pending_value.index_select(0, index)
+        self._shape = (index.numel(), self._shape[1], self._shape[2])
+        self._layout_version += 1
+        self._sealed_version += 1
+        self._invalidate_page_descriptors()
+
+    def _pools(self) -> list:
+        pools = {id(p): p for p in (self._key_pool, self._value_pool) if p is not None}
+        for seg in (*self._keys, *self._values):
+            pool = getattr(seg, "_pool", None)
+            if pool is not None:
+                pools[id(pool)] = pool
+        return list(pools.values())
 
     def _invalidate_page_descriptors(self) -> None:
         self._page_table_cache.clear()
@@ -541,250 +560,254 @@ class DartKVCache:
                 and pk.data_ptr() == tk.data_ptr() and self._pending_value.data_ptr() == self._tail_value.data_ptr()
                 and pk.shape[-2] == self._pending_value.shape[-2])
 
-    # ---- append paths (reference cache.py:403-542) ----
-    def _append_remainder(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+    # ---- appends (the lifecycle of reference cache.py:403-542) ----
+    def _append_tokens(self, keys: torch.Tensor, values: torch.Tensor) -> None:
         c = self.config
-        if c.value_local_tokens:
-            self._append_key_remainder(key_states)
-            self._append_value_remainder(value_states)
+        if c.value_local_tokens:  # Kitty: a key window and a separate value window
             self._sealed_version += 1
-            return
-        if c.hold_partial_pages or c.local_tokens:
-            pending = 0 if self._pending_key is None else self._pending_key.shape[-2]
-            total = pending + key_states.shape[-2]
-            available = max(0, total - c.local_tokens)
-            full = (available // c.page_size) * c.page_size
-            if full == 0 and self._pending_in_tail() and total <= self._tail_capacity():
-                # fast path: the new tokens only extend the held tail
-                self._tail_key[..., pending:total, :].copy_(key_states)
-                self._tail_value[..., pending:total, :].copy_(value_states)
-                self._pending_key = self._tail_key[..., :total, :]
-                self._pending_value = self._tail_value[..., :total, :]
-                return
-            if self._pending_key is not None:
-                key_states = torch.cat((self._pending_key, key_states), dim=-2)
-                value_states = torch.cat((self._pending_value, value_states), dim=-2)
-            if full:
-                self._quantize_pages(key_states[..., :full, :], value_states[..., :full, :])
-            if full < key_states.shape[-2]:
-                self._store_pending(key_states[..., full:, :], value_states[..., full:, :])
-            else:
-                self._pending_key = self._pending_value = None
+            self._append_window_keys(keys)
+            self._append_window_values(values)
+        elif c.hold_partial_pages or c.local_tokens:
+            self._append_held(keys, values)
+        else:
             self._sealed_version += 1
+            self._seal(keys, values)  # every page, the last one possibly short
+
+    def _append_held(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Pending tokens plus the new ones: every full page (past the local window) is sealed, the rest is
+        held dense."""
+        c = self.config
+        pending = 0 if self._pending_key is None else self._pending_key.shape[-2]
+        total = pending + keys.shape[-2]
+        sealable = (max(0, total - c.local_tokens) // c.page_size) * c.page_size
+        if sealable == 0 and self._pending_in_tail() and total <= self._tail_capacity():
+            # the new tokens only extend the held tail
+            self._tail_key[..., pending:total, :].copy_(keys)
+            self._tail_value[..., pending:total, :].copy_(values)
+            self._pending_key = self._tail_key[..., :total, :]
+            self._pending_value = self._tail_value[..., :total, :]
             return
-        self._quantize_pages(key_states, value_states)
         self._sealed_version += 1
+        if pending:
+            keys = torch.cat((self._pending_key, keys), dim=-2)
+            values = torch.cat((self._pending_value, values), dim=-2)
+        if sealable:
+            self._seal(keys[..., :sealable, :], values[..., :sealable, :])
+        if sealable < total:
+            self._store_pending(keys[..., sealable:, :], values[..., sealable:, :])
+        else:
+            self._pending_key = self._pending_value = None
 
-    def _append_key_remainder(self, key_states: torch.Tensor) -> None:
-        """Kitty key Q-buffer lifecycle (reference cache.py:424-455)."""
+    def _append_window_keys(self, keys: torch.Tensor) -> None:
+        """Kitty's key window (reference cache.py:424-455): with local_tokens == 1, the first one-token
+        append after a prefill that ended on a page boundary packs the last page again from its
+        dequantized values; later, a page is packed once a token past it arrives."""
         c = self.config
-        if (self._seen_tokens > 0 and self._pending_key is None and c.local_tokens == 1
-                and key_states.shape[-2] == 1 and self._key_segments
-                and not isinstance(self._key_segments[-1], torch.Tensor)):
-            final_page = _materialize(self._key_segments.pop())
-            self._key_pages_only(final_page)
+        last = self._keys[-1] if self._keys else None
+        if (self._seen_tokens > 0 and self._pending_key is None and c.local_tokens == 1 and keys.shape[-2] == 1
+                and last is not None and not isinstance(last, torch.Tensor)):
+            dense = last.dequantize()
+            self._keys.pop()
+            pool = getattr(last, "_pool", None)
+            if pool is not None and pool is self._key_pool and last._at == pool.used - 1:
+                pool.used -= 1  # the page is packed again into the same slot
+            self._seal_keys(dense)
         if self._pending_key is not None:
-            key_states = torch.cat((self._pending_key, key_states), dim=-2)
-        local = 0 if self._seen_tokens == 0 else c.local_tokens
-        available = max(0, key_states.shape[-2] - local)
-        full = (available // c.page_size) * c.page_size
-        if full:
-            self._key_pages_only(key_states[..., :full, :])
-        self._pending_key = key_states[..., full:, :].clone() if full < key_states.shape[-2] else None
+            keys = torch.cat((self._pending_key, keys), dim=-2)
+        window = 0 if self._seen_tokens == 0 else c.local_tokens
+        sealable = (max(0, keys.shape[-2] - window) // c.page_size) * c.page_size
+        if sealable:
+            self._seal_keys(keys[..., :sealable, :])
+        self._pending_key = keys[..., sealable:, :].clone() if sealable < keys.shape[-2] else None
 
-    def _append_value_remainder(self, value_states: torch.Tensor) -> None:
-        """Kitty value Local buffer (reference cache.py:457-470)."""
+    def _append_window_values(self, values: torch.Tensor) -> None:
+        """Kitty's value window (reference cache.py:457-470): all but the newest value_local_tokens
+        tokens are packed, page-sized chunks in order."""
         c = self.config
         if self._pending_value is not None:
-            value_states = torch.cat((self._pending_value, value_states), dim=-2)
-        quantized = max(0, value_states.shape[-2] - c.value_local_tokens)
-        if quantized:
+            values = torch.cat((self._pending_value, values), dim=-2)
+        packed = max(0, values.shape[-2] - c.value_local_tokens)
+        if packed:
             with self._finite_inputs():
-                for start in range(0, quantized, c.page_size):
-                    stop = min(start + c.page_size, quantized)
-                    for seg in self._quantize_value_chunks(value_states[..., start:stop, :], stop - start):
-                        self._append_quantized_value_page(seg)
-        self._pending_value = value_states[..., quantized:, :].clone() if quantized < value_states.shape[-2] else None
+                rows = self._pack_values(values[..., :packed, :])
+                for start in range(0, packed, c.page_size):
+                    self._push_values(rows.rows(start, min(c.page_size, packed - start)))
+        self._pending_value = values[..., packed:, :].clone() if packed < values.shape[-2] else None
 
     @contextlib.contextmanager
     def _finite_inputs(self):
         """Quantize launches inside this scope report NaN or infinite inputs through device flags;
         on exit the flags are read (one host synchronization) and such an input raises the reference's
-        ValueError (quantization.py:159-160, mixed.py:187-188) with the segment lists restored."""
+        ValueError (quantization.py:159-160, mixed.py:187-188) with the tracks and pools restored."""
         flags = self._nonfinite
         if flags is None or flags.device != self._device:
             flags = self._nonfinite = torch.zeros(2, dtype=torch.int32, device=self._device)
         else:
             flags.zero_()
-        keys, values = list(self._key_segments), list(self._value_segments)
+        keys, values = list(self._keys), list(self._values)
+        pools = [(p, p.used) for p in (self._key_pool, self._value_pool) if p is not None]
         self._nonfinite_ptrs = (flags.data_ptr(), flags.data_ptr() + 4)
         try:
             yield
         finally:
             self._nonfinite_ptrs = (0, 0)
+            self._value_job = None
         bad_keys, bad_values = flags.tolist()
         if bad_keys or bad_values:
-            self._key_segments, self._value_segments = keys, values
+            self._keys, self._values = keys, values
+            for pool, used in pools:
+                pool.used = used
+            for pool in (self._key_pool, self._value_pool):  # pools first created by this launch
+                if pool is not None and all(pool is not p for p, _ in pools):
+                    pool.used = 0
             if bad_keys and self.config.promote_ratio > 0.0:
                 raise ValueError("key_states must contain finite values")
             raise ValueError("quantize expects all values to be finite")
 
-    def _quantize_pages(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
-        """Quantize consecutive pages; the last may be partial (reference cache.py:472-479)."""
-        if key_states.shape[-2] != value_states.shape[-2]:
+    def _seal(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Pack consecutive pages of keys and values; the last may be short (reference cache.py:472-479).
+        The key launch that covers the last page quantizes all the tokens' values too."""
+        if keys.shape[-2] != values.shape[-2]:
             raise RuntimeError("key/value page lengths diverged before quantization")
+        page = self.config.page_size
+        T = values.shape[-2]
         with self._finite_inputs():
-            jobs: list = []
-            values = self._quantize_value_chunks(value_states, self.config.page_size, jobs)
-            keys = self._quantize_key_chunks(key_states, jobs)
-            for kseg, vseg in zip(keys, values):
-                self._key_segments.append(kseg)
-                self._append_quantized_value_page(vseg)
+            rows = self._pack_values(values, defer=True)
+            for i, kseg in enumerate(self._pack_key_pages(keys)):
+                self._keys.append(kseg)
+                self._push_values(rows.rows(i * page, min(page, T - i * page)))
 
-    def _key_pages_only(self, key_states: torch.Tensor) -> None:
+    def _seal_keys(self, keys: torch.Tensor) -> None:
         with self._finite_inputs():
-            self._key_segments.extend(self._quantize_key_chunks(key_states))
+            self._keys.extend(self._pack_key_pages(keys))
 
-    def _quantize_key_chunks(self, key_states: torch.Tensor, value_jobs: Optional[list] = None) -> List[Segment]:
-        """Key pages of ``page_size`` tokens (last may be shorter), one launch per page size.
+    def _push_values(self, segment: PoolValues) -> None:
+        """Add a value segment to the value track.  When it continues the pool rows of a value segment
+        that is not yet a full page, it fills that page first (the reference concatenates such pieces,
+        cache.py:514-542); rows past the page start the next segment."""
+        page = self.config.page_size
+        last = self._values[-1] if self._values else None
+        if (isinstance(last, PoolValues) and last._pool is segment._pool and last._at + last._rows == segment._at
+                and last._rows < page):
+            take = min(page - last._rows, segment._rows)
+            self._values[-1] = last.rows(0, last._rows + take)
+            if take == segment._rows:
+                return
+            segment = segment.rows(take, segment._rows - take)
+        self._values.append(segment)
 
-        ``value_jobs`` from _quantize_value_chunks: each goes into the key
-        launch that covers the same tokens.
-        """
+    # ---- packing into the pools ----
+    def _value_pool_for(self, values: torch.Tensor) -> PagePool:
+        if self._value_pool is None:
+            c = self.config
+            B, H, _, D = values.shape
+            vg = c.resolved_value_group_size
+            groups = -(-D // vg)
+            packed = -(-groups * vg // (8 // c.resolved_value_bits))
+            meta = c.metadata_dtype
+            self._value_pool = PagePool(
+                {"values": ((B, H, 0, packed), torch.uint8), "scale": ((B, H, 0, groups), meta),
+                 "zero_point": ((B, H, 0, groups), meta)}, axis=2, batch_axis=0, device=values.device, align=64)
+        return self._value_pool
+
+    def _pack_values(self, values: torch.Tensor, defer: bool = False) -> PoolValues:
+        """Quantize value rows [B, H, T, D] along head_dim into new value pool rows.  With ``defer`` the
+        launch rides with the key launch of the same tokens (``_value_job``)."""
         c = self.config
-        T = key_states.shape[-2]
-        P = c.page_size
-        full = T // P
-        jobs = {start: (n, job) for start, n, job, _ in (value_jobs or [])}
+        B, H, T, D = values.shape
+        pool = self._value_pool_for(values)
+        row0 = pool.reserve(T, headroom=max(pool.align, T // 16) if pool.used == 0 else None)
+        bits, vg = c.resolved_value_bits, c.resolved_value_group_size
+        job, keep = _value_rows_job(values, bits, vg, c.metadata_dtype, pool, row0, self._nonfinite_ptrs[1])
+        if defer:
+            self._value_job = (job, keep)
+        else:
+            lib = _lib.load()
+            _lib.check(lib.dkv_quantize_value_rows(job, _lib.stream_ptr(values.device)), "dkv_quantize_value_rows")
+        groups = pool.shapes["scale"][3]
+        return PoolValues(pool, row0, T, D, groups * vg, pool.shapes["values"][3] * (8 // bits), vg, bits,
+                          values.dtype)
 
-        def job_for(start: int, n: int):
-            entry = jobs.pop(start, None)
-            if entry is None:
-                return None
-            if entry[0] != n:
-                raise RuntimeError("value rows and key pages cover different tokens")
-            return entry[1]
-
-        out: List[Segment] = []
-        if full:
-            out.extend(self._quantize_key_launch(key_states[..., : full * P, :], P, full, job_for(0, full * P)))
-        if T - full * P:
-            out.extend(self._quantize_key_launch(key_states[..., full * P:, :], T - full * P, 1,
-                                                 job_for(full * P, T - full * P)))
-        if jobs:
-            raise RuntimeError("value rows left without a key launch")
-        return out
-
-    def _quantize_key_launch(self, src: torch.Tensor, tokens: int, n_pages: int, values=None) -> List[Segment]:
+    def _key_pool_for(self, keys: torch.Tensor, groups: int, fresh: bool) -> PagePool:
+        """The cache's key pool (pages with the full page's group count), or with ``fresh`` an exact pool
+        for pages of another shape (a short last page)."""
+        if not fresh and self._key_pool is not None:
+            return self._key_pool
         c = self.config
-        B, H, _, D = src.shape
-        dev = src.device
-        meta = c.metadata_dtype
-        kg = c.resolved_key_group_size
-        G = (tokens + kg - 1) // kg
+        B, H, _, D = keys.shape
+        kg, meta = c.resolved_key_group_size, c.metadata_dtype
         if c.promote_ratio > 0.0:
             K = promoted_count(D, c.promote_ratio)
             nb = (kg + 3) // 4
-            low = torch.empty(n_pages, B, H, D, G, nb, dtype=torch.uint8, device=dev)
-            high = torch.empty(n_pages, B, H, K, G, nb if K else nb * 4, dtype=torch.uint8, device=dev)
-            idx = torch.empty(n_pages, B, H, K, dtype=torch.int32, device=dev)
-            scale = torch.empty(n_pages, B, H, D, G, dtype=meta, device=dev)
-            zero = torch.empty(n_pages, B, H, D, G, dtype=meta, device=dev)
-            strategy = c.channel_selection
-            given = None
-            if strategy == "random" and 0 < K < D:
-                # one randperm per KV head per page, shared across the batch (mixed.py:145-153)
-                given = torch.stack([random_channels(H, D, K, dev) for _ in range(n_pages)], 0).to(torch.int32)
+            fields = {"low_values": ((0, B, H, D, groups, nb), torch.uint8),
+                      "high_values": ((0, B, H, K, groups, nb if K else nb * 4), torch.uint8),
+                      "channel_indices": ((0, B, H, K), torch.int32),
+                      "scale": ((0, B, H, D, groups), meta), "zero_point": ((0, B, H, D, groups), meta)}
+        else:
+            per = 8 // c.resolved_key_bits
+            fields = {"values": ((0, B, H, D, -(-groups * kg // per)), torch.uint8),
+                      "scale": ((0, B, H, D, groups), meta), "zero_point": ((0, B, H, D, groups), meta)}
+        pool = PagePool(fields, axis=0, batch_axis=1, device=keys.device)
+        if not fresh:
+            self._key_pool = pool
+        return pool
+
+    def _pack_key_pages(self, keys: torch.Tensor) -> List[Segment]:
+        """Quantize keys [B, H, T, D] along the tokens, one page per page_size tokens (the last may be
+        short).  Full-shape pages go to the key pool, pages with another group count to an exact pool of
+        their own.  A deferred value job rides with the last launch."""
+        P = self.config.page_size
+        T = keys.shape[-2]
+        full, rest = divmod(T, P)
+        launches = ([(0, P, full)] if full else []) + ([(full * P, rest, 1)] if rest else [])
+        job, self._value_job = self._value_job, None
+        out: List[Segment] = []
+        for i, (start, tokens, n_pages) in enumerate(launches):
+            ride = job if i == len(launches) - 1 else None
+            out.extend(self._key_launch(keys[..., start:start + n_pages * tokens, :], tokens, n_pages, ride))
+        return out
+
+    def _key_launch(self, src: torch.Tensor, tokens: int, n_pages: int, job) -> List[Segment]:
+        c = self.config
+        H, D = src.shape[1], src.shape[3]
+        kg, meta = c.resolved_key_group_size, c.metadata_dtype
+        groups = -(-tokens // kg)
+        fresh = groups != -(-c.page_size // kg)
+        pool = self._key_pool_for(src, groups, fresh)
+        slot = pool.reserve(n_pages, headroom=0 if fresh else (max(2, n_pages // 16) if pool.used == 0 else None))
+        t = {name: tensor[slot:slot + n_pages] for name, tensor in pool.tensors.items()}
+        values = None if job is None else job[0]
+        flag = self._nonfinite_ptrs[0]
+        if c.promote_ratio > 0.0:
+            K = promoted_count(D, c.promote_ratio)
             selection = {"magnitude": _lib.SELECT_MAGNITUDE, "variance": _lib.SELECT_VARIANCE,
-                         "random": _lib.SELECT_GIVEN}[strategy]
+                         "random": _lib.SELECT_GIVEN}[c.channel_selection]
+            given = None
+            if c.channel_selection == "random" and 0 < K < D:
+                # one randperm per KV head per page, shared across the batch (reference mixed.py:145-153)
+                given = torch.stack([random_channels(H, D, K, src.device) for _ in range(n_pages)], 0).to(torch.int32)
+            common = dict(key_mode=_lib.KEY_MIXED, bits=2, group=kg, promoted=K, selection=selection, meta=meta,
+                          nonfinite=flag)
             if given is not None and n_pages > 1:
                 for p in range(n_pages):
                     launch_key_pages(src[..., p * tokens:(p + 1) * tokens, :], page_tokens=tokens, n_pages=1,
-                                     key_mode=_lib.KEY_MIXED, bits=2, group=kg, promoted=K, selection=selection,
-                                     given_idx=given[p].contiguous(), meta=meta, low=low[p], high=high[p],
-                                     idx=idx[p], scale=scale[p], zero=zero[p],
-                                     values=values if p == n_pages - 1 else None,
-                                     nonfinite=self._nonfinite_ptrs[0])
+                                     given_idx=given[p].contiguous(), low=t["low_values"][p],
+                                     high=t["high_values"][p], idx=t["channel_indices"][p], scale=t["scale"][p],
+                                     zero=t["zero_point"][p], values=values if p == n_pages - 1 else None, **common)
             else:
-                launch_key_pages(src, page_tokens=tokens, n_pages=n_pages, key_mode=_lib.KEY_MIXED, bits=2,
-                                 group=kg, promoted=K, selection=selection,
-                                 given_idx=None if given is None else given[0].contiguous(), meta=meta,
-                                 low=low, high=high, idx=idx, scale=scale, zero=zero, values=values,
-                                 nonfinite=self._nonfinite_ptrs[0])
-            run = _PageRun(dict(low_values=low, high_values=high, channel_indices=idx, scale=scale, zero_point=zero),
-                           0, 1, dict(original_shape=(B, H, tokens, D), padded_tokens=G * kg, group_size=kg,
-                                      low_bits=2, promote_bits=c.promote_bits, output_dtype=src.dtype))
-            return [_PagedMixedKey(run, p) for p in range(n_pages)]
+                launch_key_pages(src, page_tokens=tokens, n_pages=n_pages,
+                                 given_idx=None if given is None else given[0].contiguous(), low=t["low_values"],
+                                 high=t["high_values"], idx=t["channel_indices"], scale=t["scale"],
+                                 zero=t["zero_point"], values=values, **common)
+            return [PoolMixedKey(pool, slot + p, tokens, D, groups * kg, kg, c.promote_bits, src.dtype)
+                    for p in range(n_pages)]
         bits = c.resolved_key_bits
-        per = 8 // bits
-        padded = G * kg
-        packed_dim = ((padded + per - 1) // per) * per
-        codes = torch.empty(n_pages, B, H, D, packed_dim // per, dtype=torch.uint8, device=dev)
-        scale = torch.empty(n_pages, B, H, D, G, dtype=meta, device=dev)
-        zero = torch.empty(n_pages, B, H, D, G, dtype=meta, device=dev)
         launch_key_pages(src, page_tokens=tokens, n_pages=n_pages, key_mode=_lib.KEY_UNIFORM, bits=bits, group=kg,
-                         promoted=0, selection=0, given_idx=None, meta=meta, low=codes, high=None, idx=None,
-                         scale=scale, zero=zero, values=values, nonfinite=self._nonfinite_ptrs[0])
-        run = _PageRun(dict(values=codes, scale=scale, zero_point=zero), 0, 1,
-                       dict(original_shape=(B, H, tokens, D), original_dim=tokens, padded_dim=padded,
-                            packed_dim=packed_dim, group_size=kg, bits=bits, output_dtype=src.dtype, axis=2))
-        return [_PagedQuantized(run, p) for p in range(n_pages)]
-
-    def _quantize_value_chunks(self, value_states: torch.Tensor, chunk: int,
-                               jobs: Optional[list] = None) -> List[QuantizedTensor]:
-        """Value segments of ``chunk`` tokens (last may be shorter) quantized along head_dim.
-
-        All full chunks share one launch and one [B,H,T,P] code tensor; each
-        segment is a token-range view of it.  With ``jobs`` (a list) nothing is
-        launched here: each launch's (token start, token count, job, keepalive)
-        is appended for the caller to hand to the key launch of the same tokens.
-        """
-        c = self.config
-        B, H, T, D = value_states.shape
-        dev = value_states.device
-        bits, vg, meta = c.resolved_value_bits, c.resolved_value_group_size, c.metadata_dtype
-        Gv = (D + vg - 1) // vg
-        per = 8 // bits
-        padded = Gv * vg
-        packed_dim = ((padded + per - 1) // per) * per
-        full = T // chunk
-        out: List[QuantizedTensor] = []
-        for start, count, size in ((0, full, chunk), (full * chunk, 1 if T - full * chunk else 0, T - full * chunk)):
-            if not count:
-                continue
-            n = count * size
-            src = value_states[..., start:start + n, :]
-            values = torch.empty(B, H, n, packed_dim // per, dtype=torch.uint8, device=dev)
-            scale = torch.empty(B, H, n, Gv, dtype=meta, device=dev)
-            zero = torch.empty(B, H, n, Gv, dtype=meta, device=dev)
-            if jobs is None:
-                _launch_value_rows(src, bits, vg, meta, values, scale, zero, self._nonfinite_ptrs[1])
-            else:
-                job, keep = _value_rows_job(src, bits, vg, meta, values, scale, zero, self._nonfinite_ptrs[1])
-                jobs.append((start, n, job, keep))
-            run = _PageRun(dict(values=values, scale=scale, zero_point=zero), 2, size,
-                           dict(original_shape=(B, H, size, D), original_dim=D, padded_dim=padded,
-                                packed_dim=packed_dim, group_size=vg, bits=bits, output_dtype=value_states.dtype,
-                                axis=3))
-            out.extend(_PagedQuantized(run, i) for i in range(count))
-        return out
-
-    def _append_quantized_value_page(self, segment: QuantizedTensor) -> None:
-        """Merge token-wise values into page-sized segments (reference cache.py:514-542)."""
-        if not self._value_segments or isinstance(self._value_segments[-1], torch.Tensor):
-            self._value_segments.append(segment)
-            return
-        previous = self._value_segments[-1]
-        if not isinstance(previous, QuantizedTensor):
-            raise RuntimeError("unexpected value segment type while coalescing pages")
-        if previous.original_shape[-2] == self.config.page_size:
-            self._value_segments.append(segment)
-            return
-        combined = _merge_quantized_tensors([previous, segment])
-        n = combined.original_shape[-2]
-        self._value_segments[-1] = _slice_quantized_tensor(combined, 0, min(self.config.page_size, n))
-        if n > self.config.page_size:
-            self._value_segments.append(_slice_quantized_tensor(combined, self.config.page_size, n))
+                         promoted=0, selection=0, given_idx=None, meta=meta, low=t["values"], high=None, idx=None,
+                         scale=t["scale"], zero=t["zero_point"], values=values, nonfinite=flag)
+        packed = pool.shapes["values"][4]
+        return [PoolKeys(pool, slot + p, tokens, D, groups * kg, packed * (8 // bits), kg, bits, src.dtype)
+                for p in range(n_pages)]
 
     # ---- replayable decode steps ----
     def enable_device_tail(self) -> None:
@@ -803,6 +826,8 @@ class DartKVCache:
             raise ValueError("device-side tail counts need a held tail (hold_partial_pages or local_tokens)")
         if self._shape is None:
             raise RuntimeError("append the prompt before enabling device-side tail counts")
+        if self._tail_count_dev is not None:
+            return  # already on: a second call keeps the count tensor captured graphs read
         if self._tail_key is None:
             B, H, D = self._shape
             cap = self._tail_capacity()
@@ -828,6 +853,7 @@ class DartKVCache:
         if self._tail_count_dev is not None:
             if self._pending_key is not None and not self._pending_in_tail():
                 self._store_pending(self._pending_key, self._pending_value)
+                self._sealed_version += 1
             self._tail_count_dev.fill_(self._pending_tokens())
 
     def next_append_seals(self, tokens: int = 1) -> bool:
@@ -893,11 +919,9 @@ class DartKVCache:
         plan = self._decode_plan_cache
         if plan is not None and plan.version == self._sealed_version and plan.device == device:
             return plan
-        pairs = self.iter_segments()
-        tail_in_pairs = self.config.value_local_tokens == 0 and self._pending_in_tail()
-        sealed = pairs[:-1] if tail_in_pairs else pairs
-        tail_is_pending = tail_in_pairs or self._tail_count_dev is not None
-        keepalive: list = []
+        sealed = self._sealed_pairs()
+        tail_is_pending = self._tail_resident() or self._tail_count_dev is not None
+        keepalive: list = [dict(p.tensors) for p in self._pools()]  # storage outlives the table
         descs = (_lib.Segment * max(1, len(sealed)))()
         n_tokens = 0
         for i, (kseg, vseg) in enumerate(sealed):
@@ -919,9 +943,72 @@ class DartKVCache:
 # helpers
 # ---------------------------------------------------------------------------
 
-def _value_rows_job(src: torch.Tensor, bits: int, group: int, meta: torch.dtype, values: torch.Tensor,
-                    scale: torch.Tensor, zero: torch.Tensor, nonfinite: int = 0):
-    """The C description of quantizing [B,H,T,D] value rows along head_dim.
+def _union_pairs(keys: list, values: list) -> list:
+    """Cut two segment tracks that cover the same tokens at every boundary of either one; a piece that
+    covers part of a segment becomes that part, dequantized."""
+    if not keys or not values:
+        return []
+    k_len = [_segment_tokens(s) for s in keys]
+    v_len = [_segment_tokens(s) for s in values]
+    if min(k_len + v_len) <= 0:
+        raise RuntimeError("DartKVCache contains an empty logical segment")
+    k_ends, v_ends = list(accumulate(k_len)), list(accumulate(v_len))
+    if k_ends[-1] != v_ends[-1]:
+        raise RuntimeError("DartKVCache key/value logical lengths diverged")
+    pairs, start, ki, vi = [], 0, 0, 0
+    for stop in sorted(set(k_ends).union(v_ends)):
+        k0, v0 = k_ends[ki] - k_len[ki], v_ends[vi] - v_len[vi]
+        pairs.append((_piece(keys[ki], start - k0, stop - k0), _piece(values[vi], start - v0, stop - v0)))
+        ki += stop == k_ends[ki]
+        vi += stop == v_ends[vi]
+        start = stop
+    return pairs
+
+
+def _piece(segment: Segment, start: int, stop: int) -> Segment:
+    if start == 0 and stop == _segment_tokens(segment):
+        return segment
+    return _materialize(segment)[..., start:stop, :].contiguous()
+
+
+def _page_mode(segment: Segment) -> int:
+    """DENSE_PAGE 0, QUANTIZED_PAGE 1, MIXED_PAGE 2 (reference page_table.py:19-21)."""
+    if isinstance(segment, torch.Tensor):
+        return 0
+    return 2 if isinstance(segment, MixedQuantizedKey) else 1
+
+
+def _full_uniform(kseg: Segment, vseg: Segment, page: int) -> bool:
+    return (isinstance(kseg, QuantizedTensor) and isinstance(vseg, QuantizedTensor)
+            and kseg.original_shape[-2] == page and vseg.original_shape[-2] == page)
+
+
+def _same_run_layout(a: tuple, b: tuple) -> bool:
+    """Two full uniform pages whose packed fields stack into one page-major run."""
+    return all(x.original_shape == y.original_shape and x.bits == y.bits and x.group_size == y.group_size
+               and x.packed_dim == y.packed_dim and x.padded_dim == y.padded_dim for x, y in zip(a, b))
+
+
+def _run_fields(segments: list, names: tuple, page_major: bool) -> list:
+    """Page-major [n, ...] tensors of ``names`` over ``segments``: a slice of the pool when the segments
+    are consecutive slots (keys) or consecutive equal-length row runs (values), else a stacked copy."""
+    first = segments[0]
+    pool = getattr(first, "_pool", None)
+    n = len(segments)
+    step = 1 if page_major else first._rows if pool is not None else 0
+    if pool is not None and all(getattr(s, "_pool", None) is pool and s._at == first._at + i * step
+                                and (page_major or s._rows == step) for i, s in enumerate(segments)):
+        if page_major:
+            return [pool.field(name, first._at, n) for name in names]
+        # [B, H, n * rows, ...] -> [n, B, H, rows, ...]
+        return [pool.field(name, first._at, n * step).unflatten(2, (n, step)).movedim(2, 0) for name in names]
+    return [torch.stack([getattr(s, name) for s in segments], 0) for name in names]
+
+
+def _value_rows_job(src: torch.Tensor, bits: int, group: int, meta: torch.dtype, pool: Optional[PagePool],
+                    row0: int, nonfinite: int = 0, out: Optional[tuple] = None):
+    """The C description of quantizing [B,H,T,D] value rows along head_dim into value pool rows
+    [row0, row0 + T) (or, with ``out`` = (values, scale, zero) contiguous [B,H,T,...] tensors, into those).
 
     A token slice of a [B,H,T',D] tensor is B*H blocks of T contiguous rows;
     the kernel reads it in place.  Other layouts are copied first.  Returns
@@ -942,17 +1029,25 @@ def _value_rows_job(src: torch.Tensor, bits: int, group: int, meta: torch.dtype,
     if blocks is None:
         src = src.contiguous()
         blocks, block_stride = B * H, T * D
+    if out is not None:
+        values, scale, zero = out
+        out_rows, row0 = T, 0
+    else:
+        values, scale, zero = pool.tensors["values"], pool.tensors["scale"], pool.tensors["zero_point"]
+        out_rows = pool.capacity
     job = _lib.ValueRowsArgs(src=src.data_ptr(), src_dtype=_lib.dtype_code(src.dtype), blocks=blocks,
                              block_stride=block_stride, block_rows=T, n=D, row_stride=D, bits=bits, group=group,
                              values=values.data_ptr(), scale=scale.data_ptr(), zero=zero.data_ptr(),
-                             meta_dtype=_lib.dtype_code(meta), nonfinite=nonfinite or None)
+                             meta_dtype=_lib.dtype_code(meta), nonfinite=nonfinite or None,
+                             out_block_rows=out_rows, out_row0=row0)
     return job, src
 
 
 def _launch_value_rows(src: torch.Tensor, bits: int, group: int, meta: torch.dtype, values: torch.Tensor,
                        scale: torch.Tensor, zero: torch.Tensor, nonfinite: int = 0) -> None:
-    """Quantize [B,H,T,D] value rows along head_dim (dkv_quantize_value_rows)."""
-    job, src = _value_rows_job(src, bits, group, meta, values, scale, zero, nonfinite)
+    """Quantize [B,H,T,D] value rows along head_dim into contiguous [B,H,T,...] outputs
+    (dkv_quantize_value_rows)."""
+    job, src = _value_rows_job(src, bits, group, meta, None, 0, nonfinite, out=(values, scale, zero))
     lib = _lib.load()
     _lib.check(lib.dkv_quantize_value_rows(job, _lib.stream_ptr(src.device)), "dkv_quantize_value_rows")
 
@@ -965,52 +1060,15 @@ def _segment_tokens(segment: Segment) -> int:
     return segment.shape[-2] if isinstance(segment, torch.Tensor) else segment.original_shape[-2]
 
 
-def _slice_segment(segment: Segment, start: int, stop: int) -> Segment:
-    if start == 0 and stop == _segment_tokens(segment):
-        return segment
-    return _materialize(segment)[..., start:stop, :].contiguous()
-
-
-def _slice_quantized_tensor(segment: QuantizedTensor, start: int, stop: int) -> QuantizedTensor:
-    shape = list(segment.original_shape)
-    shape[-2] = stop - start
-    return QuantizedTensor(values=segment.values[..., start:stop, :], scale=segment.scale[..., start:stop, :],
-                           zero_point=segment.zero_point[..., start:stop, :], original_shape=tuple(shape),
-                           original_dim=segment.original_dim, padded_dim=segment.padded_dim,
-                           packed_dim=segment.packed_dim, group_size=segment.group_size, bits=segment.bits,
-                           output_dtype=segment.output_dtype, axis=segment.axis)
-
-
-def _merge_quantized_tensors(segments: list) -> QuantizedTensor:
-    if not segments:
-        raise ValueError("cannot merge an empty quantized segment list")
-    ref = segments[0]
-    if any((s.original_shape[:-2] != ref.original_shape[:-2] or s.original_dim != ref.original_dim
-            or s.padded_dim != ref.padded_dim or s.packed_dim != ref.packed_dim or s.group_size != ref.group_size
-            or s.bits != ref.bits or s.output_dtype != ref.output_dtype or s.axis != ref.axis)
-           for s in segments[1:]):
-        raise ValueError("quantized segments have incompatible layouts")
-    shape = list(ref.original_shape)
-    shape[-2] = sum(s.original_shape[-2] for s in segments)
-    return QuantizedTensor(values=torch.cat([s.values for s in segments], dim=-2),
-                           scale=torch.cat([s.scale for s in segments], dim=-2),
-                           zero_point=torch.cat([s.zero_point for s in segments], dim=-2),
-                           original_shape=tuple(shape), original_dim=ref.original_dim, padded_dim=ref.padded_dim,
-                           packed_dim=ref.packed_dim, group_size=ref.group_size, bits=ref.bits,
-                           output_dtype=ref.output_dtype, axis=ref.axis)
-
-
 def _segment_layout(segment: Segment) -> DartSegmentLayout:
     if isinstance(segment, torch.Tensor):
         return DartSegmentLayout("dense", tuple(segment.shape), (("values", tuple(segment.shape), tuple(segment.stride())),))
-    if isinstance(segment, QuantizedTensor):
-        fields = tuple((name, tuple(t.shape), tuple(t.stride())) for name, t in (
-            ("values", segment.values), ("scale", segment.scale), ("zero_point", segment.zero_point)))
-        return DartSegmentLayout("quantized", segment.original_shape, fields)
-    fields = tuple((name, tuple(t.shape), tuple(t.stride())) for name, t in (
-        ("low_values", segment.low_values), ("high_values", segment.high_values),
-        ("channel_indices", segment.channel_indices), ("scale", segment.scale), ("zero_point", segment.zero_point)))
-    return DartSegmentLayout("mixed_key", segment.original_shape, fields)
+    if isinstance(segment, MixedQuantizedKey):
+        kind, names = "mixed_key", ("low_values", "high_values", "channel_indices", "scale", "zero_point")
+    else:
+        kind, names = "quantized", ("values", "scale", "zero_point")
+    fields = tuple((name, tuple(t.shape), tuple(t.stride())) for name, t in ((n, getattr(segment, n)) for n in names))
+    return DartSegmentLayout(kind, tuple(segment.original_shape), fields)
 
 
 def _segment_nbytes(segment: Segment) -> int:
@@ -1051,13 +1109,14 @@ def _bh_block(t: torch.Tensor, keepalive: list) -> Tuple[int, int]:
 
 
 def _field_block(seg, name: str, keepalive: list) -> Tuple[int, int]:
-    """_bh_block of a segment field; a page of a run that has not materialized the field is read
-    from the run's tensor directly (no view); empty fields give (0, 0)."""
-    run = getattr(seg, "_run", None)
-    if run is not None and name not in seg.__dict__:
-        blk = run.block(name, seg._page)
-        if blk is not None:
-            return blk
+    """(address, (batch, head) stride) of a segment field; a pool segment's comes from the pool's layout
+    without making a view.  Empty fields give (0, 0)."""
+    pool = getattr(seg, "_pool", None)
+    if pool is not None:
+        shape = pool.shapes[name]
+        if 0 in shape[:pool.axis] + shape[pool.axis + 1:]:
+            return 0, 0
+        return seg.block(name)
     t = getattr(seg, name)
     if t.numel() == 0:
         return 0, 0

@@ -52,7 +52,14 @@ struct RowsParams {
   void* scale;
   void* zero;
   uint32_t* nonfinite;  // optional flag, set when a group holds a non-finite value
+  // output placement: source row blk * block_rows + i is written to output row
+  // blk * out_block_rows + out_row0 + i
+  int64_t out_block_rows, out_row0;
 };
+
+__device__ __forceinline__ int64_t out_row(const RowsParams& p, int64_t r) {
+  return (r / p.block_rows) * p.out_block_rows + p.out_row0 + r % p.block_rows;
+}
 
 __device__ __forceinline__ float row_elem(const RowsParams& p, int64_t r, int64_t i) {
   if (i >= p.n) i = p.n - 1;  // replicate the last element (quantization.py:174-177)
@@ -70,8 +77,9 @@ __device__ __forceinline__ void group_stats(const RowsParams& p, int64_t r, int6
   }
   flag_nonfinite(p.nonfinite, mn, mx);
   const float s = dev_group_scale(mn, mx, qmax, p.src_dtype);
-  dev_store_meta(p.scale, r * p.groups + g, s, p.meta_dtype);
-  dev_store_meta(p.zero, r * p.groups + g, mn, p.meta_dtype);
+  const int64_t o = out_row(p, r);
+  dev_store_meta(p.scale, o * p.groups + g, s, p.meta_dtype);
+  dev_store_meta(p.zero, o * p.groups + g, mn, p.meta_dtype);
   *mn_out = mn;
   *scale_out = s;
 }
@@ -84,7 +92,7 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_aligned(RowsParams p) 
   const float qmax = (float)((1 << p.bits) - 1);
   float mn, s;
   group_stats(p, r, g, qmax, &mn, &s);
-  uint8_t* out = p.values + r * p.packed_bytes;
+  uint8_t* out = p.values + out_row(p, r) * p.packed_bytes;
   const int64_t first = g * p.group;
   for (int64_t b = first / p.per_byte; b < (first + p.group) / p.per_byte; ++b) {
     uint32_t byte = 0;
@@ -185,7 +193,7 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
       mx = nmax(mx, __shfl_xor(mx, off, 64));
     }
     if (!active) continue;
-    r += blk * p.block_rows;  // output row
+    r += blk * p.out_block_rows + p.out_row0;  // output row
     const float s = rows_group_scale<SRC>(mn, mx, qmax, inv_qmax);
     const float y = __fdiv_rn(1.0f, s);
     if ((li & (lanes_per_group - 1)) == 0) {  // the group's first lane (groups are power-of-two lanes)
@@ -221,7 +229,7 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_serial(RowsParams p) {
   if (r >= p.rows) return;
   const float qmax = (float)((1 << p.bits) - 1);
   const int64_t padded = p.groups * p.group;
-  uint8_t* out = p.values + r * p.packed_bytes;
+  uint8_t* out = p.values + out_row(p, r) * p.packed_bytes;
   float mn = 0.0f, s = 1.0f;
   int64_t cur = -1;
   for (int64_t b = 0; b < p.packed_bytes; ++b) {
@@ -1057,7 +1065,8 @@ struct RowsLaunch {
 // Validate a value-row job and plan its launch (nothing is launched).
 static int prepare_rows(const void* src, int src_dtype, int64_t blocks, int64_t block_stride, int64_t block_rows,
                         int64_t n, int64_t row_stride, int64_t elem_stride, int bits, int64_t group, uint8_t* values,
-                        void* scale, void* zero, int meta_dtype, uint32_t* nonfinite, RowsLaunch& L) {
+                        void* scale, void* zero, int meta_dtype, uint32_t* nonfinite, int64_t out_block_rows,
+                        int64_t out_row0, RowsLaunch& L) {
   const int64_t rows = blocks * block_rows;
   DKV_CHECK(valid_float_dtype(src_dtype), DKV_ERR_DTYPE, "quantize expects a floating-point tensor (f32/f16/bf16)");
   DKV_CHECK(valid_meta_dtype(meta_dtype), DKV_ERR_DTYPE, "metadata dtype must be floating point");
@@ -1085,6 +1094,10 @@ static int prepare_rows(const void* src, int src_dtype, int64_t blocks, int64_t 
   p.scale = scale;
   p.zero = zero;
   p.nonfinite = nonfinite;
+  p.out_block_rows = out_block_rows > 0 ? out_block_rows : block_rows;
+  p.out_row0 = out_row0;
+  DKV_CHECK(p.out_block_rows >= block_rows && out_row0 >= 0 && out_row0 <= p.out_block_rows - block_rows,
+            DKV_ERR_INVALID, "value rows: output rows [out_row0, out_row0 + block_rows) must lie in out_block_rows");
   L.rows = rows;
   L.bits = bits;
   L.src_dtype = src_dtype;
@@ -1136,10 +1149,11 @@ static void launch_rows(const RowsLaunch& L, hipStream_t s) {
 static int quantize_rows_impl(const void* src, int src_dtype, int64_t blocks, int64_t block_stride,
                               int64_t block_rows, int64_t n, int64_t row_stride, int64_t elem_stride, int bits,
                               int64_t group, uint8_t* values, void* scale, void* zero, int meta_dtype,
-                              uint32_t* nonfinite, void* stream, const char* name) {
+                              uint32_t* nonfinite, int64_t out_block_rows, int64_t out_row0, void* stream,
+                              const char* name) {
   RowsLaunch L;
   const int rc = prepare_rows(src, src_dtype, blocks, block_stride, block_rows, n, row_stride, elem_stride, bits,
-                              group, values, scale, zero, meta_dtype, nonfinite, L);
+                              group, values, scale, zero, meta_dtype, nonfinite, out_block_rows, out_row0, L);
   if (rc != DKV_OK) return rc;
   if (L.rows == 0) return DKV_OK;
   launch_rows(L, (hipStream_t)stream);
@@ -1151,7 +1165,7 @@ extern "C" int dkv_quantize_rows(const void* src, int src_dtype, int64_t rows, i
                                  void* zero, int meta_dtype, void* stream) {
   DKV_CHECK(rows >= 0, DKV_ERR_INVALID, "rows must be non-negative");
   return quantize_rows_impl(src, src_dtype, 1, 0, rows, n, row_stride, elem_stride, bits, group, values, scale, zero,
-                            meta_dtype, nullptr, stream, "dkv_quantize_rows");
+                            meta_dtype, nullptr, 0, 0, stream, "dkv_quantize_rows");
 }
 
 extern "C" int dkv_quantize_row_blocks(const void* src, int src_dtype, int64_t blocks, int64_t block_stride,
@@ -1160,7 +1174,7 @@ extern "C" int dkv_quantize_row_blocks(const void* src, int src_dtype, int64_t b
   DKV_CHECK(blocks >= 0 && block_rows >= 0, DKV_ERR_INVALID, "blocks and block_rows must be non-negative");
   DKV_CHECK(block_rows == 0 || blocks <= INT64_MAX / block_rows, DKV_ERR_INVALID, "blocks * block_rows overflows");
   return quantize_rows_impl(src, src_dtype, blocks, block_stride, block_rows, n, row_stride, 1, bits, group, values,
-                            scale, zero, meta_dtype, nullptr, stream, "dkv_quantize_row_blocks");
+                            scale, zero, meta_dtype, nullptr, 0, 0, stream, "dkv_quantize_row_blocks");
 }
 
 extern "C" int dkv_quantize_value_rows(const dkv_value_rows_args* args, void* stream) {
@@ -1169,8 +1183,8 @@ extern "C" int dkv_quantize_value_rows(const dkv_value_rows_args* args, void* st
   DKV_CHECK(v.blocks >= 0 && v.block_rows >= 0, DKV_ERR_INVALID, "blocks and block_rows must be non-negative");
   DKV_CHECK(v.block_rows == 0 || v.blocks <= INT64_MAX / v.block_rows, DKV_ERR_INVALID, "blocks * block_rows overflows");
   return quantize_rows_impl(v.src, (int)v.src_dtype, v.blocks, v.block_stride, v.block_rows, v.n, v.row_stride, 1,
-                            (int)v.bits, v.group, v.values, v.scale, v.zero, (int)v.meta_dtype, v.nonfinite, stream,
-                            "dkv_quantize_value_rows");
+                            (int)v.bits, v.group, v.values, v.scale, v.zero, (int)v.meta_dtype, v.nonfinite,
+                            v.out_block_rows, v.out_row0, stream, "dkv_quantize_value_rows");
 }
 
 extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stream) {
@@ -1203,7 +1217,8 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
     DKV_CHECK(v.block_rows == 0 || v.blocks <= INT64_MAX / v.block_rows, DKV_ERR_INVALID,
               "value blocks * block_rows overflows");
     const int rc = prepare_rows(v.src, (int)v.src_dtype, v.blocks, v.block_stride, v.block_rows, v.n, v.row_stride, 1,
-                                (int)v.bits, v.group, v.values, v.scale, v.zero, (int)v.meta_dtype, v.nonfinite, VL);
+                                (int)v.bits, v.group, v.values, v.scale, v.zero, (int)v.meta_dtype, v.nonfinite,
+                                v.out_block_rows, v.out_row0, VL);
     if (rc != DKV_OK) return rc;
   }
   hipStream_t s = (hipStream_t)stream;

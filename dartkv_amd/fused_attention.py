@@ -12,7 +12,7 @@ from typing import Optional, Sequence
 
 import torch
 
-from .attention import decode_attention, streamed_dart_attention
+from .attention import MAX_GROUP, MAX_HEAD_DIM, decode_attention, segment_attention, streamed_dart_attention
 from .cache import DartKVCache
 from .page_table import DartPageRun, DartPageTable
 
@@ -45,6 +45,11 @@ def fused_dart_attention(
         raise ValueError("query heads must be divisible by cache KV heads")
     if page_table is not None or page_runs is not None:
         _validate_descriptors(query, cache, page_table, page_runs)
+    if query.shape[1] // kv_heads > MAX_GROUP or head_dim > MAX_HEAD_DIM:
+        if not fallback:
+            raise ValueError(f"the HIP decode kernels take at most {MAX_GROUP} query heads per KV head and "
+                             f"head_dim {MAX_HEAD_DIM}")
+        return segment_attention(query, cache, scale=scale)
     return decode_attention(query, cache, scale=scale)
 
 

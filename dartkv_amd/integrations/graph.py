@@ -44,9 +44,8 @@ class GraphDecodeStep:
         self.eager_steps = 0
         self.replays = 0
         self._graph: Optional[torch.cuda.CUDAGraph] = None
+        self._epoch = -1  # the cache's graph_epoch when the graph was captured
         self._fresh = True  # the decode descriptors are rebuilt by an eager step before a capture
-        if use_graph:
-            cache.enable_graph_decode()
 
     def _forward(self) -> None:
         out = self.model(self.input_ids, position_ids=self.position_ids, past_key_values=self.cache,
@@ -60,6 +59,15 @@ class GraphDecodeStep:
 
     def step(self) -> torch.Tensor:
         """Run one decode step; returns ``input_ids`` (now the generated tokens)."""
+        if self.use_graph and not self.cache.graph_decode_ready():
+            # device-side tail counts for every layer the prefill created (a step object may be built
+            # before the prefill); the step after enabling them runs eagerly
+            if not self.cache.layers or not all(layer.is_initialized for layer in self.cache.layers):
+                raise RuntimeError("GraphDecodeStep needs the prompt prefilled into every layer of the cache")
+            self.cache.enable_graph_decode()
+            self._fresh = True
+        if self._graph is not None and self.cache.graph_epoch != self._epoch:
+            self._graph, self._fresh = None, True  # batch rows moved: descriptors were rebuilt
         if not self.use_graph or self._fresh or self.cache.graph_step_seals():
             self._forward()
             self.eager_steps += 1
@@ -72,6 +80,7 @@ class GraphDecodeStep:
                 self._forward()
             graph.replay()
             self._graph = graph
+            self._epoch = self.cache.graph_epoch
             self.captures += 1
         else:
             self.cache.advance_graph_step(1)

@@ -23,7 +23,7 @@ Update lifecycle (reference huggingface.py:39-69, Kitty's PostQuant timing):
 
 from __future__ import annotations
 
-from typing import Callable, Dict, Optional
+from typing import Dict, Optional
 
 import torch
 
@@ -84,27 +84,21 @@ class DartCacheLayer(CacheLayerMixin):
         self.is_initialized = False
         self.last_update_prefill = False
 
-    def _rebuild(self, select: Callable[[torch.Tensor], torch.Tensor]) -> None:
-        """Re-pack the layer from ``select`` applied to its materialized contents.
-
-        Reference huggingface.py:117-127 rebuilds selected beams this way, with
-        no dense copy kept.
-        """
-        if self.cache.get_seq_length() == 0:
-            return
-        keys, values = self.cache.get()
-        rebuilt = DartKVCache(self.dart_config)
-        rebuilt.update(select(keys), select(values))
-        self.cache = rebuilt
-
+    # Batch reordering gathers the packed bytes along the batch axis (DartKVCache.reorder_batch); the
+    # reference re-packs the selected rows from their dequantized contents instead
+    # (huggingface.py:117-127), which changes the codes of a second quantization.
     def reorder_cache(self, beam_idx: torch.LongTensor) -> None:
-        self._rebuild(lambda t: t.index_select(0, beam_idx.to(t.device)))
+        self.cache.reorder_batch(beam_idx)
 
     def batch_repeat_interleave(self, repeats: int) -> None:
-        self._rebuild(lambda t: t.repeat_interleave(repeats, dim=0))
+        if self.cache.shape is not None:
+            rows = torch.arange(self.cache.shape[0], device=self.cache.device)
+            self.cache.reorder_batch(rows.repeat_interleave(repeats))
 
     def batch_select_indices(self, indices: torch.Tensor) -> None:
-        self._rebuild(lambda t: t[indices.to(t.device) if isinstance(indices, torch.Tensor) else indices])
+        if self.cache.shape is not None:
+            rows = torch.arange(self.cache.shape[0], device=self.cache.device)
+            self.cache.reorder_batch(rows[indices.to(rows.device) if isinstance(indices, torch.Tensor) else indices])
 
     def crop(self, tokens_to_remove: int) -> None:
         raise NotImplementedError("DartHFCache pages are append-only; crop is not supported")
@@ -124,6 +118,7 @@ class DartHFCache(Cache):
         super().__init__(layers=[])
         self.dart_config = config or DartKVCacheConfig()
         self._seen_tokens = 0
+        self.graph_epoch = 0  # bumps when batch rows move: captured decode graphs must be captured again
 
     # ---- lifecycle ----
     def _layer(self, layer_idx: int) -> DartCacheLayer:
@@ -181,7 +176,13 @@ class DartHFCache(Cache):
         again after it.
         """
         for layer in self.layers:
-            layer.cache.enable_device_tail()
+            if layer.is_initialized:
+                layer.cache.enable_device_tail()
+
+    def graph_decode_ready(self) -> bool:
+        """Whether every layer keeps its held-tail length on the device (``enable_graph_decode``)."""
+        return bool(self.layers) and all(layer.is_initialized and layer.cache.device_tail is not None
+                                         for layer in self.layers)
 
     def prepared_append_ok(self, layer_idx: int) -> bool:
         """Whether layer ``layer_idx`` can take its next token from the decode-step preparation kernel."""
@@ -219,11 +220,20 @@ class DartHFCache(Cache):
         return layer.page_runs(device=device, rebuild=rebuild) if layer is not None else None
 
     def reorder_cache(self, beam_idx: torch.LongTensor) -> "DartHFCache":
-        """Rebuild selected beams without retaining a dense fallback copy."""
+        """Reorder the beams of every layer; packed pages keep their bytes (no re-quantization)."""
         for layer in self.layers:
             layer.reorder_cache(beam_idx)
             layer.last_update_prefill = False
+        self.graph_epoch += 1
         return self
+
+    def batch_repeat_interleave(self, repeats: int) -> None:
+        super().batch_repeat_interleave(repeats)
+        self.graph_epoch += 1
+
+    def batch_select_indices(self, indices: torch.Tensor) -> None:
+        super().batch_select_indices(indices)
+        self.graph_epoch += 1
 
     # ---- dense views and accounting ----
     @property

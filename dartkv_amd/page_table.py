@@ -1,21 +1,29 @@
-"""Page descriptors for DartKV cache segments (reference src/dart/page_table.py:1-401).
+"""Page descriptors of a DartKV cache: the public ``DartPageTable`` / ``DartPageRun`` types.
 
-``DartPageTable`` and ``DartPageRun`` keep the reference's fields, validation
-order and messages.  They describe the cache for callers that inspect or
-reorder pages; the decode kernel itself reads the cache's device segment table
-(``DartKVCache.decode_plan``), so building these objects is never on the decode
-hot path.
+The field names, mode codes, validation messages and the run semantics are
+the reference's interface (reference src/dart/page_table.py:19-299).  The
+arrays themselves are views of the cache's own page directory and page pool:
+
+* ``DartPageTable.from_cache`` reads the cache's device page directory (an
+  int32 [N, 4] table of start, tokens, key mode and value mode per segment,
+  rebuilt only when a page is sealed), so a table costs no walk over Python
+  segment objects; ``page_ids`` and ``valid`` are broadcast views;
+* ``uniform_quantized_runs`` hands out slices of the page pool (keys are
+  page-major slots, values token-major rows), not stacked copies;
+* ``validate`` evaluates every per-page invariant on the device and reads
+  them back in one transfer.
+
+The decode kernels do not read these objects: they walk the descriptor table
+``DartKVCache.decode_plan`` builds.
 """
 
 from __future__ import annotations
 
+import dataclasses
 from dataclasses import dataclass
 from typing import TYPE_CHECKING, Sequence
 
 import torch
-
-from .mixed import MixedQuantizedKey
-from .quantization import QuantizedTensor
 
 if TYPE_CHECKING:
     from .cache import DartKVCache
@@ -23,25 +31,21 @@ if TYPE_CHECKING:
 DENSE_PAGE = 0
 QUANTIZED_PAGE = 1
 MIXED_PAGE = 2
-_VALID_PAGE_MODES = (DENSE_PAGE, QUANTIZED_PAGE, MIXED_PAGE)
 
 
-def _tokens(seg) -> int:
-    return seg.shape[-2] if isinstance(seg, torch.Tensor) else seg.original_shape[-2]
-
-
-def _mode(seg) -> int:
-    if isinstance(seg, torch.Tensor):
-        return DENSE_PAGE
-    return MIXED_PAGE if isinstance(seg, MixedQuantizedKey) else QUANTIZED_PAGE
+def _require(ok: bool, message: str) -> None:
+    if not ok:
+        raise ValueError(message)
 
 
 @dataclass(frozen=True)
 class DartPageTable:
     """Batch-indexed page descriptors on one device (reference page_table.py:30-48).
 
-    ``page_ids`` [B, N] maps each batch row to the segment index in
-    ``cache.iter_segments()``; the other arrays are page-major.
+    ``page_ids`` [B, N] maps a batch row to a segment index of
+    ``cache.iter_segments()``; ``sequence_starts`` / ``token_counts`` [N]
+    int32, ``key_modes`` / ``value_modes`` [N] int8 (``DENSE_PAGE``,
+    ``QUANTIZED_PAGE``, ``MIXED_PAGE``), ``valid`` [B, N] bool.
     """
 
     page_ids: torch.Tensor
@@ -55,33 +59,25 @@ class DartPageTable:
 
     @classmethod
     def from_cache(cls, cache: "DartKVCache", *, device=None) -> "DartPageTable":
-        """reference page_table.py:50-87."""
-        shape = cache.shape
-        batch = shape[0] if shape is not None else 0
-        segments = cache.iter_segments()
-        starts, counts, kmodes, vmodes = [], [], [], []
-        start = 0
-        for kseg, vseg in segments:
-            kt, vt = _tokens(kseg), _tokens(vseg)
-            if kt != vt:
-                raise RuntimeError("DartKVCache key/value page lengths diverged")
-            starts.append(start)
-            counts.append(kt)
-            kmodes.append(_mode(kseg))
-            vmodes.append(_mode(vseg))
-            start += kt
-        if start != cache.seen_tokens:
-            raise RuntimeError(f"page table covers {start} tokens, expected {cache.seen_tokens}")
+        """The table of ``cache`` as it is now (reference page_table.py:50-87), on ``device``."""
         target = torch.device(device) if device is not None else (cache.device or torch.device("cpu"))
-        n = len(segments)
-        ids = torch.arange(n, dtype=torch.int64, device=target).unsqueeze(0).expand(batch, -1).contiguous()
+        if target.type == "cuda" and target.index is None:
+            target = torch.device("cuda", torch.cuda.current_device())
+        shape = cache.shape
+        if shape is None:
+            directory = torch.zeros(0, 4, dtype=torch.int32, device=target)
+            batch = 0
+        else:
+            directory = cache._directory(target)
+            batch = shape[0]
+        n = directory.shape[0]
         return cls(
-            page_ids=ids,
-            sequence_starts=torch.tensor(starts, dtype=torch.int32, device=target),
-            token_counts=torch.tensor(counts, dtype=torch.int32, device=target),
-            key_modes=torch.tensor(kmodes, dtype=torch.int8, device=target),
-            value_modes=torch.tensor(vmodes, dtype=torch.int8, device=target),
-            valid=torch.ones((batch, n), dtype=torch.bool, device=target),
+            page_ids=torch.arange(n, dtype=torch.int64, device=target).expand(batch, n),
+            sequence_starts=directory[:, 0],
+            token_counts=directory[:, 1],
+            key_modes=directory[:, 2].to(torch.int8),
+            value_modes=directory[:, 3].to(torch.int8),
+            valid=torch.ones((), dtype=torch.bool, device=target).expand(batch, n),
             seen_tokens=cache.seen_tokens,
             page_size=cache.config.page_size,
         )
@@ -102,84 +98,71 @@ class DartPageTable:
         return self.page_count
 
     def validate(self) -> "DartPageTable":
-        """Shape, mode, id, order and total-length invariants (reference page_table.py:104-141)."""
+        """Shape, order, length, mode and id invariants, checked in the reference's order
+        (reference page_table.py:104-141)."""
         n = self.page_count
-        if self.page_ids.ndim != 2 or self.valid.shape != self.page_ids.shape:
-            raise ValueError("page_ids and valid must have shape [batch, page_count]")
-        for name, t in (("sequence_starts", self.sequence_starts), ("token_counts", self.token_counts),
-                        ("key_modes", self.key_modes), ("value_modes", self.value_modes)):
-            if t.ndim != 1 or t.shape[0] != n:
-                raise ValueError(f"{name} must have shape [page_count]")
-        if self.page_size <= 0 or self.seen_tokens < 0:
-            raise ValueError("page_size and seen_tokens must be non-negative/positive")
-        if n:
-            counts = self.token_counts.to("cpu", torch.int64)
-            starts = self.sequence_starts.to("cpu", torch.int64)
-            expected = torch.cumsum(torch.cat((torch.zeros(1, dtype=torch.int64), counts[:-1])), dim=0)
-            if not torch.equal(starts, expected):
-                raise ValueError("sequence_starts are not contiguous")
-            if bool((counts <= 0).any()):
-                raise ValueError("token_counts must be positive")
-            if int(counts.sum()) != self.seen_tokens:
-                raise ValueError("token_counts do not cover seen_tokens")
-            modes = torch.tensor(_VALID_PAGE_MODES)
-            if bool((~(self.key_modes.cpu().long()[:, None] == modes).any(dim=-1)).any()):
-                raise ValueError("key_modes contain an unsupported mode")
-            if bool((~(self.value_modes.cpu().long()[:, None] == modes).any(dim=-1)).any()):
-                raise ValueError("value_modes contain an unsupported mode")
-            ids = self.page_ids.cpu()[self.valid.cpu()]
-            if bool((ids < 0).any()) or bool((ids >= n).any()):
-                raise ValueError("valid page IDs are outside the page range")
-        elif self.seen_tokens != 0:
-            raise ValueError("an empty page table cannot cover non-empty cache")
+        _require(self.page_ids.ndim == 2 and self.valid.shape == self.page_ids.shape,
+                 "page_ids and valid must have shape [batch, page_count]")
+        for name in ("sequence_starts", "token_counts", "key_modes", "value_modes"):
+            t = getattr(self, name)
+            _require(t.ndim == 1 and t.shape[0] == n, f"{name} must have shape [page_count]")
+        _require(self.page_size > 0 and self.seen_tokens >= 0, "page_size and seen_tokens must be non-negative/positive")
+        if n == 0:
+            _require(self.seen_tokens == 0, "an empty page table cannot cover non-empty cache")
+            return self
+        counts = self.token_counts.to(torch.int64)
+        starts = self.sequence_starts.to(torch.int64)
+        ids_ok = ((self.page_ids >= 0) & (self.page_ids < n)) | ~self.valid
+        checks = torch.stack([
+            (starts == torch.cumsum(counts, 0) - counts).all(),
+            (counts > 0).all(),
+            counts.sum() == self.seen_tokens,
+            ((self.key_modes >= DENSE_PAGE) & (self.key_modes <= MIXED_PAGE)).all(),
+            ((self.value_modes >= DENSE_PAGE) & (self.value_modes <= MIXED_PAGE)).all(),
+            ids_ok.all(),
+        ]).tolist()
+        for ok, message in zip(checks, ("sequence_starts are not contiguous", "token_counts must be positive",
+                                        "token_counts do not cover seen_tokens", "key_modes contain an unsupported mode",
+                                        "value_modes contain an unsupported mode",
+                                        "valid page IDs are outside the page range")):
+            _require(ok, message)
         return self
 
     def sequence_ranges(self) -> torch.Tensor:
-        """[start, stop) per page on the table device."""
+        """[start, stop) of every page, [N, 2] on the table's device."""
         return torch.stack((self.sequence_starts, self.sequence_starts + self.token_counts), dim=-1)
 
     def reorder(self, batch_indices) -> "DartPageTable":
-        """Reorder batch rows like a beam update without touching packed storage."""
+        """Batch rows in a new order (a beam update); the packed storage is not touched."""
         indices = torch.as_tensor(batch_indices, dtype=torch.long, device=self.device)
         if indices.ndim != 1:
             raise ValueError("batch_indices must be one-dimensional")
         if indices.numel() and bool(((indices < 0) | (indices >= self.batch_size)).any()):
             raise IndexError("batch_indices contain an invalid batch row")
-        return DartPageTable(self.page_ids.index_select(0, indices), self.sequence_starts, self.token_counts,
-                             self.key_modes, self.value_modes, self.valid.index_select(0, indices),
-                             self.seen_tokens, self.page_size)
+        return dataclasses.replace(self, page_ids=self.page_ids.index_select(0, indices),
+                                   valid=self.valid.index_select(0, indices))
 
     def to(self, device) -> "DartPageTable":
-        return DartPageTable(self.page_ids.to(device), self.sequence_starts.to(device), self.token_counts.to(device),
-                             self.key_modes.to(device), self.value_modes.to(device), self.valid.to(device),
-                             self.seen_tokens, self.page_size)
+        """The same table with its arrays on ``device``."""
+        moved = {f.name: getattr(self, f.name).to(device) for f in dataclasses.fields(self)
+                 if isinstance(getattr(self, f.name), torch.Tensor)}
+        return dataclasses.replace(self, **moved)
 
     def uniform_quantized_runs(self, cache: "DartKVCache") -> tuple:
-        """Stack consecutive full uniform pages page-major (reference page_table.py:181-211)."""
-        segments = cache.iter_segments()
-        if len(segments) != self.page_count or cache.seen_tokens != self.seen_tokens:
-            raise ValueError("cache and page_table describe different page lifecycles")
-        runs = []
-        start = 0
-        while start < len(segments):
-            k0, v0 = segments[start]
-            if not _uniform_full(k0, v0, self.page_size):
-                start += 1
-                continue
-            end = start + 1
-            while end < len(segments):
-                k1, v1 = segments[end]
-                if not _uniform_full(k1, v1, self.page_size) or not _same_layout(k0, v0, k1, v1):
-                    break
-                end += 1
-            runs.append(_stack_run(self, segments[start:end], start))
-            start = end
-        return tuple(runs)
+        """Runs of consecutive full uniform pages with one layout, as page-major slices of the cache's
+        page pool (reference page_table.py:181-211).  Dense sink pages, mixed keys and the pending tail
+        end a run."""
+        return cache.uniform_page_runs(self)
 
 
 @dataclass(frozen=True)
 class DartPageRun:
-    """Page-major packed fields of one run of consecutive uniform pages (reference page_table.py:214-299)."""
+    """Page-major packed fields of consecutive uniform pages (reference page_table.py:214-299).
+
+    ``key_values`` [n, B, H, D, packed], ``key_scale`` / ``key_zero_point``
+    [n, B, H, D, groups], ``value_values`` [n, B, H, page, packed],
+    ``value_scale`` / ``value_zero_point`` [n, B, H, page, groups].
+    """
 
     first_page_index: int
     page_indices: torch.Tensor
@@ -197,6 +180,8 @@ class DartPageRun:
     value_group_size: int
     page_size: int
 
+    _PAGE_MAJOR = ("key_values", "key_scale", "key_zero_point", "value_values", "value_scale", "value_zero_point")
+
     @property
     def page_count(self) -> int:
         return self.page_indices.shape[0]
@@ -206,77 +191,33 @@ class DartPageRun:
         return self.key_values.device
 
     def validate(self) -> "DartPageRun":
-        if self.page_indices.ndim != 1:
-            raise ValueError("page_indices must have shape [run_pages]")
+        """Shape, id order, contiguity, width and size checks with the reference's messages."""
+        _require(self.page_indices.ndim == 1, "page_indices must have shape [run_pages]")
         n = self.page_count
-        if n == 0:
-            raise ValueError("a page run cannot be empty")
-        if self.first_page_index < 0:
-            raise ValueError("first_page_index must be non-negative")
-        for name, t in (("sequence_starts", self.sequence_starts), ("token_counts", self.token_counts)):
-            if t.ndim != 1 or t.shape[0] != n:
-                raise ValueError(f"{name} must have shape [run_pages]")
-        for name, t in (("key_values", self.key_values), ("key_scale", self.key_scale),
-                        ("key_zero_point", self.key_zero_point), ("value_values", self.value_values),
-                        ("value_scale", self.value_scale), ("value_zero_point", self.value_zero_point)):
-            if t.ndim < 1 or t.shape[0] != n:
-                raise ValueError(f"{name} must be page-major with first dimension {n}")
-        if bool((self.token_counts <= 0).any()):
-            raise ValueError("run token_counts must be positive")
+        _require(n > 0, "a page run cannot be empty")
+        _require(self.first_page_index >= 0, "first_page_index must be non-negative")
+        for name in ("sequence_starts", "token_counts"):
+            t = getattr(self, name)
+            _require(t.ndim == 1 and t.shape[0] == n, f"{name} must have shape [run_pages]")
+        for name in self._PAGE_MAJOR:
+            t = getattr(self, name)
+            _require(t.ndim >= 1 and t.shape[0] == n, f"{name} must be page-major with first dimension {n}")
+        _require(not bool((self.token_counts <= 0).any()), "run token_counts must be positive")
         if n > 1:
-            if not torch.equal(self.page_indices[1:], self.page_indices[:-1] + 1):
-                raise ValueError("page IDs in a run must be consecutive")
-            if not torch.equal(self.sequence_starts[1:], self.sequence_starts[:-1] + self.token_counts[:-1]):
-                raise ValueError("run sequence_starts are not contiguous")
-        if self.key_bits not in (2, 4, 8) or self.value_bits not in (2, 4, 8):
-            raise ValueError("run bit widths must be 2, 4, or 8")
-        if self.key_group_size <= 0 or self.value_group_size <= 0 or self.page_size <= 0:
-            raise ValueError("run group sizes and page_size must be positive")
+            _require(torch.equal(self.page_indices[1:] - self.page_indices[:-1],
+                                 torch.ones_like(self.page_indices[1:])), "page IDs in a run must be consecutive")
+            _require(torch.equal(self.sequence_starts[1:], self.sequence_starts[:-1] + self.token_counts[:-1]),
+                     "run sequence_starts are not contiguous")
+        _require(self.key_bits in (2, 4, 8) and self.value_bits in (2, 4, 8), "run bit widths must be 2, 4, or 8")
+        _require(min(self.key_group_size, self.value_group_size, self.page_size) > 0,
+                 "run group sizes and page_size must be positive")
         return self
 
     def to(self, device) -> "DartPageRun":
-        return DartPageRun(self.first_page_index, self.page_indices.to(device), self.sequence_starts.to(device),
-                           self.token_counts.to(device), self.key_values.to(device), self.key_scale.to(device),
-                           self.key_zero_point.to(device), self.value_values.to(device),
-                           self.value_scale.to(device), self.value_zero_point.to(device), self.key_bits,
-                           self.value_bits, self.key_group_size, self.value_group_size, self.page_size)
-
-
-def _uniform_full(kseg, vseg, page_size: int) -> bool:
-    return (isinstance(kseg, QuantizedTensor) and isinstance(vseg, QuantizedTensor)
-            and kseg.original_shape[-2] == page_size and vseg.original_shape[-2] == page_size)
-
-
-def _same_layout(k0, v0, k1, v1) -> bool:
-    if not isinstance(k1, QuantizedTensor) or not isinstance(v1, QuantizedTensor):
-        return False
-    return (k0.original_shape == k1.original_shape and v0.original_shape == v1.original_shape
-            and k0.values.shape == k1.values.shape and v0.values.shape == v1.values.shape
-            and k0.scale.shape == k1.scale.shape and v0.scale.shape == v1.scale.shape
-            and k0.bits == k1.bits and v0.bits == v1.bits
-            and k0.group_size == k1.group_size and v0.group_size == v1.group_size)
-
-
-def _stack_run(table: DartPageTable, segments: Sequence, first: int) -> DartPageRun:
-    keys = [p[0] for p in segments]
-    values = [p[1] for p in segments]
-    dev = keys[0].values.device
-    stop = first + len(segments)
-    run = DartPageRun(
-        first_page_index=first,
-        page_indices=table.page_ids[0, first:stop].to(dev),
-        sequence_starts=table.sequence_starts[first:stop].to(dev),
-        token_counts=table.token_counts[first:stop].to(dev),
-        key_values=torch.stack([s.values for s in keys], 0),
-        key_scale=torch.stack([s.scale for s in keys], 0),
-        key_zero_point=torch.stack([s.zero_point for s in keys], 0),
-        value_values=torch.stack([s.values for s in values], 0),
-        value_scale=torch.stack([s.scale for s in values], 0),
-        value_zero_point=torch.stack([s.zero_point for s in values], 0),
-        key_bits=keys[0].bits, value_bits=values[0].bits, key_group_size=keys[0].group_size,
-        value_group_size=values[0].group_size, page_size=table.page_size,
-    )
-    return run.validate()
+        """The same run with every array on ``device``."""
+        moved = {f.name: getattr(self, f.name).to(device) for f in dataclasses.fields(self)
+                 if isinstance(getattr(self, f.name), torch.Tensor)}
+        return dataclasses.replace(self, **moved)
 
 
 __all__ = ["DENSE_PAGE", "MIXED_PAGE", "QUANTIZED_PAGE", "DartPageTable", "DartPageRun"]

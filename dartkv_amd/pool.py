@@ -1,0 +1,197 @@
+"""Device page pool: growable storage for the packed pages of one cache.
+
+Key pages are page-major: every packed field is one tensor
+``[slots, B, H, ...]`` and a key page is one slot.  Value pages are
+token-major: every field is one tensor ``[B, H, rows, ...]`` with one row per
+token, so a value page is a run of consecutive rows, and value tokens
+quantized a few at a time fill their page in place.  The quantize kernels
+write straight into the pool (key pages with a page stride, value rows at a
+row offset inside each (batch, head) block), the decode kernels read it
+through descriptors, and a run of consecutive pages is a slice of the pool
+tensors, never a copy.
+
+Segments are views of a pool (a key slot, or a run of value rows) that
+behave as the reference's ``MixedQuantizedKey`` / ``QuantizedTensor``
+(reference src/dart/mixed.py:13-35, src/dart/quantization.py:56-76): their
+field tensors are read from the pool on access, so they follow the pool when
+it grows, moves or has its batch rows reordered.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from .mixed import MixedQuantizedKey
+from .quantization import QuantizedTensor
+
+
+class PagePool:
+    """Growable packed storage.  ``fields`` maps a field name to (shape, dtype) with the slot axis
+    ``axis`` sized 0; ``batch_axis`` is the batch dimension.  Slots [0, used) hold data."""
+
+    def __init__(self, fields: Dict[str, Tuple[Tuple[int, ...], torch.dtype]], axis: int, batch_axis: int,
+                 device: torch.device, align: int = 1) -> None:
+        self.shapes = {name: tuple(shape) for name, (shape, _) in fields.items()}
+        self.dtypes = {name: dtype for name, (_, dtype) in fields.items()}
+        self.axis, self.batch_axis, self.align = axis, batch_axis, align
+        self.device = device
+        self.capacity = 0
+        self.used = 0
+        self.tensors: Dict[str, torch.Tensor] = {}
+        self.generation = 0  # bumps whenever the tensors are replaced (field addresses change)
+
+    @property
+    def batch(self) -> int:
+        return next(iter(self.shapes.values()))[self.batch_axis]
+
+    def reserve(self, n: int, headroom: Optional[int] = None) -> int:
+        """Slots [start, start + n) for new data; grows (copying the used slots) when they do not fit."""
+        if self.used + n > self.capacity:
+            extra = max(self.align, (self.used + n) // 8) if headroom is None else headroom
+            cap = self.used + n + extra
+            cap = -(-cap // self.align) * self.align
+            self._resize(cap)
+        start = self.used
+        self.used += n
+        return start
+
+    def _resize(self, capacity: int) -> None:
+        fresh = {}
+        for name, shape in self.shapes.items():
+            full = list(shape)
+            full[self.axis] = capacity
+            t = torch.empty(full, dtype=self.dtypes[name], device=self.device)
+            old = self.tensors.get(name)
+            if old is not None and self.used:
+                t.narrow(self.axis, 0, self.used).copy_(old.narrow(self.axis, 0, self.used))
+            fresh[name] = t
+        self.tensors, self.capacity = fresh, capacity
+        self.generation += 1
+
+    def field(self, name: str, at: int, n: Optional[int] = None) -> torch.Tensor:
+        """Field ``name`` of slot ``at`` (n None: the slot axis dropped) or of slots [at, at + n)."""
+        t = self.tensors[name]
+        return t.select(self.axis, at) if n is None else t.narrow(self.axis, at, n)
+
+    def block(self, name: str, at: int) -> Tuple[int, int]:
+        """(address of slot ``at``'s (batch 0, head 0) block, elements between consecutive (batch, head)
+        blocks) of field ``name``: the form the decode descriptors take."""
+        t = self.tensors[name]
+        bh = t.stride(self.batch_axis + 1) if t.shape[self.batch_axis + 1] > 1 or t.shape[self.batch_axis] == 1 \
+            else t.stride(self.batch_axis)
+        return t.data_ptr() + at * t.stride(self.axis) * t.element_size(), bh
+
+    def select_batch(self, index: torch.Tensor) -> None:
+        """Keep batch rows ``index`` (a permutation or any selection): bytes are gathered, not recomputed.
+        With the batch size unchanged the gather lands in the same tensors, so descriptors stay valid."""
+        index = index.to(self.device)
+        same = index.numel() == self.batch
+        for name, t in self.tensors.items():
+            picked = t.index_select(self.batch_axis, index)
+            if same:
+                t.copy_(picked)
+            else:
+                self.tensors[name] = picked
+        if not same:
+            for name, shape in self.shapes.items():
+                s = list(shape)
+                s[self.batch_axis] = index.numel()
+                self.shapes[name] = tuple(s)
+            self.generation += 1
+
+    def to(self, device: torch.device) -> None:
+        self.tensors = {name: t.to(device) for name, t in self.tensors.items()}
+        self.device = device
+        self.generation += 1
+
+
+class _PoolField:
+    """A packed field of a pool-backed segment, read from the pool on every access."""
+
+    def __init__(self, name: str) -> None:
+        self.name = name
+
+    def __get__(self, obj, cls=None):
+        if obj is None:
+            return self
+        return obj._pool.field(self.name, obj._at, obj._rows)
+
+
+class PoolMixedKey(MixedQuantizedKey):
+    """One Dart key page stored in a key pool slot."""
+
+    low_values = _PoolField("low_values")
+    high_values = _PoolField("high_values")
+    channel_indices = _PoolField("channel_indices")
+    scale = _PoolField("scale")
+    zero_point = _PoolField("zero_point")
+
+    def __init__(self, pool: PagePool, slot: int, tokens: int, head_dim: int, padded_tokens: int, group_size: int,
+                 promote_bits: int, output_dtype: torch.dtype) -> None:  # pylint: disable=super-init-not-called
+        self._pool, self._at, self._rows = pool, slot, None
+        self._tokens, self._head_dim = tokens, head_dim
+        self.padded_tokens, self.group_size = padded_tokens, group_size
+        self.low_bits, self.promote_bits, self.output_dtype = 2, promote_bits, output_dtype
+
+    @property
+    def original_shape(self) -> Tuple[int, ...]:
+        s = self._pool.shapes["low_values"]
+        return (s[1], s[2], self._tokens, self._head_dim)
+
+    def block(self, name: str) -> Tuple[int, int]:
+        return self._pool.block(name, self._at)
+
+
+class PoolKeys(QuantizedTensor):
+    """One uniform key page (codes along the tokens) stored in a key pool slot."""
+
+    values = _PoolField("values")
+    scale = _PoolField("scale")
+    zero_point = _PoolField("zero_point")
+
+    def __init__(self, pool: PagePool, slot: int, tokens: int, head_dim: int, padded_dim: int, packed_dim: int,
+                 group_size: int, bits: int, output_dtype: torch.dtype) -> None:  # pylint: disable=super-init-not-called
+        self._pool, self._at, self._rows = pool, slot, None
+        self._head_dim = head_dim
+        self.original_dim, self.padded_dim, self.packed_dim = tokens, padded_dim, packed_dim
+        self.group_size, self.bits, self.output_dtype, self.axis = group_size, bits, output_dtype, 2
+
+    @property
+    def original_shape(self) -> Tuple[int, ...]:
+        s = self._pool.shapes["values"]
+        return (s[1], s[2], self.original_dim, self._head_dim)
+
+    def block(self, name: str) -> Tuple[int, int]:
+        return self._pool.block(name, self._at)
+
+
+class PoolValues(QuantizedTensor):
+    """Value rows [row0, row0 + rows) of a value pool: one value segment (codes along head_dim)."""
+
+    values = _PoolField("values")
+    scale = _PoolField("scale")
+    zero_point = _PoolField("zero_point")
+
+    def __init__(self, pool: PagePool, row0: int, rows: int, head_dim: int, padded_dim: int, packed_dim: int,
+                 group_size: int, bits: int, output_dtype: torch.dtype) -> None:  # pylint: disable=super-init-not-called
+        self._pool, self._at, self._rows = pool, row0, rows
+        self.original_dim, self.padded_dim, self.packed_dim = head_dim, padded_dim, packed_dim
+        self.group_size, self.bits, self.output_dtype, self.axis = group_size, bits, output_dtype, 3
+
+    @property
+    def original_shape(self) -> Tuple[int, ...]:
+        s = self._pool.shapes["values"]
+        return (s[0], s[1], self._rows, self.original_dim)
+
+    def rows(self, start: int, count: int) -> "PoolValues":
+        """The segment's rows [start, start + count) as a segment of their own."""
+        return PoolValues(self._pool, self._at + start, count, self.original_dim, self.padded_dim, self.packed_dim,
+                          self.group_size, self.bits, self.output_dtype)
+
+    def block(self, name: str) -> Tuple[int, int]:
+        return self._pool.block(name, self._at)
+
+
+__all__ = ["PagePool", "PoolMixedKey", "PoolKeys", "PoolValues"]

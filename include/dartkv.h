@@ -47,7 +47,7 @@ extern "C" {
 /* Thread-local description of the last error on this thread. */
 const char* dkv_last_error(void);
 
-/* ABI version (9); bumps when a struct or an entry point below changes. */
+/* ABI version (10); bumps when a struct or an entry point below changes. */
 int dkv_abi_version(void);
 
 /*
@@ -103,6 +103,11 @@ typedef struct dkv_value_rows_args {
    * NaN or an infinity (the reference raises ValueError for such inputs,
    * src/dart/quantization.py:159-160); never cleared by the library. */
   uint32_t* nonfinite;
+  /* Output placement: source row blk * block_rows + i goes to output row
+   * blk * out_block_rows + out_row0 + i (out_block_rows 0: block_rows, the
+   * contiguous layout), so a caller can quantize new token rows straight into
+   * a [B][H][capacity][...] store at token offset out_row0. */
+  int64_t out_block_rows, out_row0;
 } dkv_value_rows_args;
 
 /*

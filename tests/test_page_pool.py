@@ -1,0 +1,176 @@
+"""The device page pool behind DartKVCache (GPU): byte-exact batch reordering, page runs as pool slices,
+page tables as views of the page directory, and attention for shapes beyond the HIP decode kernels.
+
+Reordering is checked against the cache's own bytes (every packed field of every segment, row by row)
+and against the oracle on the reordered inputs; the reference re-quantizes reordered rows
+(integrations/huggingface.py:117-127), which this build deliberately does not, so the oracle comparison
+is of decode outputs, not of codes.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from tests.golden_util import bits_equal
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _fields(seg):
+    if isinstance(seg, torch.Tensor):
+        return [seg]
+    if hasattr(seg, "low_values"):
+        return [seg.low_values, seg.high_values, seg.channel_indices, seg.scale, seg.zero_point]
+    return [seg.values, seg.scale, seg.zero_point]
+
+
+def _snapshot(cache):
+    return [[t.detach().clone() for t in _fields(k) + _fields(v)] for k, v in cache.iter_segments()]
+
+
+def _cache(B, T, **over):
+    import dartkv_amd as dart
+    from dartkv_amd import synthetic
+    cfg = dict(bits=2, page_size=128, key_group_size=128, value_group_size=64, promote_ratio=0.25, sink_tokens=32,
+               hold_partial_pages=True, metadata_dtype=torch.float16)
+    cfg.update(over)
+    k, v, q = synthetic.outlier_kv(B, 4, T, 128, query_heads=16, dtype=torch.bfloat16, seed=B * 7 + T, device=DEV)
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    cache.append(k, v)
+    return cache, k, v, q
+
+
+@pytest.mark.parametrize("index", [[2, 0, 1], [1, 1, 0], [0, 2], [2, 2, 1, 0, 0]])
+@pytest.mark.parametrize("over", [{}, dict(promote_ratio=0.0, bits=4), dict(page_size=64, key_group_size=32,
+                                                                              value_group_size=32, sink_tokens=5)])
+def test_reorder_batch_gathers_packed_bytes(index, over):
+    """Every packed field of every segment, batch row by row, is the old row the index names; the decode
+    of the reordered cache is the reordered decode, bit for bit."""
+    import dartkv_amd as dart
+    cache, k, v, q = _cache(3, 700, **over)
+    before = _snapshot(cache)
+    out_before = dart.decode_attention(q, cache)
+    idx = torch.tensor(index, device=DEV)
+    cache.reorder_batch(idx)
+    after = _snapshot(cache)
+    assert len(after) == len(before)
+    for seg_before, seg_after in zip(before, after):
+        for a, b in zip(seg_before, seg_after):
+            assert bits_equal(a.index_select(0, idx).cpu(), b.cpu())
+    out_after = dart.decode_attention(q.index_select(0, idx), cache)
+    torch.cuda.synchronize()
+    expected = out_before.index_select(0, idx).cpu()
+    if len(index) == 3:  # same batch size, same split counts: the same arithmetic
+        assert bits_equal(out_after.cpu(), expected)
+    else:  # another batch size may choose other split counts (fp16 rounding of the weights differs)
+        err = float(((out_after.float().cpu() - expected.float()).abs().amax(-1) /
+                     expected.float().abs().amax(-1)).max())
+        assert err <= 1e-2, err
+    assert cache.shape[0] == len(index)
+    # appends after a reorder keep working: one token, then enough to seal a page
+    nk, nv = k[:1, :, :200].expand(len(index), -1, -1, -1).contiguous(), v[:1, :, :200].expand(len(index), -1, -1, -1).contiguous()
+    cache.append(nk[:, :, :1], nv[:, :, :1])
+    cache.append(nk[:, :, 1:], nv[:, :, 1:])
+    assert cache.get_seq_length() == 900
+    assert bool(torch.isfinite(dart.decode_attention(q.index_select(0, idx), cache).float()).all())
+
+
+def test_reordered_cache_decodes_like_the_oracle_on_reordered_inputs():
+    import dartkv_amd as dart
+    from oracle import dart_oracle as O
+    cache, k, v, q = _cache(3, 900)
+    idx = [2, 0, 1]
+    cache.reorder_batch(idx)
+    out32 = torch.empty(3, 16, 128, dtype=torch.float32, device=DEV)
+    dart.decode_attention(q[idx], cache, out_f32=out32)
+    cfg = dict(bits=2, page_size=128, key_group_size=128, value_group_size=64, promote_ratio=0.25, sink_tokens=32,
+               hold_partial_pages=True, metadata_dtype=torch.float16)
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    oc.append(k[idx].cpu(), v[idx].cpu())
+    _, ref32 = O.streamed_attention(q[idx].cpu(), oc, return_fp32=True)
+    a, b = out32.cpu(), ref32.reshape(3, 16, 128)
+    err = float(((a - b).abs().amax(-1) / b.abs().amax(-1)).max())
+    assert err <= 2e-3, err
+
+
+def test_hf_reorder_select_and_repeat_keep_bytes_and_length():
+    import dartkv_amd as dart
+    from dartkv_amd.integrations import DartHFCache
+    from dartkv_amd import synthetic
+    cfg = dart.DartKVCacheConfig(bits=2, page_size=16, key_group_size=16, value_group_size=16, promote_ratio=0.25,
+                                 sink_tokens=3, hold_partial_pages=True, metadata_dtype=torch.float16)
+    k, v, _ = synthetic.outlier_kv(4, 2, 50, 32, dtype=torch.bfloat16, seed=3, device=DEV)
+    hf = DartHFCache(cfg)
+    for layer in range(2):
+        hf.update(k, v, layer)
+    rows0 = [hf.layer_for_attention(i).get() for i in range(2)]
+    epoch = hf.graph_epoch
+    hf.reorder_cache(torch.tensor([3, 2, 1, 0]))
+    assert hf.graph_epoch == epoch + 1 and hf.get_seq_length() == 50
+    for i in range(2):
+        kk, vv = hf.layer_for_attention(i).get()
+        assert bits_equal(kk.cpu(), rows0[i][0].flip(0).cpu()) and bits_equal(vv.cpu(), rows0[i][1].flip(0).cpu())
+    hf.batch_select_indices(torch.tensor([0, 2]))
+    kk, _ = hf.layer_for_attention(0).get()
+    assert kk.shape[0] == 2 and bits_equal(kk.cpu(), rows0[0][0][[3, 1]].cpu())
+    hf.batch_repeat_interleave(2)
+    kk, _ = hf.layer_for_attention(1).get()
+    assert kk.shape[0] == 4 and bits_equal(kk.cpu(), rows0[1][0][[3, 3, 1, 1]].cpu())
+    out_k, _ = hf.update(k[:4, :, :1], v[:4, :, :1], 0)
+    assert out_k.shape == (4, 2, 51, 32)
+
+
+def test_page_runs_are_pool_slices_and_tables_follow_the_tail():
+    import dartkv_amd as dart
+    cache, k, v, q = _cache(2, 1000, promote_ratio=0.0, bits=4)
+    runs = cache.page_runs()
+    assert len(runs) == 1 and runs[0].page_count == (1000 - 32) // 128
+    run = runs[0].validate()
+    pairs = cache.iter_segments()
+    for p in range(run.page_count):
+        ks, vs = pairs[1 + p]
+        assert bits_equal(run.key_values[p].cpu(), ks.values.cpu())
+        assert bits_equal(run.value_values[p].cpu(), vs.values.cpu())
+        assert bits_equal(run.value_scale[p].cpu(), vs.scale.cpu())
+    pool = cache._key_pool
+    assert run.key_values.data_ptr() == pool.tensors["values"][pairs[1][0]._at].data_ptr()  # a view, not a copy
+    assert run.value_values.untyped_storage().data_ptr() == cache._value_pool.tensors["values"].untyped_storage().data_ptr()
+    table = cache.page_table()
+    assert table.sequence_starts.untyped_storage().data_ptr() == table.token_counts.untyped_storage().data_ptr()
+    last = table.token_counts[-1].item()
+    cache.append(k[:, :, :1], v[:, :, :1])
+    fresh = cache.page_table().validate()
+    assert fresh is not table and fresh.token_counts[-1].item() == last + 1
+    assert table.token_counts[-1].item() == last  # an old table keeps its snapshot
+    assert fresh.page_count == table.page_count
+
+
+@pytest.mark.parametrize("Hkv,Hq,D", [(1, 20, 64), (2, 4, 640)])
+def test_shapes_beyond_the_decode_kernels_fall_back_to_segment_attention(Hkv, Hq, D):
+    """More than 16 query heads per KV head, or head_dim above 512: fused (fallback=True) and streamed
+    attention run segment_attention and match the oracle; fused with fallback=False raises."""
+    import dartkv_amd as dart
+    from dartkv_amd import synthetic
+    from dartkv_amd.attention import segment_attention
+    from oracle import dart_oracle as O
+    cfg = dict(bits=2, page_size=32, key_group_size=32, value_group_size=32, promote_ratio=0.25, sink_tokens=4,
+               hold_partial_pages=True, metadata_dtype=torch.float16)
+    k, v, q = synthetic.outlier_kv(2, Hkv, 150, D, query_heads=Hq, dtype=torch.bfloat16, seed=D)
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    cache.append(k.to(DEV), v.to(DEV))
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    oc.append(k, v)
+    _, ref32 = O.streamed_attention(q, oc, return_fp32=True)
+    out32 = torch.empty(2, Hq, 1, D, dtype=torch.float32, device=DEV)
+    segment_attention(q.to(DEV), cache, out_f32=out32)
+    a, b = out32.cpu().flatten(2), ref32.flatten(2)
+    err = float(((a - b).abs().amax(-1) / b.abs().amax(-1)).max())
+    assert err <= 1e-5, err
+    fused = dart.fused_dart_attention(q.to(DEV), cache)
+    streamed = dart.streamed_dart_attention(q.to(DEV), cache)
+    assert bits_equal(fused.cpu(), streamed.cpu())
+    with pytest.raises(ValueError, match="query heads per KV head"):
+        dart.fused_dart_attention(q.to(DEV), cache, fallback=False)
