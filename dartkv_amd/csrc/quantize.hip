@@ -15,6 +15,7 @@
 #include "dkv_capi_util.h"
 #include "dkv_device.h"
 #include "dkv_select.h"
+#include "dkv_select_wave.h"
 
 using namespace dkv;
 
@@ -258,6 +259,60 @@ struct KeyParams {
   int64_t nb;           // mixed: bytes per group
   int64_t pk;           // uniform: bytes per channel
 };
+
+// One wave64 as the lane model of dkv_select_wave.h: lane l owns positions l
+// and l + 64; LDS written by one lane is read by another only across sync().
+struct DeviceWave {
+  int lane;
+  template <class T>
+  struct PerPos {
+    T v[2];
+    __device__ T& at(int, int h) { return v[h]; }
+  };
+  template <class F>
+  __device__ void each(F fn) {
+    fn(lane, 0);
+    fn(lane + 64, 1);
+  }
+  template <class F>
+  __device__ uint64_t ballot(F pred, int h) {
+    return __ballot(pred(lane + 64 * h));
+  }
+  __device__ bool first_lane() const { return lane == 0; }
+  __device__ void sync() const {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+};
+
+// Promoted channels of n <= 128 scores in torch.topk(sorted=True) order,
+// ties included, by the calling wave (every lane of it calls): packed (rank,
+// index) words, the wave-parallel selection, and lane 0 alone on the serial
+// form where libstdc++ takes heap select or partial_sort.  wb.stack holds
+// 3 * kSelectStack ints.  The K indices go to `out` (LDS or global memory).
+constexpr int kSelectStack = 16;  // >= 2 floor(log2(128)) + 1
+static_assert(kSelectStack >= kWaveSelStack, "one stack serves both forms");
+
+__device__ __forceinline__ void wave_select_topk(const float* score, int n, int K, int lane, const WaveSelBuffers& wb,
+                                                 int32_t* out) {
+  DeviceWave w{lane};
+  auto fill = [&]() {
+    w.each([&](int x, int) {
+      if (x < n) wb.a[x] = (sel_rank(score[x], score, n) << 7) | (uint32_t)x;
+    });
+    w.sync();
+  };
+  fill();
+  if (!wsel_topk(wb, w, n, K)) {
+    fill();
+    if (lane == 0) sel_topk(n, K, PtrArray<PackedItem>{(PackedItem*)wb.a}, PtrArray<int>{wb.stack}, kSelectStack);
+    w.sync();
+  }
+  w.each([&](int x, int) {
+    if (x < K) out[x] = (int32_t)(wb.a[x] & 127u);
+  });
+}
 
 __device__ __forceinline__ float key_elem(const KeyParams& k, int64_t b, int64_t h, int64_t page, int64_t t,
                                           int64_t c) {
@@ -645,14 +700,16 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_tiled(KeyParams k
 //   3. selection: each channel's rank is the number of channels with a larger
 //      score; with all scores distinct, rank < K is the promoted set in
 //      torch.topk(sorted=True) order.  A page with equal (or NaN) scores needs
-//      the exact serial selection (select_topk).  Equal bf16 scores are the
-//      rule, not the exception (32 of 128 means in about one binade), so for
-//      many pages the launcher runs mode kKeyScores (steps 1-2, scores to the
-//      page's low-code region), key_select_pages (one lane per page) and mode
-//      kKeyCodes (steps 1, 4, 5 with the channels and the channel ranges read
-//      back); mode kKeyAll does everything here (pages without a
-//      data-dependent selection, and the rank path with the one-lane fallback
-//      when few pages are quantized);
+//      the exact libstdc++ order, which wave 0 computes (wave_select_topk)
+//      while the other waves wait.  Equal bf16 scores are the rule, not the
+//      exception (32 of 128 means in about one binade), so for many pages the
+//      launcher runs mode kKeyScores (steps 1-2, scores to the page's low-code
+//      region), key_select_pages (one wave per page: many selections in
+//      flight hide the latency of their dependent LDS steps, which a
+//      workgroup waiting on its own cannot) and mode kKeyCodes (steps 1, 4, 5
+//      with the channels and the channel ranges read back); mode kKeyAll does
+//      everything here (pages without a data-dependent selection, and few
+//      pages);
 //   4. scales, zero points and one reciprocal per channel;
 //   5. codes: thread (c, half) quantizes 64 tokens of channel c with the
 //      exact chain (div_rn); the packed rows leave through LDS.
@@ -719,8 +776,9 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
   __shared__ __attribute__((aligned(16))) float score[kFastKeyD];
   __shared__ float ch_mn[kFastKeyD], ch_s[kFastKeyD], ch_y[kFastKeyD];
   __shared__ int32_t slot[kFastKeyD], sel[kFastKeyD];
-  __shared__ SelItem work[kFastKeyD];
-  __shared__ int sel_stack[3 * kSelStack];
+  __shared__ uint32_t sel_words[kFastKeyD];
+  __shared__ uint8_t sel_lpos[kFastKeyD], sel_rpos[kFastKeyD];
+  __shared__ int sel_stack[3 * kSelectStack];
   const dkv_key_pages_args& a = k.a;
   const int bh = blockIdx.x, page = blockIdx.y;
   const int b = bh / (int)a.H, h = bh % (int)a.H;
@@ -833,7 +891,8 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
         }
       }
       if (__syncthreads_or(tie)) {
-        if (tid == 0) select_topk(score, kFastKeyD, K, work, sel, sel_stack);
+        if (tid < 64)
+          wave_select_topk(score, kFastKeyD, K, tid, WaveSelBuffers{sel_words, sel_lpos, sel_rpos, sel_stack}, sel);
       } else if (half == 0 && rank < K) {
         sel[rank] = c;
       }
@@ -918,54 +977,41 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
 }
 
 // Promoted-channel selection for many pages at once: one wave per
-// (batch * head, page) runs the exact top-k on the scores kKeyScores left in
-// the page's low-code region and writes the channel indices.  The selection
-// is a serial chain of data-dependent LDS reads and writes; with one page per
-// lane the lanes' different branches serialized inside the wave (C3: 253 us),
-// so lane 0 runs it alone while the wave's lanes only load the scores, and the
-// small LDS footprint lets many such waves run side by side.
+// (batch * head, page) runs the exact top-k (wave_select_topk) on the scores
+// kKeyScores left in the page's low-code region and writes the channel
+// indices.  The selection is a chain of dependent LDS steps; its small LDS
+// footprint lets many such waves run side by side and hide that latency.
 constexpr int kSelectMaxD = 128;
-constexpr int kSelectStack = 16;  // >= 2 floor(log2(kSelectMaxD)) + 1
 
-// Page `item` (page-major over (b, h)): the lanes of one wave stage its scores
-// in `sc` and turn each into a packed (rank, index) word in `work` (the rank
-// orders and ties exactly like the score), then lane 0 runs the exact
-// selection on the words (one 4-byte LDS access and an integer compare per
-// step) and writes the indices.
-__device__ __forceinline__ void select_page(const KeyParams& k, int row_bytes, int64_t item, int lane,
-                                            PackedItem* work, float* sc, int* stack) {
+struct SelectLds {
+  float sc[kSelectMaxD];
+  uint32_t words[kSelectMaxD];
+  uint8_t lpos[kSelectMaxD], rpos[kSelectMaxD];
+  int stack[3 * kSelectStack];
+};
+
+__device__ __forceinline__ void select_page(const KeyParams& k, int row_bytes, int64_t item, int lane, SelectLds& l) {
   const dkv_key_pages_args& a = k.a;
   const int64_t bhs = a.B * a.H;
   const int64_t page = item / bhs, bh = item % bhs;
   const int D = (int)a.D, K = (int)a.promoted;
   const float* score = (const float*)(a.low + page * a.low_page_stride + bh * D * row_bytes);
-  for (int j = lane; j < D; j += 64) sc[j] = score[j];
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  for (int j = lane; j < D; j += 64) work[j] = PackedItem{(sel_rank(sc[j], sc, D) << 7) | (uint32_t)j};
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane != 0) return;
+  for (int j = lane; j < D; j += 64) l.sc[j] = score[j];
+  DeviceWave{lane}.sync();
   int32_t* idx_out = (int32_t*)((char*)a.idx + page * a.idx_page_stride) + bh * K;
-  const PtrArray<PackedItem> w{work};
-  sel_topk(D, K, w, PtrArray<int>{stack}, kSelectStack);
-  for (int j = 0; j < K; ++j) idx_out[j] = (int32_t)(w.get(j).k & 127u);
+  wave_select_topk(l.sc, D, K, lane, WaveSelBuffers{l.words, l.lpos, l.rpos, l.stack}, idx_out);
 }
 
 __global__ void __launch_bounds__(64) key_select_pages(KeyParams k, int row_bytes) {
-  __shared__ PackedItem work[kSelectMaxD];
-  __shared__ float sc[kSelectMaxD];
-  __shared__ int stack[3 * kSelectStack];
-  select_page(k, row_bytes, blockIdx.x, threadIdx.x, work, sc, stack);
+  __shared__ SelectLds l;
+  select_page(k, row_bytes, blockIdx.x, threadIdx.x, l);
 }
 
 // The key path's channel selection and a value-row job in one launch.
 // Workgroups [0, sel_blocks) select (one wave per page, as key_select_pages);
 // the others quantize value rows (workgroup b - sel_blocks of the gx x gy grid
-// of quantize_rows_vec).  A selection keeps one lane busy and its wave waiting
-// on LDS; the value rows use the rest of each SIMD meanwhile.
+// of quantize_rows_vec).  A selection wave mostly waits on its LDS steps;
+// the value rows use each SIMD meanwhile.
 constexpr int kSelectWaves = kThreads / 64;
 // Shared launches pay off while every selection wave is resident at once (one
 // wave per page, 256 CUs x 32 waves); past that the selections queue in rounds
@@ -976,13 +1022,11 @@ template <int BITS, int SRC>
 __global__ void __launch_bounds__(kThreads) select_pages_and_rows(KeyParams k, int row_bytes, int64_t items,
                                                                   int64_t sel_blocks, RowsParams p, int lpg,
                                                                   int row_shift, int64_t gx, int64_t gy) {
-  __shared__ PackedItem work[kSelectWaves][kSelectMaxD];
-  __shared__ float sc[kSelectWaves][kSelectMaxD];
-  __shared__ int stack[kSelectWaves][3 * kSelectStack];
+  __shared__ SelectLds l[kSelectWaves];
   if ((int64_t)blockIdx.x < sel_blocks) {
     const int wave = threadIdx.x >> 6;
     const int64_t item = (int64_t)blockIdx.x * kSelectWaves + wave;
-    if (item < items) select_page(k, row_bytes, item, threadIdx.x & 63, work[wave], sc[wave], stack[wave]);
+    if (item < items) select_page(k, row_bytes, item, threadIdx.x & 63, l[wave]);
     return;
   }
   const int64_t b = (int64_t)blockIdx.x - sel_blocks;

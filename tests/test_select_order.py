@@ -4,7 +4,8 @@ torch.topk(sorted=True) on CPU orders tied scores the way libstdc++'s
 nth_element / sort / partial_sort leave them (reference src/dart/mixed.py:155-161
 selects promoted channels with it), so the HIP selection restates those
 algorithms.  A host build of the same header is run against std:: on random
-scores with many ties, for both item forms the GPU uses.  The GPU kernels are
+scores with many ties, for both item forms the GPU uses, and a host model of the
+wave-parallel form (dkv_select_wave.h) likewise.  The GPU kernels are
 checked end to end by the golden tie-order vectors (test_gpu_parity.py).
 """
 
@@ -51,3 +52,18 @@ def test_selection_matches_torch_topk_on_ties(tmp_path):
         want = torch.topk(s, k, sorted=True).indices.tolist()
         assert [int(x) for x in lines[2 * c].split()] == want, (n, k)
         assert [int(x) for x in lines[2 * c + 1].split()] == want, (n, k)
+
+
+def test_wave_selection_matches_libstdcxx(tmp_path):
+    """The wave-parallel form (dartkv_amd/csrc/dkv_select_wave.h), its 64 lanes run in a loop on the host,
+    gives the first k items of std::nth_element + std::sort for random tied scores, NaN and presorted runs
+    included; where libstdc++ would take partial_sort or heap select it hands back (counted, not compared)."""
+    exe = tmp_path / "select_wave"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-I", os.path.join(REPO, "dartkv_amd", "csrc"),
+                    os.path.join(REPO, "tests", "select", "select_wave.cpp"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe), "30000"], capture_output=True, text=True)
+    print(out.stdout.strip())
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "mismatches 0" in out.stdout
+    fallbacks = int(out.stdout.split("fallbacks")[1])
+    assert fallbacks < 30000 // 20  # the parallel form covers nearly every case (k * 64 > n)
