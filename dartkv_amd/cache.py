@@ -128,6 +128,43 @@ class DartKVCacheConfig:
         return self.value_group_size if self.value_group_size is not None else self.group_size
 
 
+class _FiniteScope:
+    """Bookkeeping of one append's non-finite check: the flags once a quantize launch uses them, and
+    what a failed check restores.  Within an append the tracks only grow, or change their last
+    element (a value page filled further, a key page packed again), so their lengths and last
+    elements are a complete snapshot."""
+
+    __slots__ = ("flags", "tracks", "pools", "pending", "undo")
+
+    def __init__(self, cache: "DartKVCache") -> None:
+        self.flags: Optional[torch.Tensor] = None
+        self.tracks = [(len(t), t[-1] if t else None) for t in (cache._keys, cache._values)]
+        self.pools = [(p, p.used) for p in (cache._key_pool, cache._value_pool) if p is not None]
+        self.pending = (cache._pending_key, cache._pending_value)
+        self.undo: list = []
+
+    def restore(self, cache: "DartKVCache") -> None:
+        for fn in reversed(self.undo):
+            fn()
+        cache._keys, cache._values = [self._trimmed(track, *t) for track, t in
+                                      zip((cache._keys, cache._values), self.tracks)]
+        known = [p for p, _ in self.pools]
+        for pool, used in self.pools:
+            pool.used = used
+        for pool in (cache._key_pool, cache._value_pool):  # pools first created by this append
+            if pool is not None and all(pool is not p for p in known):
+                pool.used = 0
+        cache._pending_key, cache._pending_value = self.pending
+        cache._sealed_version += 1
+        if cache._tail_count_dev is not None:
+            cache._tail_count_dev.fill_(cache._pending_tokens())
+
+    @staticmethod
+    def _trimmed(track: list, n: int, last) -> list:
+        kept = track[:max(0, n - 1)]
+        return kept + [last] if n else kept
+
+
 class _DecodePlan:
     """Device table of sealed segment descriptors plus the tensors it points into.
 
@@ -181,7 +218,7 @@ class DartKVCache:
         self._tail_value: Optional[torch.Tensor] = None
         self._tail_count_dev: Optional[torch.Tensor] = None  # held tail length on the device (graph replay)
         self._nonfinite: Optional[torch.Tensor] = None  # int32 [2] flags (keys, values) set by the quantizers
-        self._nonfinite_ptrs: Tuple[int, int] = (0, 0)
+        self._finite_scope: Optional[_FiniteScope] = None
         self._sealed_pairs_cache: Optional[Tuple[int, list]] = None
         self._directory_cache: dict = {}
         self._decode_plan_cache: Optional[_DecodePlan] = None
@@ -236,17 +273,21 @@ class DartKVCache:
             value_states = value_states.contiguous()
         chunk = key_states.shape[-2]
         sink = min(max(0, self.config.sink_tokens - self._seen_tokens), chunk)
-        if sink:
-            self._keys.append(key_states[..., :sink, :].clone())
-            self._values.append(value_states[..., :sink, :].clone())
-            self._sealed_version += 1
-        if sink < chunk:
-            keys, values = key_states[..., sink:, :], value_states[..., sink:, :]
-            if not self._device_tail_append(keys, values):
-                if self._tail_count_dev is not None and torch.cuda.is_current_stream_capturing():
-                    raise RuntimeError("a captured append may only extend the held tail by one token")
-                self._append_tokens(keys, values)
-                self._sync_device_tail()
+        with self._finite_inputs():
+            at_keys, at_values = len(self._keys), len(self._values)
+            if sink < chunk:
+                keys, values = key_states[..., sink:, :], value_states[..., sink:, :]
+                if not self._device_tail_append(keys, values):
+                    if self._tail_count_dev is not None and torch.cuda.is_current_stream_capturing():
+                        raise RuntimeError("a captured append may only extend the held tail by one token")
+                    self._append_tokens(keys, values)
+                    self._sync_device_tail()
+            if sink:
+                # the dense sink tokens precede this append's pages (every earlier token is a sink
+                # token too); they are copied after the quantize launches, which then start sooner
+                self._keys.insert(at_keys, key_states[..., :sink, :].clone())
+                self._values.insert(at_values, value_states[..., :sink, :].clone())
+                self._sealed_version += 1
         self._seen_tokens += chunk
         self._layout_version += 1
         self._invalidate_page_descriptors()
@@ -589,8 +630,15 @@ class DartKVCache:
             return
         self._sealed_version += 1
         if pending:
+            in_tail = self._pending_in_tail()
             keys = torch.cat((self._pending_key, keys), dim=-2)
             values = torch.cat((self._pending_value, values), dim=-2)
+            if in_tail and self._finite_scope is not None:
+                # the new tail overwrites the held tokens in the tail buffers: a failed check puts them back
+                old_k, old_v = keys[..., :pending, :], values[..., :pending, :]
+                tk, tv = self._tail_key, self._tail_value
+                self._finite_scope.undo.append(lambda: (tk[..., :pending, :].copy_(old_k),
+                                                        tv[..., :pending, :].copy_(old_v)))
         if sealable:
             self._seal(keys[..., :sealable, :], values[..., :sealable, :])
         if sealable < total:
@@ -636,33 +684,46 @@ class DartKVCache:
 
     @contextlib.contextmanager
     def _finite_inputs(self):
-        """Quantize launches inside this scope report NaN or infinite inputs through device flags;
-        on exit the flags are read (one host synchronization) and such an input raises the reference's
-        ValueError (quantization.py:159-160, mixed.py:187-188) with the tracks and pools restored."""
-        flags = self._nonfinite
-        if flags is None or flags.device != self._device:
-            flags = self._nonfinite = torch.zeros(2, dtype=torch.int32, device=self._device)
-        else:
-            flags.zero_()
-        keys, values = list(self._keys), list(self._values)
-        pools = [(p, p.used) for p in (self._key_pool, self._value_pool) if p is not None]
-        self._nonfinite_ptrs = (flags.data_ptr(), flags.data_ptr() + 4)
+        """Quantize launches inside this scope report NaN or infinite inputs through device flags
+        (``_flag_ptr``).  The outermost scope (one append) reads them once on exit, after every launch of
+        the append and only when a launch used them (one host synchronization); such an input raises the
+        reference's ValueError (quantization.py:159-160, mixed.py:187-188) with the tracks, pools and
+        held tail as they were.  The flags are zero between appends: only a failure clears them."""
+        if self._finite_scope is not None:
+            yield
+            return
+        scope = self._finite_scope = _FiniteScope(self)
+        ok = False
         try:
             yield
+            ok = True
         finally:
-            self._nonfinite_ptrs = (0, 0)
+            self._finite_scope = None
             self._value_job = None
-        bad_keys, bad_values = flags.tolist()
+            if not ok and scope.flags is not None:
+                scope.flags.zero_()  # launches before the error may have set them
+        if scope.flags is None:
+            return
+        bad_keys, bad_values = scope.flags.tolist()
         if bad_keys or bad_values:
-            self._keys, self._values = keys, values
-            for pool, used in pools:
-                pool.used = used
-            for pool in (self._key_pool, self._value_pool):  # pools first created by this launch
-                if pool is not None and all(pool is not p for p, _ in pools):
-                    pool.used = 0
+            scope.flags.zero_()
+            scope.restore(self)
             if bad_keys and self.config.promote_ratio > 0.0:
                 raise ValueError("key_states must contain finite values")
             raise ValueError("quantize expects all values to be finite")
+
+    def _flag_ptr(self, which: int) -> int:
+        """Device address of the non-finite flag of keys (0) or values (1) for a launch inside the
+        append's scope, which then checks it; 0 (no check) outside a scope."""
+        scope = self._finite_scope
+        if scope is None:
+            return 0
+        if scope.flags is None:
+            flags = self._nonfinite
+            if flags is None or flags.device != self._device:
+                flags = self._nonfinite = torch.zeros(2, dtype=torch.int32, device=self._device)
+            scope.flags = flags
+        return scope.flags.data_ptr() + 4 * which
 
     def _seal(self, keys: torch.Tensor, values: torch.Tensor) -> None:
         """Pack consecutive pages of keys and values; the last may be short (reference cache.py:472-479).
@@ -718,7 +779,7 @@ class DartKVCache:
         pool = self._value_pool_for(values)
         row0 = pool.reserve(T, headroom=max(pool.align, T // 16) if pool.used == 0 else None)
         bits, vg = c.resolved_value_bits, c.resolved_value_group_size
-        job, keep = _value_rows_job(values, bits, vg, c.metadata_dtype, pool, row0, self._nonfinite_ptrs[1])
+        job, keep = _value_rows_job(values, bits, vg, c.metadata_dtype, pool, row0, self._flag_ptr(1))
         if defer:
             self._value_job = (job, keep)
         else:
@@ -775,9 +836,9 @@ class DartKVCache:
         fresh = groups != -(-c.page_size // kg)
         pool = self._key_pool_for(src, groups, fresh)
         slot = pool.reserve(n_pages, headroom=0 if fresh else (max(2, n_pages // 16) if pool.used == 0 else None))
-        t = {name: tensor[slot:slot + n_pages] for name, tensor in pool.tensors.items()}
+        t = pool.tensors  # page-major: the launch writes pages [slot, slot + n_pages)
         values = None if job is None else job[0]
-        flag = self._nonfinite_ptrs[0]
+        flag = self._flag_ptr(0)
         if c.promote_ratio > 0.0:
             K = promoted_count(D, c.promote_ratio)
             selection = {"magnitude": _lib.SELECT_MAGNITUDE, "variance": _lib.SELECT_VARIANCE,
@@ -791,20 +852,20 @@ class DartKVCache:
             if given is not None and n_pages > 1:
                 for p in range(n_pages):
                     launch_key_pages(src[..., p * tokens:(p + 1) * tokens, :], page_tokens=tokens, n_pages=1,
-                                     given_idx=given[p].contiguous(), low=t["low_values"][p],
-                                     high=t["high_values"][p], idx=t["channel_indices"][p], scale=t["scale"][p],
-                                     zero=t["zero_point"][p], values=values if p == n_pages - 1 else None, **common)
+                                     given_idx=given[p].contiguous(), low=t["low_values"], high=t["high_values"],
+                                     idx=t["channel_indices"], scale=t["scale"], zero=t["zero_point"],
+                                     values=values if p == n_pages - 1 else None, slot=slot + p, **common)
             else:
                 launch_key_pages(src, page_tokens=tokens, n_pages=n_pages,
                                  given_idx=None if given is None else given[0].contiguous(), low=t["low_values"],
                                  high=t["high_values"], idx=t["channel_indices"], scale=t["scale"],
-                                 zero=t["zero_point"], values=values, **common)
+                                 zero=t["zero_point"], values=values, slot=slot, **common)
             return [PoolMixedKey(pool, slot + p, tokens, D, groups * kg, kg, c.promote_bits, src.dtype)
                     for p in range(n_pages)]
         bits = c.resolved_key_bits
         launch_key_pages(src, page_tokens=tokens, n_pages=n_pages, key_mode=_lib.KEY_UNIFORM, bits=bits, group=kg,
                          promoted=0, selection=0, given_idx=None, meta=meta, low=t["values"], high=None, idx=None,
-                         scale=t["scale"], zero=t["zero_point"], values=values, nonfinite=flag)
+                         scale=t["scale"], zero=t["zero_point"], values=values, nonfinite=flag, slot=slot)
         packed = pool.shapes["values"][4]
         return [PoolKeys(pool, slot + p, tokens, D, groups * kg, packed * (8 // bits), kg, bits, src.dtype)
                 for p in range(n_pages)]

@@ -217,11 +217,13 @@ def quantize_key_mixed(
 def launch_key_pages(src: torch.Tensor, *, page_tokens: int, n_pages: int, key_mode: int, bits: int, group: int,
                      promoted: int, selection: int, given_idx: Optional[torch.Tensor], meta: torch.dtype,
                      low: torch.Tensor, high: Optional[torch.Tensor], idx: Optional[torch.Tensor],
-                     scale: torch.Tensor, zero: torch.Tensor, values=None, nonfinite: int = 0) -> None:
+                     scale: torch.Tensor, zero: torch.Tensor, values=None, nonfinite: int = 0,
+                     slot: int = 0) -> None:
     """Quantize ``n_pages`` pages of keys from ``src`` [B,H,T,D] into page-major outputs.
 
     Each output tensor has the page index as its leading dim when n_pages > 1
-    (and may omit it when n_pages == 1); page strides are taken from dim 0.
+    (and may omit it when n_pages == 1 and ``slot`` is 0); page strides are
+    taken from dim 0, and the pages written are [slot, slot + n_pages).
     ``values`` (a ``_lib.ValueRowsArgs``) adds the same tokens' value rows to
     the call: the library quantizes them alongside the key path.  ``nonfinite`` is
     the address of a device uint32 the kernels set on a NaN or an infinity (0: no check).
@@ -233,6 +235,11 @@ def launch_key_pages(src: torch.Tensor, *, page_tokens: int, n_pages: int, key_m
             return 0
         return t.stride(0) * t.element_size()
 
+    def page(t: Optional[torch.Tensor]) -> int:
+        if t is None:
+            return 0
+        return t.data_ptr() + (slot * t.stride(0) * t.element_size() if slot else 0)
+
     a = _lib.KeyPagesArgs()
     a.src = src.data_ptr()
     a.src_dtype = _lib.dtype_code(src.dtype)
@@ -243,11 +250,11 @@ def launch_key_pages(src: torch.Tensor, *, page_tokens: int, n_pages: int, key_m
     a.promoted, a.selection = promoted, selection
     a.given_idx = _lib.ptr(given_idx)
     a.meta_dtype = _lib.dtype_code(meta)
-    a.low, a.low_page_stride = low.data_ptr(), page_stride(low)
-    a.high, a.high_page_stride = _lib.ptr(high), page_stride(high)
-    a.idx, a.idx_page_stride = _lib.ptr(idx), page_stride(idx)
-    a.scale, a.scale_page_stride = scale.data_ptr(), page_stride(scale)
-    a.zero, a.zero_page_stride = zero.data_ptr(), page_stride(zero)
+    a.low, a.low_page_stride = page(low), page_stride(low)
+    a.high, a.high_page_stride = page(high), page_stride(high)
+    a.idx, a.idx_page_stride = page(idx), page_stride(idx)
+    a.scale, a.scale_page_stride = page(scale), page_stride(scale)
+    a.zero, a.zero_page_stride = page(zero), page_stride(zero)
     a.values = 0 if values is None else ctypes.addressof(values)
     a.nonfinite = nonfinite or None
     lib = _lib.load()

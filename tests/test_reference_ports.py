@@ -484,14 +484,56 @@ def test_non_finite_page_inputs_raise_like_the_reference(side, bad, promote, hea
     (bad_keys if side == "key" else bad_values)[1, 0, 7, 3] = bad
     msg = "key_states must contain finite values" if (side == "key" and promote > 0) else \
         "quantize expects all values to be finite"
+    held = [t.clone() for t in cache.get()]
     with pytest.raises(ValueError, match=msg):
         cache.update(bad_keys, bad_values)
     assert cache.get_seq_length() == 20
     assert [(s.sequence_start, s.token_count) for s in cache.page_metadata()] == before
+    # the held tail lives in buffers the failed append overwrote: its tokens are back, bit for bit
+    assert all(torch.equal(a, b) for a, b in zip(cache.get(), held))
     cache.update(keys[..., 20:, :], values[..., 20:, :])
     assert cache.get_seq_length() == 40
     k, v = cache.get()
     assert bool(torch.isfinite(k).all()) and bool(torch.isfinite(v).all())
+
+
+@gpu
+@pytest.mark.parametrize("first", [True, False])
+def test_failed_append_leaves_sink_tail_and_device_count_as_they_were(first):
+    """A non-finite token in a page an append seals: the append raises and the cache is as before it,
+    including the dense sink tokens of that append (copied after the quantize launches), the held tail
+    and the device-side tail count; the same cache then takes the finite tokens and ends up bit for
+    bit like a cache that never saw the bad append."""
+    cfg = DartKVCacheConfig(bits=2, page_size=16, key_group_size=16, value_group_size=4, promote_ratio=0.25,
+                            sink_tokens=3, hold_partial_pages=True, metadata_dtype=torch.float16)
+    torch.manual_seed(4)
+    keys = torch.randn(2, 2, 70, 32, device=DEV, dtype=torch.bfloat16)
+    values = torch.randn_like(keys)
+    cache, clean = DartKVCache(cfg), DartKVCache(cfg)
+    start = 0 if first else 25
+    for c in (cache, clean):
+        if start:
+            c.update(keys[..., :start, :], values[..., :start, :])
+    if not first:
+        cache.enable_device_tail()
+        clean.enable_device_tail()
+    before = [t.clone() for t in cache.get()] if start else None
+    bad = keys[..., start:, :].clone()
+    bad[0, 1, 20, 5] = float("nan")
+    with pytest.raises(ValueError, match="finite"):
+        cache.update(bad, values[..., start:, :])
+    assert cache.get_seq_length() == start
+    if first:
+        assert cache.iter_segments() == [] and cache.page_metadata() == []
+    else:
+        assert all(torch.equal(a, b) for a, b in zip(cache.get(), before))
+        assert int(cache.device_tail.item()) == (start - 3) % 16
+    for c in (cache, clean):
+        c.update(keys[..., start:, :], values[..., start:, :])
+    assert cache.get_seq_length() == clean.get_seq_length() == 70
+    assert all(torch.equal(a, b) for a, b in zip(cache.get(), clean.get()))
+    if not first:
+        assert int(cache.device_tail.item()) == int(clean.device_tail.item())
 
 
 @gpu
