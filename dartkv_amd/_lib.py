@@ -26,7 +26,7 @@ KEY_DENSE, KEY_UNIFORM, KEY_MIXED = 0, 1, 2
 VALUE_DENSE, VALUE_UNIFORM = 0, 1
 SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
@@ -97,6 +97,7 @@ class DecodeArgs(ctypes.Structure):
         ("fast_events", ctypes.c_void_p * 2),
         ("tail_tokens_dev", ctypes.c_void_p),
         ("fast_key_bits", ctypes.c_int64), ("fast_value_bits", ctypes.c_int64),
+        ("segments_host", ctypes.c_void_p),
     ]
 
 

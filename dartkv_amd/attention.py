@@ -12,6 +12,7 @@
 
 from __future__ import annotations
 
+import ctypes
 import math
 import os
 from typing import Optional
@@ -139,6 +140,7 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
         a.out_f32 = out_f32.data_ptr()
     a.segments = 0 if plan.table is None else plan.table.data_ptr()
     a.n_segments = plan.count
+    a.segments_host = None if plan.host_table is None else ctypes.addressof(plan.host_table)
     a.tail = tail
     a.B, a.Hq, a.Hkv, a.D = batch, Hq, kv_heads, head_dim
     a.cache_dtype = _lib.dtype_code(cache.dtype)

@@ -188,6 +188,7 @@ class _DecodePlan:
         (self.fast_first, self.fast_count, self.fast_promoted, self.fast_value_group, self.fast_key_bits,
          self.fast_value_bits) = fast
         self.rest_dense = rest_dense
+        self.host_table = None  # the descriptors in host memory (dkv_decode_args.segments_host)
 
 
 class DartKVCache:
@@ -996,6 +997,7 @@ class DartKVCache:
         rest_dense = _rest_dense(self, descs, len(sealed), fast)
         plan = _DecodePlan(self._sealed_version, device, table, len(sealed), keepalive, tail_is_pending, n_tokens,
                            fast, rest_dense)
+        plan.host_table = descs if sealed else None
         self._decode_plan_cache = plan
         return plan
 

@@ -431,7 +431,8 @@ __device__ __forceinline__ void dense_chunk(const DecodeParams& p, int chunks, i
     float* rec =
         wsp + (((int64_t)b * a.Hq + hq) * p.split_stride + p.split_offset + (int64_t)v * chunks + chunk) * (kDenseDim + 2);
     if (lane == 0) {
-      // a segment this kernel cannot read poisons its record (NaN output)
+      // a segment this kernel cannot read (a caller that passed no host copy of
+      // the descriptors to check) poisons its record (NaN output)
       rec[0] = ok ? m[h] : NAN;
       rec[1] = l[h];
     }
@@ -624,6 +625,53 @@ extern "C" int64_t dkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, 
   return B * Hq * n_splits * (D + 2) * (int64_t)sizeof(float);
 }
 
+// The caller's guarantees for the page kernels' run and for the dense rest
+// (declared with dkv_decode_args), checked on the host: against
+// segments_host when the caller passes one, and always for the tail.
+static bool aligned16(uint64_t addr, int64_t bh, int elem_bytes) {
+  return addr % 16 == 0 && (bh * elem_bytes) % 16 == 0;
+}
+
+static bool fast_page_ok(const dkv_decode_args& a, const dkv_segment& g) {
+  if (!(g.tokens == 128 && g.key_group == 128 && g.value_kind == DKV_VALUE_UNIFORM &&
+        g.value_group == a.fast_value_group))
+    return false;
+  if (a.fast_promoted > 0) {
+    if (!(g.key_kind == DKV_KEY_MIXED && g.promoted == a.fast_promoted && g.value_bits == 2)) return false;
+    if (!(aligned16(g.key[1], g.key_bh[1], 1) && aligned16(g.key[2], g.key_bh[2], 4))) return false;
+  } else if (!(g.key_kind == DKV_KEY_UNIFORM && g.key_bits == a.fast_key_bits && g.value_bits == a.fast_value_bits)) {
+    return false;
+  }
+  return aligned16(g.key[0], g.key_bh[0], 1) && aligned16(g.key[3], g.key_bh[3], 2) &&
+         aligned16(g.key[4], g.key_bh[4], 2) && aligned16(g.value[0], g.value_bh[0], 1) &&
+         aligned16(g.value[1], g.value_bh[1], 2) && aligned16(g.value[2], g.value_bh[2], 2);
+}
+
+static bool dense_rest_ok(const dkv_decode_args& a, const dkv_segment& g) {
+  return g.key_kind == DKV_KEY_DENSE && g.value_kind == DKV_VALUE_DENSE && g.tokens <= a.rest_dense_tokens &&
+         aligned16(g.key[0], g.key_bh[0], 2) && aligned16(g.value[0], g.value_bh[0], 2);
+}
+
+static int check_segments(const dkv_decode_args& a, int64_t fast_count, bool dense_rest) {
+  if (dense_rest && a.tail.tokens > 0)
+    DKV_CHECK(dense_rest_ok(a, a.tail), DKV_ERR_INVALID,
+              "rest_dense_tokens: the tail must be a dense bf16/fp16 segment of at most %lld tokens with 16-byte "
+              "aligned rows", (long long)a.rest_dense_tokens);
+  if (a.segments_host == nullptr) return DKV_OK;
+  for (int64_t i = 0; i < a.n_segments; ++i) {
+    const dkv_segment& g = a.segments_host[i];
+    if (fast_count > 0 && i >= a.fast_first && i < a.fast_first + fast_count) {
+      DKV_CHECK(fast_page_ok(a, g), DKV_ERR_INVALID, "descriptor %lld is not a page the fast page kernel reads",
+                (long long)i);
+    } else if (dense_rest) {
+      DKV_CHECK(dense_rest_ok(a, g), DKV_ERR_INVALID,
+                "rest_dense_tokens: descriptor %lld is not a dense segment of at most %lld tokens with 16-byte "
+                "aligned rows", (long long)i, (long long)a.rest_dense_tokens);
+    }
+  }
+  return DKV_OK;
+}
+
 extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
   DKV_CHECK(args != nullptr, DKV_ERR_INVALID, "args is NULL");
   const dkv_decode_args& a = *args;
@@ -673,6 +721,10 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
   DKV_CHECK(stride <= 8192, DKV_ERR_UNSUPPORTED, "too many splits");
   DKV_CHECK(a.workspace_bytes >= dkv_decode_workspace_bytes(a.B, a.Hq, a.D, stride), DKV_ERR_INVALID,
             "workspace too small");
+  {
+    const int rc = check_segments(a, fast_count, rest > 0 && a.rest_dense_tokens > 0);
+    if (rc != DKV_OK) return rc;
+  }
   hipStream_t s = (hipStream_t)stream;
   if (fast_count > 0) {
     int rc = record_event(a.fast_events[0], s);

@@ -287,6 +287,7 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) O[j] = float4v{0.f, 0.f, 0.f, 0.f};
 
+  int qexp;  // the query's power-of-two scale (query_exponent)
   {
     uint16_t* q16 = (uint16_t*)(lds + M.q16);
     float qv[4 * kD / 64];
@@ -294,8 +295,10 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
       const int i = lane + 64 * r, h = i / kD, c = i % kD;
       return h < GQ ? (int64_t)b * p.q_sb + (int64_t)(kvh * GQ + h) * p.q_sh + c : -1;
     });
+    qexp = query_exponent(qv);
 #pragma unroll
-    for (int r = 0; r < 4 * kD / 64; ++r) q16[lane + 64 * r] = __builtin_bit_cast(uint16_t, (_Float16)qv[r]);
+    for (int r = 0; r < 4 * kD / 64; ++r)
+      q16[lane + 64 * r] = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(qv[r], -qexp));
     *(uint32_t*)(lds + M.zero + 4 * lane) = 0u;
   }
   lds_sync();
@@ -317,7 +320,7 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     issue_keys(M, lds, a0, np, lane);
     issue_values(M, lds, a0, lane);
   }
-  const float c2 = p.scale * kLog2e;
+  const float c2 = ldexpf(p.scale * kLog2e, qexp);
   const uint32_t m3 = in_sgpr(0x03030303u);
   const uint32_t sel2 = in_vgpr(0x04000400u);
   // LDS address of the 4-bit tables; its low byte is zero (the map and every

@@ -190,6 +190,7 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
   }
   O[0] = O[1] = float4v{0.f, 0.f, 0.f, 0.f};
 
+  int qexp;  // the query's power-of-two scale (query_exponent)
   {
     uint16_t* q16 = (uint16_t*)(lds + M.q16);
     float qv[4 * kD / 64];
@@ -197,8 +198,10 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
       const int i = lane + 64 * r, h = i / kD, c = i % kD;
       return h < GQ ? (int64_t)b * p.q_sb + (int64_t)(kvh * GQ + h) * p.q_sh + c : -1;
     });
+    qexp = query_exponent(qv);
 #pragma unroll
-    for (int r = 0; r < 4 * kD / 64; ++r) q16[lane + 64 * r] = __builtin_bit_cast(uint16_t, (_Float16)qv[r]);
+    for (int r = 0; r < 4 * kD / 64; ++r)
+      q16[lane + 64 * r] = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(qv[r], -qexp));
     *(uint32_t*)(lds + M.zero + 4 * lane) = 0u;
   }
   lds_sync();
@@ -217,7 +220,7 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
     issue_keys_u(M, lds, a0, KB, hp0 & 1, lane);
     issue_values_u(M, lds, a0, VB, gv, hp0 & 1, lane);
   }
-  const float c2 = p.scale * kLog2e;
+  const float c2 = ldexpf(p.scale * kLog2e, qexp);
   const uint32_t kmask = code_mask<KB>(), vmask = code_mask<VB>();
 
 #pragma unroll 1

@@ -195,5 +195,20 @@ __device__ __forceinline__ float uniform(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
+// Power-of-two exponent e that brings the largest |q| of the wave's query
+// elements (N per lane) into [2^14, 2^15): fp16 then holds q * 2^-e at full
+// precision, and the logit scale takes 2^e back exactly.  Zero for an all-zero
+// query or one whose largest element is infinite (NaN elements are ignored
+// here and propagate through the products).
+template <int N>
+__device__ __forceinline__ int query_exponent(const float (&qv)[N]) {
+  float amax = 0.f;
+#pragma unroll
+  for (int r = 0; r < N; ++r) amax = fmaxf(amax, fabsf(qv[r]));
+  amax = uniform(wave_max64(amax));
+  if (!(amax > 0.f) || amax == INFINITY) return 0;
+  return __builtin_amdgcn_readfirstlane(ilogbf(amax) - 14);
+}
+
 
 }  // namespace

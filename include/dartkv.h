@@ -47,7 +47,7 @@ extern "C" {
 /* Thread-local description of the last error on this thread. */
 const char* dkv_last_error(void);
 
-/* ABI version (10); bumps when a struct or an entry point below changes. */
+/* ABI version (11); bumps when a struct or an entry point below changes. */
 int dkv_abi_version(void);
 
 /*
@@ -252,7 +252,20 @@ typedef struct dkv_segment {
  * (bf16 or fp16) with 16-byte aligned rows and at most rest_dense_tokens
  * tokens each; then one wave per 32-token chunk handles them (head_dim 128, at
  * most 8 query heads per KV head, n_splits = number of those segments *
- * ceil(rest_dense_tokens / 32)).  A segment that breaks this yields NaN.
+ * ceil(rest_dense_tokens / 32)).
+ *
+ * Checked guarantees: when segments_host is not NULL it holds the same
+ * n_segments descriptors in host memory, and every entry of the fast range and,
+ * with rest_dense_tokens > 0, every other entry is checked against the rules
+ * above (DKV_ERR_INVALID naming the entry); the tail is always checked.
+ * Without a host copy the caller guarantees them, and a non-page segment the
+ * dense kernel cannot read makes the result NaN instead of wrong.
+ *
+ * Query range: the page kernels compute with fp16 operands; each split scales
+ * its query heads by a power of two that brings the largest |q| into
+ * [2^14, 2^15) and takes the inverse power into the logit scale (exact), so any
+ * finite query works, and queries in fp16's normal range give the same bits as
+ * without the scaling.
  *
  * Timing: fast_events[0] / [1], when not NULL, are hipEvent_t handles recorded
  * on `stream` right before and right after the page kernel's launch.
@@ -287,6 +300,7 @@ typedef struct dkv_decode_args {
   void* fast_events[2];
   const int64_t* tail_tokens_dev;
   int64_t fast_key_bits, fast_value_bits;
+  const dkv_segment* segments_host;
 } dkv_decode_args;
 
 /*

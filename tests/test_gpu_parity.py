@@ -368,3 +368,62 @@ def test_uniform_page_kernel_split_counts_agree():
     for o in outs:
         assert rel_err(o.unsqueeze(2), ref32) <= 2e-3
         assert rel_err(o.unsqueeze(2), outs[0].unsqueeze(2)) <= 1e-3
+
+
+@pytest.mark.parametrize("kind", ["dart", "uniform"])
+@pytest.mark.parametrize("factor", [3.0e4, 1.0e-6])
+def test_page_kernels_take_queries_outside_fp16_range(kind, factor):
+    """The page kernels round the query to fp16; each split first scales its query heads by a power of
+    two (largest |q| into [2^14, 2^15)) and takes the inverse power into the logit scale.  A bf16 query
+    with elements far above fp16's largest value (65504), or far below its normal range, then matches
+    the oracle like any other; before, the first overflowed to inf (NaN output)."""
+    from dartkv_amd import synthetic
+    from oracle import dart_oracle as O
+    dart = _dkv()
+    cfg = dict(bits=2, page_size=128, key_group_size=128, value_group_size=64, promote_ratio=0.25, sink_tokens=32,
+               hold_partial_pages=True, metadata_dtype=torch.float16)
+    if kind == "uniform":
+        cfg.update(promote_ratio=0.0, key_bits=4, value_bits=4)
+    k, v, q = synthetic.outlier_kv(2, 2, 900, 128, query_heads=8, dtype=torch.bfloat16, seed=21)
+    q = (q.float() * factor).to(torch.bfloat16)
+    if factor > 1:
+        assert float(q.float().abs().max()) > 65504.0
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    oc.append(k, v)
+    _, ref32 = O.streamed_attention(q, oc, return_fp32=True)
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    cache.append(k.to(DEV), v.to(DEV))
+    q = q.to(DEV)
+    plan = cache.decode_plan(q.device)
+    assert plan.fast_count == (900 - 32) // 128
+    out = torch.empty(2, 8, 128, dtype=torch.float32, device=DEV)
+    dart.decode_attention(q, cache, out_f32=out, fast=True)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    err = rel_err(out.unsqueeze(2), ref32)
+    print("case", kind, factor, "rel err", err, flush=True)
+    assert err <= 2e-3
+
+
+def test_decode_checks_the_page_and_dense_contracts_against_the_host_descriptors():
+    """dkv_decode_attention checks what it is told about the descriptor table against the host copy the
+    caller passes (segments_host): a fast page range that starts on the dense sink, or a dense rest that
+    holds a packed page, is an error naming the entry, not NaN or a fault."""
+    dart = _dkv()
+    cache, q, ref32 = _oracle_and_cache(1, 2, 8, 700, torch.bfloat16, seed=5)
+    plan = cache.decode_plan(q.device)
+    assert plan.fast_first == 1 and plan.fast_count == (700 - 32) // 128 and plan.rest_dense >= 0
+    first, count = plan.fast_first, plan.fast_count
+    try:
+        plan.fast_first = 0  # entry 0 is the dense sink
+        with pytest.raises(ValueError, match="descriptor 0 is not a page the fast page kernel reads"):
+            dart.decode_attention(q, cache, fast=True)
+        plan.fast_first, plan.fast_count = first, count - 1  # the last page falls to the dense kernel
+        with pytest.raises(ValueError, match=f"descriptor {first + count - 1} is not a dense segment"):
+            dart.decode_attention(q, cache, fast=True)
+    finally:
+        plan.fast_first, plan.fast_count = first, count
+    out = torch.empty(1, 8, 128, dtype=torch.float32, device=DEV)
+    dart.decode_attention(q, cache, out_f32=out, fast=True)
+    torch.cuda.synchronize()
+    assert rel_err(out.unsqueeze(2), ref32) <= 2e-3
