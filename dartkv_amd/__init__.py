@@ -13,6 +13,7 @@ from .mixed import MixedQuantizedKey, quantize_key_mixed, select_key_channels
 from .page_table import DENSE_PAGE, MIXED_PAGE, QUANTIZED_PAGE, DartPageRun, DartPageTable
 from .quantization import QuantizedTensor, dequantize, quantize, quantize_axis
 from .triton_ops import TRITON_AVAILABLE, triton_available, triton_dequantize
+from . import torch_ops  # registers torch.ops.dartkv.*
 
 __all__ = [
     "DartKVCache",
