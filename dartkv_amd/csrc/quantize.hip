@@ -145,7 +145,30 @@ __device__ __forceinline__ float rows_group_scale(float mn, float mx, float qmax
 // template argument, so the per-element chain (subtract, round, divide,
 // round, rint, clamp) has no branches; the division is one reciprocal per
 // group and three operations per element.  Workgroup (bx, by) of a gx x gy
-// grid: y strides over row blocks, x over the lanes of one block.
+// grid: y strides over row blocks, x over the lanes of one block, kRowChunks
+// chunks of kThreads lanes per step: a lane issues the loads of all its chunks
+// before it computes (one chunk per lane left each wave with one 16-byte load
+// in flight per lane, and the kernel waiting on memory latency).
+constexpr int kRowChunks = 2;
+
+template <int SRC>
+__device__ __forceinline__ void load_row_chunk(const RowsParams& p, int64_t src_row, int64_t i0, float (&x)[8]) {
+  if (SRC == kF32) {
+    const float4* src = (const float4*)((const float*)p.src + src_row + i0);
+    const float4 a = src[0], b = src[1];
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  } else {
+    const uint4 w = *(const uint4*)((const uint16_t*)p.src + src_row + i0);
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint16_t bits = (uint16_t)(ww[j / 2] >> (16 * (j % 2)));
+      x[j] = SRC == kBF16 ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
+    }
+  }
+}
+
 template <int BITS, int SRC>
 __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per_group, int row_shift, int64_t bx,
                                               int64_t by, int64_t gx, int64_t gy) {
@@ -156,66 +179,66 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
   constexpr float inv_qmax = 1.0f / (float)((1 << BITS) - 1);  // RN(1 / qmax), folded at compile time
   const int group_shift = __builtin_ctz((unsigned)lanes_per_group);
   const int lane = threadIdx.x & 63;
+  constexpr int64_t kStep = (int64_t)kThreads * kRowChunks;
   for (int64_t blk = by; blk < p.blocks; blk += gy)
-  for (int64_t v = bx * kThreads + threadIdx.x; v - lane < total; v += gx * kThreads) {
+  for (int64_t v0 = bx * kStep + threadIdx.x; v0 - lane < total; v0 += gx * kStep) {
     // whole waves stay in the loop so the shuffles see every lane of a group
-    const bool active = v < total;
-    int64_t r = 0;  // row within the block
-    int li = 0;     // lane item within the row: elements 8 li .. 8 li + 7
-    if (active) {
-      r = row_shift >= 0 ? v >> row_shift : v / lanes_per_row;
-      li = (int)(v - r * lanes_per_row);
-    }
-    const int64_t i0 = 8 * li;
-    const int64_t src_row = blk * p.block_stride + r * p.row_stride;
-    float x[8];
-    if (SRC == kF32) {
-      const float4* src = (const float4*)((const float*)p.src + src_row + i0);
-      const float4 a = src[0], b = src[1];
-      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-      x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-    } else {
-      const uint4 w = *(const uint4*)((const uint16_t*)p.src + src_row + i0);
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    int64_t r[kRowChunks];   // row within the block
+    int li[kRowChunks];      // lane item within the row: elements 8 li .. 8 li + 7
+    float x[kRowChunks][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint16_t bits = (uint16_t)(ww[j / 2] >> (16 * (j % 2)));
-        x[j] = SRC == kBF16 ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
+    for (int u = 0; u < kRowChunks; ++u) {
+      const int64_t v = v0 + u * kThreads;
+      r[u] = 0;
+      li[u] = 0;
+      if (v < total) {
+        r[u] = row_shift >= 0 ? v >> row_shift : v / lanes_per_row;
+        li[u] = (int)(v - r[u] * lanes_per_row);
+        load_row_chunk<SRC>(p, blk * p.block_stride + r[u] * p.row_stride, 8 * (int64_t)li[u], x[u]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[u][j] = 0.f;
       }
     }
-    float mn = x[0], mx = x[0];
 #pragma unroll
-    for (int j = 1; j < 8; ++j) {
-      mn = nmin(mn, x[j]);
-      mx = nmax(mx, x[j]);
-    }
-    for (int off = 1; off < lanes_per_group; off <<= 1) {
-      mn = nmin(mn, __shfl_xor(mn, off, 64));
-      mx = nmax(mx, __shfl_xor(mx, off, 64));
-    }
-    if (!active) continue;
-    r += blk * p.out_block_rows + p.out_row0;  // output row
-    const float s = rows_group_scale<SRC>(mn, mx, qmax, inv_qmax);
-    const float y = __fdiv_rn(1.0f, s);
-    if ((li & (lanes_per_group - 1)) == 0) {  // the group's first lane (groups are power-of-two lanes)
-      const int64_t g = li >> group_shift;
-      dev_store_meta(p.scale, r * p.groups + g, s, p.meta_dtype);
-      dev_store_meta(p.zero, r * p.groups + g, mn, p.meta_dtype);
-      flag_nonfinite(p.nonfinite, mn, mx);
-    }
-    uint32_t packed[2] = {0u, 0u};  // codes 0..3 and 4..7 for 8-bit, else all in [0]
+    for (int u = 0; u < kRowChunks; ++u) {
+      const int64_t v = v0 + u * kThreads;
+      if (v - lane >= total) break;  // the whole wave is past the block
+      const bool active = v < total;
+      float mn = x[u][0], mx = x[u][0];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float diff = src_round<SRC>(x[j] - mn);
-      const float q = __builtin_rintf(src_round<SRC>(div_rn(diff, s, y)));
-      const uint32_t code = (uint32_t)fminf(fmaxf(q, 0.0f), qmax);
-      if (BITS == 8) packed[j / 4] |= code << (8 * (j % 4));
-      else packed[0] |= code << (j * BITS);
+      for (int j = 1; j < 8; ++j) {
+        mn = nmin(mn, x[u][j]);
+        mx = nmax(mx, x[u][j]);
+      }
+      for (int off = 1; off < lanes_per_group; off <<= 1) {
+        mn = nmin(mn, __shfl_xor(mn, off, 64));
+        mx = nmax(mx, __shfl_xor(mx, off, 64));
+      }
+      if (!active) continue;
+      const int64_t ro = r[u] + blk * p.out_block_rows + p.out_row0;  // output row
+      const float s = rows_group_scale<SRC>(mn, mx, qmax, inv_qmax);
+      const float y = __fdiv_rn(1.0f, s);
+      if ((li[u] & (lanes_per_group - 1)) == 0) {  // the group's first lane (groups are power-of-two lanes)
+        const int64_t g = li[u] >> group_shift;
+        dev_store_meta(p.scale, ro * p.groups + g, s, p.meta_dtype);
+        dev_store_meta(p.zero, ro * p.groups + g, mn, p.meta_dtype);
+        flag_nonfinite(p.nonfinite, mn, mx);
+      }
+      uint32_t packed[2] = {0u, 0u};  // codes 0..3 and 4..7 for 8-bit, else all in [0]
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float diff = src_round<SRC>(x[u][j] - mn);
+        const float q = __builtin_rintf(src_round<SRC>(div_rn(diff, s, y)));
+        const uint32_t code = (uint32_t)fminf(fmaxf(q, 0.0f), qmax);
+        if (BITS == 8) packed[j / 4] |= code << (8 * (j % 4));
+        else packed[0] |= code << (j * BITS);
+      }
+      uint8_t* out = p.values + ro * p.packed_bytes + (int64_t)li[u] * BITS;
+      if (BITS == 2) *(uint16_t*)out = (uint16_t)packed[0];
+      else if (BITS == 4) *(uint32_t*)out = packed[0];
+      else *(uint2*)out = make_uint2(packed[0], packed[1]);
     }
-    uint8_t* out = p.values + r * p.packed_bytes + i0 * BITS / 8;
-    if (BITS == 2) *(uint16_t*)out = (uint16_t)packed[0];
-    else if (BITS == 4) *(uint32_t*)out = packed[0];
-    else *(uint2*)out = make_uint2(packed[0], packed[1]);
   }
 }
 
@@ -1158,7 +1181,8 @@ static int prepare_rows(const void* src, int src_dtype, int64_t blocks, int64_t 
   // over both, so the grid is capped at about 2^20 workgroups)
   const int64_t lanes = block_rows * (n / 8);
   L.gy = std::max<int64_t>(std::min<int64_t>(blocks, 65535), 1);
-  L.gx = std::max<int64_t>(std::min<int64_t>((lanes + kThreads - 1) / kThreads, (1 << 20) / L.gy), 1);
+  L.gx = std::max<int64_t>(
+      std::min<int64_t>((lanes + kThreads * kRowChunks - 1) / (kThreads * kRowChunks), (1 << 20) / L.gy), 1);
   return DKV_OK;
 }
 
