@@ -188,8 +188,16 @@ def require_device(*tensors: torch.Tensor) -> None:
                 "Move the tensors to the GPU (there is no CPU fallback).")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current HIP stream of ``device`` (what torch.cuda.current_stream(device).cuda_stream gives,
+    read without building a Stream object)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
 
 
 def ptr(t: Optional[torch.Tensor]) -> int:

@@ -23,6 +23,7 @@ boundaries.  How it is stored is this build's own:
 from __future__ import annotations
 
 import contextlib
+import threading
 from dataclasses import dataclass
 from itertools import accumulate
 from typing import TYPE_CHECKING, List, Optional, Tuple, Union
@@ -128,6 +129,22 @@ class DartKVCacheConfig:
         return self.value_group_size if self.value_group_size is not None else self.group_size
 
 
+_flag_store = threading.local()
+
+
+def _nonfinite_flags(device: torch.device) -> torch.Tensor:
+    """int32 [2] device flags (keys, values) for the quantizers' non-finite reports, one pair per thread
+    and device and shared by that thread's caches (an append's scope reads them before the next append
+    can start on the thread).  They are zero between appends."""
+    flags = getattr(_flag_store, "flags", None)
+    if flags is None:
+        flags = _flag_store.flags = {}
+    t = flags.get(device)
+    if t is None:
+        t = flags[device] = torch.zeros(2, dtype=torch.int32, device=device)
+    return t
+
+
 class _FiniteScope:
     """Bookkeeping of one append's non-finite check: the flags once a quantize launch uses them, and
     what a failed check restores.  Within an append the tracks only grow, or change their last
@@ -218,7 +235,6 @@ class DartKVCache:
         self._tail_key: Optional[torch.Tensor] = None
         self._tail_value: Optional[torch.Tensor] = None
         self._tail_count_dev: Optional[torch.Tensor] = None  # held tail length on the device (graph replay)
-        self._nonfinite: Optional[torch.Tensor] = None  # int32 [2] flags (keys, values) set by the quantizers
         self._finite_scope: Optional[_FiniteScope] = None
         self._sealed_pairs_cache: Optional[Tuple[int, list]] = None
         self._directory_cache: dict = {}
@@ -264,6 +280,8 @@ class DartKVCache:
 
     def append(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         """Append a chunk without materializing the cache (reference cache.py:168-190)."""
+        if self._extend_tail(key_states, value_states):
+            return
         _lib.require_device(key_states, value_states)
         self._validate_inputs(key_states, value_states)
         key_states = key_states.detach()
@@ -475,7 +493,6 @@ class DartKVCache:
             self._pending_value = self._pending_value.to(target)
         self._tail_key = self._tail_value = None
         self._tail_count_dev = None
-        self._nonfinite = None
         self._device = target
         self._layout_version += 1
         self._sealed_version += 1
@@ -595,6 +612,42 @@ class DartKVCache:
         self._tail_value[..., :n, :].copy_(values)
         self._pending_key = self._tail_key[..., :n, :]
         self._pending_value = self._tail_value[..., :n, :]
+
+    def _extend_tail(self, key_states: torch.Tensor, value_states: torch.Tensor) -> bool:
+        """The decode-step append in few host steps: tokens that only extend the held tail in its
+        buffers (no page sealed, no sink token, the cache's shape, dtype and device).  Same result as the
+        general path; False (nothing done) whenever any of that does not hold, and the general path then
+        runs, with its checks and messages."""
+        tk = self._tail_key
+        if tk is None or self._tail_count_dev is not None or self.config.value_local_tokens:
+            return False
+        ks = key_states.shape
+        if (len(ks) != 4 or ks != value_states.shape or key_states.dtype is not self._dtype
+                or value_states.dtype is not self._dtype or key_states.device != self._device
+                or value_states.device != self._device or (ks[0], ks[1], ks[3]) != self._shape
+                or key_states.stride(-1) != 1 or value_states.stride(-1) != 1):
+            return False
+        c = self.config
+        n = ks[2]
+        # a tail that already holds tokens: the sealed structure and the decode plan built for it (which
+        # reads the tail per call) stay valid; starting a tail is left to the general path, which
+        # invalidates them
+        if self._pending_key is None or not self._pending_in_tail():
+            return False
+        pending = self._pending_key.shape[2]
+        total = pending + n
+        if (n == 0 or self._seen_tokens < c.sink_tokens or not (c.hold_partial_pages or c.local_tokens)
+                or total > tk.shape[2] or (total - c.local_tokens) >= c.page_size):
+            return False
+        tv = self._tail_value
+        torch._foreach_copy_((tk.narrow(2, pending, n), tv.narrow(2, pending, n)),
+                             (key_states.detach(), value_states.detach()))
+        self._pending_key = tk.narrow(2, 0, total)
+        self._pending_value = tv.narrow(2, 0, total)
+        self._seen_tokens += n
+        self._layout_version += 1
+        self._invalidate_page_descriptors()
+        return True
 
     def _pending_in_tail(self) -> bool:
         pk, tk = self._pending_key, self._tail_key
@@ -720,10 +773,7 @@ class DartKVCache:
         if scope is None:
             return 0
         if scope.flags is None:
-            flags = self._nonfinite
-            if flags is None or flags.device != self._device:
-                flags = self._nonfinite = torch.zeros(2, dtype=torch.int32, device=self._device)
-            scope.flags = flags
+            scope.flags = _nonfinite_flags(self._device)
         return scope.flags.data_ptr() + 4 * which
 
     def _seal(self, keys: torch.Tensor, values: torch.Tensor) -> None:

@@ -174,3 +174,30 @@ def test_shapes_beyond_the_decode_kernels_fall_back_to_segment_attention(Hkv, Hq
     assert bits_equal(fused.cpu(), streamed.cpu())
     with pytest.raises(ValueError, match="query heads per KV head"):
         dart.fused_dart_attention(q.to(DEV), cache, fallback=False)
+
+
+@pytest.mark.parametrize("start", [96, 100])
+def test_one_token_appends_reach_decode_after_a_decode_at_any_tail_length(start):
+    """Decode after each of several one-token appends, starting with an empty held tail (the prompt ends on
+    a page boundary) or a partial one: the decode plan built for the sealed pages reads the tail per call,
+    so every new token is attended (oracle on the same inputs, fp32 pre-cast output)."""
+    import dartkv_amd as dart
+    from dartkv_amd import synthetic
+    from oracle import dart_oracle as O
+    cfg = dict(bits=2, page_size=32, key_group_size=32, value_group_size=32, promote_ratio=0.25, sink_tokens=0,
+               hold_partial_pages=True, metadata_dtype=torch.float16)
+    k, v, q = synthetic.outlier_kv(2, 2, start + 6, 128, query_heads=8, dtype=torch.bfloat16, seed=start)
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    cache.append(k[:, :, :start].to(DEV), v[:, :, :start].to(DEV))
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    oc.append(k[:, :, :start], v[:, :, :start])
+    for t in range(start, start + 6):
+        out = torch.empty(2, 8, 128, dtype=torch.float32, device=DEV)
+        dart.decode_attention(q.to(DEV), cache, out_f32=out)
+        _, ref = O.streamed_attention(q, oc, return_fp32=True)
+        a, b = out.cpu(), ref.reshape(2, 8, 128)
+        err = float(((a - b).abs().amax(-1) / b.abs().amax(-1)).max())
+        assert err <= 2e-3, (t, err)
+        cache.append(k[:, :, t:t + 1].to(DEV), v[:, :, t:t + 1].to(DEV))
+        oc.append(k[:, :, t:t + 1], v[:, :, t:t + 1])
+    assert cache.get_seq_length() == start + 6
