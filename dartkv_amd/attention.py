@@ -71,6 +71,22 @@ def _fast_enabled() -> bool:
     return os.environ.get("DKV_FORCE_GENERAL", "0") in ("", "0")
 
 
+_workspaces: dict = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A decode workspace for the split records: one per device and stream, kept and grown as needed (calls
+    on one stream run in order, so they can share it).  Under graph capture a fresh one, which the graph
+    keeps."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    key = (device.index, _lib.stream_ptr(device))
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = _workspaces[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return ws
+
+
 def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,
                      n_splits: Optional[int] = None, out_f32: Optional[torch.Tensor] = None,
                      fast: Optional[bool] = None, fast_events=None, out: Optional[torch.Tensor] = None,
@@ -127,7 +143,7 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
         raise ValueError("out must be a [B, Hq, 1, D] tensor of the query's dtype and device, unit stride in D")
     lib = _lib.load()
     ws_bytes = lib.dkv_decode_workspace_bytes(batch, Hq, head_dim, splits + fast_splits)
-    workspace = None if static_scratch else torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+    workspace = None if static_scratch else _workspace(query.device, ws_bytes)
     a = _lib.DecodeArgs()
     a.query = q3.data_ptr()
     a.q_dtype = _lib.dtype_code(q3.dtype)

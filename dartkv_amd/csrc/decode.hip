@@ -19,6 +19,7 @@
 
 #include "dkv_capi_util.h"
 #include "dkv_decode.h"
+#include "dkv_dense.h"
 #include "dkv_device.h"
 
 using namespace dkv;
@@ -29,32 +30,6 @@ constexpr int kThreads = 256;
 constexpr int kMaxGroup = 16;   // query heads per KV head
 constexpr int kMaxDim = 512;    // head_dim
 constexpr int kChanPerThread = kMaxDim / kThreads;
-
-struct DecodeParams {
-  dkv_decode_args a;
-  int group;        // query heads per KV head
-  int n_total;      // segments this kernel walks, including the tail
-  int splits;       // splits of this kernel
-  int split_offset; // first workspace split slot this kernel writes
-  int split_stride; // split slots per (batch, query head) record
-  int skip_first;   // descriptor entries [skip_first, skip_first + skip_count)
-  int skip_count;   // belong to the fast page kernel
-};
-
-// Segment v of the general kernel's sequence: descriptor entries outside the
-// fast range, then the tail.
-__device__ __forceinline__ dkv_segment general_segment(const DecodeParams& p, int v) {
-  const int rest = (int)p.a.n_segments - p.skip_count;
-  if (v >= rest) {
-    dkv_segment t = p.a.tail;
-    if (p.a.tail_tokens_dev != nullptr) {
-      const int64_t n = *p.a.tail_tokens_dev;
-      t.tokens = (int32_t)(n < 0 ? 0 : (n < t.tokens ? n : t.tokens));
-    }
-    return t;
-  }
-  return p.a.segments[v < p.skip_first ? v : v + p.skip_count];
-}
 
 __device__ __forceinline__ float key_value(const dkv_segment& s, int64_t bh, int c, int t, int D, const int32_t* inv,
                                            int cache_dt, int meta) {
@@ -281,166 +256,6 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
 // 128 x MG query reads first and kept them in registers (one wave per SIMD).
 // The wave
 // writes one record at split slot split_offset + segment * chunks + chunk.
-constexpr int kDenseWaves = 4;
-constexpr int kDenseChunk = 32;
-constexpr int kDenseDim = 128;
-constexpr int kDenseMaxGroup = 8;
-
-// Every head slot of the dense kernel computes (the query of slots >= G is
-// zero), so the unrolled loops carry no per-head branches; only the record
-// writes are guarded.
-#define DKV_ALL_HEADS(h) _Pragma("unroll") for (int h = 0; h < MG; ++h)
-
-template <bool BF>
-__device__ __forceinline__ float dense_elem(uint16_t bits) {
-  return BF ? bf16_to_f32(bits) : (float)__builtin_bit_cast(_Float16, bits);
-}
-
-// An offset the compiler must treat as computed from every dep[h]: reads
-// addressed with it cannot be issued before all of them are.  (Depending on
-// one head only let the compiler finish that head's chain first and keep the
-// other heads' query values live across all steps.)
-template <int MG>
-__device__ __forceinline__ int after(int offset, const float (&dep)[MG]) {
-#pragma unroll
-  for (int h = 0; h < MG; ++h) asm volatile("" : "+v"(offset) : "v"(dep[h]));
-  return offset;
-}
-
-// MG consecutive floats from LDS (one read for MG = 2, 4; two for 8)
-template <int MG>
-__device__ __forceinline__ void lds_heads(const float* src, float (&x)[MG]) {
-  if (MG == 1) {
-    x[0] = src[0];
-  } else if (MG == 2) {
-    const float2 v = *(const float2*)src;
-    x[0] = v.x; x[1 % MG] = v.y;
-  } else {
-#pragma unroll
-    for (int j = 0; j < MG; j += 4) {
-      const float4 v = *(const float4*)(src + j);
-      x[j] = v.x; x[(j + 1) % MG] = v.y; x[(j + 2) % MG] = v.z; x[(j + 3) % MG] = v.w;
-    }
-  }
-}
-
-// Chunk `chunk` of rest segment v of (batch, kv head) bhi, by one wave; qs
-// and ws are the wave's LDS (kDenseDim * MG and kDenseChunk * MG floats).
-template <int MG, bool BF>
-__device__ __forceinline__ void dense_chunk(const DecodeParams& p, int chunks, int bhi, int v, int chunk, int lane,
-                                            float* qs, float* ws) {
-  const dkv_decode_args& a = p.a;
-  const int b = bhi / (int)a.Hkv, kvh = bhi % (int)a.Hkv;
-  const int64_t bh = (int64_t)bhi;
-  const int G = p.group;
-
-  const dkv_segment seg = general_segment(p, v);
-  const bool ok = seg.key_kind == DKV_KEY_DENSE && seg.value_kind == DKV_VALUE_DENSE &&
-                  seg.tokens <= chunks * kDenseChunk;
-  const int t0 = chunk * kDenseChunk;
-  const int nt = ok ? max(0, min(kDenseChunk, seg.tokens - t0)) : 0;
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(1))) const u32x4 gu4;
-  typedef __attribute__((address_space(1))) const uint32_t gu32;
-  const uint16_t* kbase = (const uint16_t*)(seg.key[0] + 2 * (uint64_t)(bh * seg.key_bh[0]));
-  const uint16_t* vbase = (const uint16_t*)(seg.value[0] + 2 * (uint64_t)(bh * seg.value_bh[0]));
-  const int kt = lane & (kDenseChunk - 1), khalf = lane >> 5;  // token, channel half of the Q K lane
-  const int last = nt > 0 ? nt - 1 : 0;
-
-  // K rows (8 x 16 B per lane) and V pairs (one dword per token), issued
-  // before the query so one wait covers them; the query goes to LDS as fp32
-  u32x4 krow[8];
-  uint32_t vpair[kDenseChunk];
-  if (nt > 0) {
-    gu4* krp = (gu4*)(kbase + (int64_t)(t0 + (kt < nt ? kt : last)) * kDenseDim + 64 * khalf);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) krow[u] = krp[u];
-#pragma unroll
-    for (int u = 0; u < kDenseChunk; ++u)
-      vpair[u] = *(gu32*)(vbase + (int64_t)(t0 + (u < nt ? u : last)) * kDenseDim + 2 * lane);
-  }
-  {
-    float qv[kDenseDim * MG / 64];
-    dev_load_n(a.query, (int)a.q_dtype, qv, [&](int r) -> int64_t {
-      const int i = lane + 64 * r, c = i / MG, h = i % MG;
-      return h < G ? (int64_t)b * a.q_sb + (int64_t)(kvh * G + h) * a.q_sh + c : -1;
-    });
-#pragma unroll
-    for (int r = 0; r < kDenseDim * MG / 64; ++r) qs[lane + 64 * r] = qv[r];
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  float m[MG], l[MG], pv0[MG], pv1[MG];
-  if (nt > 0) {
-    // ---- logits: 8 steps of 8 channels ----
-    float logit[MG];
-    DKV_ALL_HEADS(h) logit[h] = 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const uint32_t ww[4] = {krow[u].x, krow[u].y, krow[u].z, krow[u].w};
-      const int qo = after<MG>((64 * khalf + 8 * u) * MG, logit);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float kv = dense_elem<BF>((uint16_t)(ww[i / 2] >> (16 * (i % 2))));
-        float q[MG];
-        lds_heads<MG>(qs + qo + i * MG, q);
-        DKV_ALL_HEADS(h) logit[h] = fmaf(q[h], kv, logit[h]);
-      }
-    }
-    const float scale = (float)a.scale;
-    DKV_ALL_HEADS(h) {
-      const float lg = kt < nt ? (logit[h] + __shfl_xor(logit[h], 32, 64)) * scale : -INFINITY;
-      m[h] = wave_max(lg);
-      const float w = kt < nt ? expf(lg - m[h]) : 0.f;
-      if (khalf == 0) ws[kt * MG + h] = w;
-      l[h] = wave_sum(w) * 0.5f;  // every weight appears in two lanes
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // ---- weighted values: channels 2 lane, 2 lane + 1, 4 steps of 8 tokens ----
-    DKV_ALL_HEADS(h) pv0[h] = pv1[h] = 0.f;
-#pragma unroll
-    for (int u0 = 0; u0 < kDenseChunk; u0 += 8) {
-      const int wo = after<MG>(u0 * MG, pv1);
-#pragma unroll
-      for (int u = u0; u < u0 + 8; ++u) {
-        const float v0 = dense_elem<BF>((uint16_t)vpair[u]);
-        const float v1 = dense_elem<BF>((uint16_t)(vpair[u] >> 16));
-        float w[MG];
-        lds_heads<MG>(ws + wo + (u - u0) * MG, w);
-        DKV_ALL_HEADS(h) {
-          pv0[h] = fmaf(w[h], v0, pv0[h]);
-          pv1[h] = fmaf(w[h], v1, pv1[h]);
-        }
-      }
-    }
-  } else {
-    DKV_ALL_HEADS(h) {
-      m[h] = -INFINITY;
-      l[h] = pv0[h] = pv1[h] = 0.f;
-    }
-  }
-
-  float* wsp = (float*)a.workspace;
-  DKV_FOR_HEAD(h) {
-    const int hq = kvh * G + h;
-    float* rec =
-        wsp + (((int64_t)b * a.Hq + hq) * p.split_stride + p.split_offset + (int64_t)v * chunks + chunk) * (kDenseDim + 2);
-    if (lane == 0) {
-      // a segment this kernel cannot read (a caller that passed no host copy of
-      // the descriptors to check) poisons its record (NaN output)
-      rec[0] = ok ? m[h] : NAN;
-      rec[1] = l[h];
-    }
-    rec[2 + 2 * lane] = pv0[h];
-    rec[3 + 2 * lane] = pv1[h];
-  }
-}
-
 template <int MG, bool BF>
 __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodeParams p, int chunks) {
   __shared__ __attribute__((aligned(16))) float qsh[kDenseWaves][kDenseDim * MG];    // [c][MG]
@@ -452,71 +267,6 @@ __global__ void __launch_bounds__(64 * kDenseWaves) decode_dense_rest(DecodePara
   if (worker >= (int)(p.a.B * p.a.Hkv) * per_bh) return;
   dense_chunk<MG, BF>(p, chunks, worker / per_bh, (worker % per_bh) / chunks, worker % chunks, lane, qsh[wave],
                       wsh[wave]);
-}
-
-// Combine the split records of query heads kvh * G + h (h < G) of batch b with
-// the log-sum-exp rule, then out = acc / max(sum, 1e-20) (attention.py:86).
-// Same arithmetic and summation order for every thread count: per head, the
-// maximum and the sum run over the splits in order; each output channel sums
-// even and odd splits separately and adds the two.  wgt / lsum: G * S floats of
-// LDS each; mx / den: G floats.
-__device__ __forceinline__ void merge_heads(const DecodeParams& p, int b, int hq0, int G, float* wgt, float* lsum,
-                                            float* mx, float* den) {
-  const dkv_decode_args& a = p.a;
-  const int D = (int)a.D, S = p.split_stride;
-  const int tid = threadIdx.x, nt = blockDim.x;
-  const float* ws = (const float*)a.workspace + ((int64_t)b * a.Hq + hq0) * S * (D + 2);
-  for (int i = tid; i < G * S; i += nt) {
-    wgt[i] = ws[(int64_t)i * (D + 2)];
-    lsum[i] = ws[(int64_t)i * (D + 2) + 1];
-  }
-  __syncthreads();
-  if (tid < G) {
-    const float* w = wgt + tid * S;
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, w[s]);
-    mx[tid] = M;
-  }
-  __syncthreads();
-  for (int i = tid; i < G * S; i += nt) {
-    const float ms = wgt[i];
-    wgt[i] = ms == -INFINITY ? 0.f : expf(ms - mx[i / S]);
-  }
-  __syncthreads();
-  if (tid < G) {
-    const float* w = wgt + tid * S;
-    const float* l = lsum + tid * S;
-    float L = 0.f;
-    for (int s = 0; s < S; ++s) L += l[s] * w[s];
-    den[tid] = fmaxf(L, 1e-20f);
-  }
-  __syncthreads();
-  for (int i = tid; i < G * D; i += nt) {
-    const int h = i / D, c = i % D;
-    const float* w = wgt + h * S;
-    const float* rec = ws + (int64_t)h * S * (D + 2) + 2 + c;
-    float o0 = 0.f, o1 = 0.f;
-    int s = 0;
-    for (; s + 8 <= S; s += 8) {  // eight records' loads in flight, then the same sums in order
-      float r[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) r[j] = rec[(int64_t)(s + j) * (D + 2)];
-#pragma unroll
-      for (int j = 0; j < 8; j += 2) {
-        o0 += r[j] * w[s + j];
-        o1 += r[j + 1] * w[s + j + 1];
-      }
-    }
-    for (; s + 1 < S; s += 2) {
-      o0 += rec[(int64_t)s * (D + 2)] * w[s];
-      o1 += rec[(int64_t)(s + 1) * (D + 2)] * w[s + 1];
-    }
-    if (s < S) o0 += rec[(int64_t)s * (D + 2)] * w[s];
-    const float o = (o0 + o1) / den[h];
-    const int hq = hq0 + h;
-    dev_store(a.out, (int64_t)b * a.out_sb + (int64_t)hq * a.out_sh + c, o, (int)a.q_dtype);
-    if (a.out_f32) a.out_f32[((int64_t)b * a.Hq + hq) * D + c] = o;
-  }
 }
 
 // The dense rest segments and the merge in one launch: one block per (batch,
@@ -542,7 +292,8 @@ __global__ void __launch_bounds__(64 * kDenseMergeWaves, MG <= 4 ? 4 : 2) decode
   __syncthreads();
   const int G = p.group, S = p.split_stride;
   const int b = bhi / (int)p.a.Hkv, kvh = bhi % (int)p.a.Hkv;
-  merge_heads(p, b, kvh * G, G, dyn, dyn + G * S, mx, den);
+  merge_heads(p, b, kvh * G, G, dyn, dyn + G * S, mx, den, (int)threadIdx.x, (int)blockDim.x,
+              [] __device__() { __syncthreads(); });
 }
 
 // One block per (batch, query head): the merge alone.
@@ -550,7 +301,8 @@ __global__ void __launch_bounds__(kThreads) decode_merge(DecodeParams p) {
   extern __shared__ float wsh[];  // [S] weights, [S] sums
   __shared__ float mx[1], den[1];
   const int bq = blockIdx.x;  // b * Hq + hq
-  merge_heads(p, bq / (int)p.a.Hq, bq % (int)p.a.Hq, 1, wsh, wsh + p.split_stride, mx, den);
+  merge_heads(p, bq / (int)p.a.Hq, bq % (int)p.a.Hq, 1, wsh, wsh + p.split_stride, mx, den, (int)threadIdx.x,
+              (int)blockDim.x, [] __device__() { __syncthreads(); });
 }
 
 }  // namespace
@@ -652,6 +404,12 @@ static bool dense_rest_ok(const dkv_decode_args& a, const dkv_segment& g) {
          aligned16(g.key[0], g.key_bh[0], 2) && aligned16(g.value[0], g.value_bh[0], 2);
 }
 
+// The page kernels' grid (4 waves per workgroup) holds the page and the
+// dense workers of a launch that merges.
+static bool B_Hkv_rest_chunks_ok(const dkv_decode_args& a, int64_t rest, int64_t chunks) {
+  return a.B * a.Hkv * (a.fast_splits + rest * chunks) < (int64_t)1 << 31;
+}
+
 static int check_segments(const dkv_decode_args& a, int64_t fast_count, bool dense_rest) {
   if (dense_rest && a.tail.tokens > 0)
     DKV_CHECK(dense_rest_ok(a, a.tail), DKV_ERR_INVALID,
@@ -674,7 +432,7 @@ static int check_segments(const dkv_decode_args& a, int64_t fast_count, bool den
 
 extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
   DKV_CHECK(args != nullptr, DKV_ERR_INVALID, "args is NULL");
-  const dkv_decode_args& a = *args;
+  dkv_decode_args a = *args;
   DKV_CHECK(a.B > 0 && a.Hq > 0 && a.Hkv > 0 && a.D > 0, DKV_ERR_INVALID, "bad decode shape");
   DKV_CHECK(a.Hq % a.Hkv == 0, DKV_ERR_INVALID, "query heads must be divisible by cache KV heads");
   DKV_CHECK(a.Hq / a.Hkv <= kMaxGroup, DKV_ERR_UNSUPPORTED, "at most %d query heads per KV head", kMaxGroup);
@@ -726,19 +484,6 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
     if (rc != DKV_OK) return rc;
   }
   hipStream_t s = (hipStream_t)stream;
-  if (fast_count > 0) {
-    int rc = record_event(a.fast_events[0], s);
-    if (rc) return rc;
-    rc = a.fast_promoted > 0
-             ? dkv::launch_fast_decode(a, (int)a.fast_first, (int)fast_count, (int)a.fast_promoted,
-                                       (int)a.fast_value_group, (int)fast_splits, (int)stride, s)
-             : dkv::launch_uniform_decode(a, (int)a.fast_first, (int)fast_count, (int)a.fast_key_bits,
-                                          (int)a.fast_value_bits, (int)a.fast_value_group, (int)fast_splits,
-                                          (int)stride, s);
-    if (rc) return rc;
-    rc = record_event(a.fast_events[1], s);
-    if (rc) return rc;
-  }
   DecodeParams p;
   p.a = a;
   p.group = (int)(a.Hq / a.Hkv);
@@ -749,14 +494,43 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
   p.skip_first = fast_count > 0 ? (int)a.fast_first : 0;
   p.skip_count = fast_count > 0 ? (int)fast_count : 0;
   const bool dense_rest = rest > 0 && a.rest_dense_tokens > 0;
+  const int64_t chunks = dense_rest ? (a.rest_dense_tokens + kDenseChunk - 1) / kDenseChunk : 0;
   if (dense_rest) {
-    const int64_t chunks = (a.rest_dense_tokens + kDenseChunk - 1) / kDenseChunk;
     DKV_CHECK(a.n_splits == rest * chunks, DKV_ERR_INVALID,
               "rest_dense_tokens needs n_splits == non-page segments * ceil(rest_dense_tokens / %d)", kDenseChunk);
     DKV_CHECK(a.cache_dtype == dkv::kBF16 || a.cache_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED,
               "rest_dense_tokens needs a bf16 or fp16 cache");
     DKV_CHECK(a.D == kDenseDim && p.group <= kDenseMaxGroup, DKV_ERR_UNSUPPORTED,
               "rest_dense_tokens needs head_dim %d and at most %d query heads per KV head", kDenseDim, kDenseMaxGroup);
+  }
+  if (fast_count > 0) {
+    // With a dense rest, the page kernel's launch also runs the dense chunks
+    // (extra waves beside the page waves, so their latency hides behind the
+    // pages), and one merge launch follows.  Merging in the page launch itself
+    // (the last wave of a pair merges, found with a device-scope counter) was
+    // measured twice as slow: on this multi-XCD part every wave's device-scope
+    // release writes back its L2.
+    const bool fuse = dense_rest && B_Hkv_rest_chunks_ok(a, rest, chunks) &&
+                      (size_t)2 * stride * sizeof(float) <= 64 * 1024;
+    dkv::FusedRest fr{&p, (int)chunks};
+    int rc = record_event(a.fast_events[0], s);
+    if (rc) return rc;
+    rc = a.fast_promoted > 0
+             ? dkv::launch_fast_decode(a, (int)a.fast_first, (int)fast_count, (int)a.fast_promoted,
+                                       (int)a.fast_value_group, (int)fast_splits, (int)stride, s,
+                                       fuse ? &fr : nullptr)
+             : dkv::launch_uniform_decode(a, (int)a.fast_first, (int)fast_count, (int)a.fast_key_bits,
+                                          (int)a.fast_value_bits, (int)a.fast_value_group, (int)fast_splits,
+                                          (int)stride, s, fuse ? &fr : nullptr);
+    if (rc) return rc;
+    rc = record_event(a.fast_events[1], s);
+    if (rc) return rc;
+    if (fuse) {
+      hipLaunchKernelGGL(decode_merge, dim3((unsigned)(a.B * a.Hq)), dim3(kThreads), 2 * stride * sizeof(float), s, p);
+      return dkv_check_launch("dkv_decode_attention(merge)");
+    }
+  }
+  if (dense_rest) {
     const int mg = p.group <= 1 ? 1 : p.group <= 2 ? 2 : p.group <= 4 ? 4 : 8;
     const size_t merge_lds = (size_t)2 * p.group * stride * sizeof(float);
     if (merge_lds <= 64 * 1024) {

@@ -244,16 +244,19 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   const int n = lane & 15, kq = lane >> 4;
   const int worker = blockIdx.x * kWaves + wave;
   const int total_workers = p.B * p.Hkv * p.splits;
-  if (worker >= total_workers) return;
-  // wave-uniform indices (kept in scalar registers)
-  const int split = __builtin_amdgcn_readfirstlane(worker % p.splits);
-  const int bh = __builtin_amdgcn_readfirstlane(worker / p.splits);
-  const int b = __builtin_amdgcn_readfirstlane(bh / p.Hkv), kvh = __builtin_amdgcn_readfirstlane(bh % p.Hkv);
   constexpr int np = NP;
   constexpr bool bf16 = BF16;
   const int gv = p.gv;
   const LdsMap M = lds_map(np, gv);
   uint8_t* lds = smem + wave * M.bytes;
+  if (worker >= total_workers) {  // a dense-rest worker, or none
+    dense_worker<GQ, BF16>(p, worker - total_workers, lane, (float*)lds);
+    return;
+  }
+  // wave-uniform indices (kept in scalar registers)
+  const int split = __builtin_amdgcn_readfirstlane(worker % p.splits);
+  const int bh = __builtin_amdgcn_readfirstlane(worker / p.splits);
+  const int b = __builtin_amdgcn_readfirstlane(bh / p.Hkv), kvh = __builtin_amdgcn_readfirstlane(bh % p.Hkv);
   const int page0 = __builtin_amdgcn_readfirstlane((int)(((int64_t)split * p.count) / p.splits));
   const int page1 = __builtin_amdgcn_readfirstlane((int)(((int64_t)(split + 1) * p.count) / p.splits));
 
@@ -548,9 +551,10 @@ namespace dkv {
 int fast_decode_max_loads(int np, int gv) { return n_small_loads(np, gv) + n_key_loads(np); }
 
 size_t fast_decode_lds_bytes(int np, int gv) { return (size_t)kWaves * lds_map(np, gv).bytes; }
+size_t fast_decode_wave_lds_bytes(int np, int gv) { return (size_t)lds_map(np, gv).bytes; }
 
 int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, int vg, int splits, int split_stride,
-                       hipStream_t stream) {
+                       hipStream_t stream, const FusedRest* fused) {
   FastParams p;
   p.segs = a.segments;
   p.first = first;
@@ -571,7 +575,8 @@ int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, i
   p.q_sb = a.q_sb;
   p.q_sh = a.q_sh;
   p.ws = (float*)a.workspace;
-  const int64_t workers = (int64_t)p.B * p.Hkv * splits;
+  set_fused(p, fused);
+  const int64_t workers = (int64_t)p.B * p.Hkv * splits + p.dense_workers;
   const unsigned blocks = (unsigned)((workers + kWaves - 1) / kWaves);
   const size_t lds = fast_decode_lds_bytes(np, p.gv);
   const dim3 grid(blocks), block(256);

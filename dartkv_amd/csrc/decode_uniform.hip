@@ -154,13 +154,16 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, kq = lane >> 4;
   const int worker = blockIdx.x * kWaves + wave;
-  if (worker >= p.B * p.Hkv * p.splits) return;
-  const int split = __builtin_amdgcn_readfirstlane(worker % p.splits);
-  const int bh = __builtin_amdgcn_readfirstlane(worker / p.splits);
-  const int b = __builtin_amdgcn_readfirstlane(bh / p.Hkv), kvh = __builtin_amdgcn_readfirstlane(bh % p.Hkv);
   const int gv = p.gv;
   const UMap M = umap(KB, VB, gv);
   uint8_t* lds = smem + wave * M.bytes;
+  if (worker >= p.B * p.Hkv * p.splits) {  // a dense-rest worker, or none
+    dense_worker<GQ, BF16>(p, worker - p.B * p.Hkv * p.splits, lane, (float*)lds);
+    return;
+  }
+  const int split = __builtin_amdgcn_readfirstlane(worker % p.splits);
+  const int bh = __builtin_amdgcn_readfirstlane(worker / p.splits);
+  const int b = __builtin_amdgcn_readfirstlane(bh / p.Hkv), kvh = __builtin_amdgcn_readfirstlane(bh % p.Hkv);
   const int hp0 = __builtin_amdgcn_readfirstlane((int)(((int64_t)split * 2 * p.count) / p.splits));
   const int hp1 = __builtin_amdgcn_readfirstlane((int)(((int64_t)(split + 1) * 2 * p.count) / p.splits));
 
@@ -353,12 +356,14 @@ namespace dkv {
 
 // The kernel waits until at most one half page's key or value loads are in
 // flight; vm_wait takes counts below 16.
+size_t uniform_decode_wave_lds_bytes(int kb, int vb, int gv) { return (size_t)umap(kb, vb, gv).bytes; }
+
 int uniform_decode_max_loads(int kb, int vb) {
   return n_key_loads_u(kb) > n_value_loads_u(vb) ? n_key_loads_u(kb) : n_value_loads_u(vb);
 }
 
 int launch_uniform_decode(const dkv_decode_args& a, int first, int count, int kb, int vb, int vg, int splits,
-                          int split_stride, hipStream_t stream) {
+                          int split_stride, hipStream_t stream, const FusedRest* fused) {
   FastParams p;
   p.segs = a.segments;
   p.first = first;
@@ -379,7 +384,8 @@ int launch_uniform_decode(const dkv_decode_args& a, int first, int count, int kb
   p.q_sb = a.q_sb;
   p.q_sh = a.q_sh;
   p.ws = (float*)a.workspace;
-  const int64_t workers = (int64_t)p.B * p.Hkv * splits;
+  set_fused(p, fused);
+  const int64_t workers = (int64_t)p.B * p.Hkv * splits + p.dense_workers;
   const dim3 grid((unsigned)((workers + kWaves - 1) / kWaves)), block(256);
   const size_t lds = (size_t)kWaves * umap(kb, vb, p.gv).bytes;
   if ((kb != 2 && kb != 4 && kb != 8) || (vb != 2 && vb != 4 && vb != 8)) {

@@ -6,6 +6,7 @@
 
 #include "dkv_capi_util.h"
 #include "dkv_decode.h"
+#include "dkv_dense.h"
 #include "dkv_device.h"
 
 namespace {
@@ -63,7 +64,32 @@ struct FastParams {
   int q_dtype;
   int64_t q_sb, q_sh;
   float* ws;
+  // With a dense rest in the launch (dense_workers > 0), the workers past the
+  // page workers run its chunks (dense_worker) and write their records.
+  int dense_chunks, dense_workers;
+  DecodeParams rest;
 };
+
+// Host side: the dense-rest fields of a page kernel's parameters (none when
+// f is null).  Call after p.B and p.Hkv are set.
+inline void set_fused(FastParams& p, const FusedRest* f) {
+  p.dense_chunks = p.dense_workers = 0;
+  if (f == nullptr) return;
+  p.rest = *f->rest;
+  p.dense_chunks = f->chunks;
+  p.dense_workers = p.B * p.Hkv * p.rest.n_total * f->chunks;
+}
+
+// Dense-rest worker dw of a page kernel launch: chunk dw % (n_total * chunks)
+// of (batch, kv head) dw / (n_total * chunks), with the wave's LDS region.
+template <int MG, bool BF>
+__device__ __forceinline__ void dense_worker(const FastParams& p, int dw, int lane, float* lds) {
+  if (dw >= p.dense_workers) return;
+  const int per_bh = p.rest.n_total * p.dense_chunks;
+  const int bhi = dw / per_bh, t = dw % per_bh;
+  dense_chunk<MG, BF>(p.rest, p.dense_chunks, bhi, t / p.dense_chunks, t % p.dense_chunks, lane, lds,
+                      lds + kDenseDim * MG);
+}
 
 struct PageAddr {
   const uint8_t *kl, *kh, *vc;
