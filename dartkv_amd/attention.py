@@ -87,6 +87,51 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+def _call_layout(plan, cache: DartKVCache, q3: torch.Tensor, kv_heads: int, head_dim: int, tail, use_fast: bool,
+                 dense_ok: bool, n_splits: Optional[int], factor: float):
+    """The parts of a decode call's arguments that depend only on the plan and the call's shape: split
+    counts, the kernels' descriptors and options (a ``DecodeArgs`` without the per-call pointers), and the
+    workspace size.  Kept per plan and call shape."""
+    batch, Hq = q3.shape[0], q3.shape[1]
+    group = Hq // kv_heads
+    fast_count = plan.fast_count if use_fast else 0
+    rest = plan.count - fast_count + (1 if tail.tokens > 0 else 0)
+    # the dense kernel takes the non-page segments (sink, tail) when they are
+    # all dense: one record per 32-token chunk of each
+    dense_tokens = 0
+    if use_fast and rest and group <= 8 and plan.rest_dense >= 0 and dense_ok:
+        dense_tokens = max(plan.rest_dense, tail.tokens)
+    if fast_count:
+        # the uniform page kernel splits over half pages
+        units = fast_count if plan.fast_promoted else 2 * fast_count
+        fast_splits = n_splits or page_kernel_splits(batch, kv_heads, units)
+        fast_splits = max(1, min(fast_splits, units))
+        splits = rest * -(-dense_tokens // 32) if dense_tokens else (max(1, min(rest, 4)) if rest else 0)
+    else:
+        fast_splits = 0
+        splits = n_splits or default_splits(batch, kv_heads, rest)
+        splits = max(1, min(splits, max(1, rest)))
+    a = _lib.DecodeArgs()
+    a.q_dtype = _lib.dtype_code(q3.dtype)
+    a.q_sb, a.q_sh = q3.stride(0), q3.stride(1)
+    a.segments = 0 if plan.table is None else plan.table.data_ptr()
+    a.n_segments = plan.count
+    a.segments_host = None if plan.host_table is None else ctypes.addressof(plan.host_table)
+    a.B, a.Hq, a.Hkv, a.D = batch, Hq, kv_heads, head_dim
+    a.cache_dtype = _lib.dtype_code(cache.dtype)
+    a.meta_dtype = _lib.dtype_code(cache.config.metadata_dtype)
+    a.scale = float(factor)
+    a.n_splits = splits
+    a.workspace_bytes = _lib.load().dkv_decode_workspace_bytes(batch, Hq, head_dim, splits + fast_splits)
+    if fast_count:
+        a.fast_first, a.fast_count = plan.fast_first, fast_count
+        a.fast_promoted, a.fast_value_group, a.fast_splits = plan.fast_promoted, plan.fast_value_group, fast_splits
+        a.fast_key_bits, a.fast_value_bits = plan.fast_key_bits, plan.fast_value_bits
+    # a whole number of chunks: valid for every tail length with this chunk count
+    a.rest_dense_tokens = 32 * -(-dense_tokens // 32)
+    return a, a.workspace_bytes
+
+
 def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,
                      n_splits: Optional[int] = None, out_f32: Optional[torch.Tensor] = None,
                      fast: Optional[bool] = None, fast_events=None, out: Optional[torch.Tensor] = None,
@@ -116,61 +161,34 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     factor = scale if scale is not None else 1.0 / math.sqrt(head_dim)
     plan = cache.decode_plan(query.device)
     tail = tail_segment(cache) if plan.tail_is_pending else _lib.Segment()
-    group = q3.shape[1] // kv_heads
-    use_fast = (_fast_enabled() if fast is None else fast) and plan.fast_count > 0 and group in (1, 2, 4)
-    fast_count = plan.fast_count if use_fast else 0
-    rest = plan.count - fast_count + (1 if tail.tokens > 0 else 0)
-    # the dense kernel takes the non-page segments (sink, tail) when they are
-    # all dense: one record per 32-token chunk of each
-    dense_tokens = 0
-    if use_fast and rest and group <= 8 and plan.rest_dense >= 0 and (tail.tokens == 0 or _dense16_ok(tail)):
-        dense_tokens = max(plan.rest_dense, tail.tokens)
-    if fast_count:
-        # the uniform page kernel splits over half pages
-        units = fast_count if plan.fast_promoted else 2 * fast_count
-        fast_splits = n_splits or page_kernel_splits(batch, kv_heads, units)
-        fast_splits = max(1, min(fast_splits, units))
-        splits = rest * -(-dense_tokens // 32) if dense_tokens else (max(1, min(rest, 4)) if rest else 0)
-    else:
-        fast_splits = 0
-        splits = n_splits or default_splits(batch, kv_heads, rest)
-        splits = max(1, min(splits, max(1, rest)))
     Hq = q3.shape[1]
+    use_fast = (_fast_enabled() if fast is None else fast) and plan.fast_count > 0 and Hq // kv_heads in (1, 2, 4)
+    dense_ok = tail.tokens == 0 or _dense16_ok(tail)
+    chunks = -(-max(plan.rest_dense, tail.tokens) // 32)
+    key = (Hq, q3.dtype, q3.stride(0), q3.stride(1), use_fast, n_splits, factor, static_scratch, tail.tokens > 0,
+           dense_ok, chunks)
+    layout = plan.call_layouts.get(key)
+    if layout is None:
+        layout = plan.call_layouts[key] = _call_layout(plan, cache, q3, kv_heads, head_dim, tail, use_fast, dense_ok,
+                                                       n_splits, factor)
+    template, ws_bytes = layout
     if out is None:
         out = torch.empty(batch, Hq, 1, head_dim, dtype=query.dtype, device=query.device)
     elif out.shape != (batch, Hq, 1, head_dim) or out.dtype != query.dtype or out.device != query.device \
             or out.stride(-1) != 1:
         raise ValueError("out must be a [B, Hq, 1, D] tensor of the query's dtype and device, unit stride in D")
     lib = _lib.load()
-    ws_bytes = lib.dkv_decode_workspace_bytes(batch, Hq, head_dim, splits + fast_splits)
     workspace = None if static_scratch else _workspace(query.device, ws_bytes)
-    a = _lib.DecodeArgs()
+    a = _lib.DecodeArgs.from_buffer_copy(template)
     a.query = q3.data_ptr()
-    a.q_dtype = _lib.dtype_code(q3.dtype)
-    a.q_sb, a.q_sh = q3.stride(0), q3.stride(1)
     a.out = out.data_ptr()
     a.out_sb, a.out_sh = out.stride(0), out.stride(1)
     if out_f32 is not None:
         if out_f32.shape != (batch, Hq, head_dim) or out_f32.dtype != torch.float32 or not out_f32.is_contiguous():
             raise ValueError("out_f32 must be a contiguous float32 [B, Hq, D] tensor")
         a.out_f32 = out_f32.data_ptr()
-    a.segments = 0 if plan.table is None else plan.table.data_ptr()
-    a.n_segments = plan.count
-    a.segments_host = None if plan.host_table is None else ctypes.addressof(plan.host_table)
     a.tail = tail
-    a.B, a.Hq, a.Hkv, a.D = batch, Hq, kv_heads, head_dim
-    a.cache_dtype = _lib.dtype_code(cache.dtype)
-    meta = cache.config.metadata_dtype
-    a.meta_dtype = _lib.dtype_code(meta)
-    a.scale = float(factor)
-    a.n_splits = splits
     a.workspace = _lib.ptr(workspace)
-    a.workspace_bytes = ws_bytes
-    if fast_count:
-        a.fast_first, a.fast_count = plan.fast_first, fast_count
-        a.fast_promoted, a.fast_value_group, a.fast_splits = plan.fast_promoted, plan.fast_value_group, fast_splits
-        a.fast_key_bits, a.fast_value_bits = plan.fast_key_bits, plan.fast_value_bits
-    a.rest_dense_tokens = dense_tokens
     if cache.device_tail is not None and plan.tail_is_pending:
         a.tail_tokens_dev = cache.device_tail.data_ptr()
     if fast_events is not None:

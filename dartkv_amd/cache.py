@@ -206,6 +206,7 @@ class _DecodePlan:
          self.fast_value_bits) = fast
         self.rest_dense = rest_dense
         self.host_table = None  # the descriptors in host memory (dkv_decode_args.segments_host)
+        self.call_layouts: dict = {}  # decode call shape -> (DecodeArgs template, workspace bytes)
 
 
 class DartKVCache:
@@ -236,6 +237,7 @@ class DartKVCache:
         self._tail_value: Optional[torch.Tensor] = None
         self._tail_count_dev: Optional[torch.Tensor] = None  # held tail length on the device (graph replay)
         self._finite_scope: Optional[_FiniteScope] = None
+        self._tail_desc = None  # (tail tensors' addresses and strides, their descriptor without a token count)
         self._sealed_pairs_cache: Optional[Tuple[int, list]] = None
         self._directory_cache: dict = {}
         self._decode_plan_cache: Optional[_DecodePlan] = None
@@ -1371,23 +1373,30 @@ def tail_segment(cache: DartKVCache):
     """Descriptor of the held tail (pending tokens in the tail buffer).
 
     With device-side tail counts the descriptor spans the whole tail buffer
-    (its capacity) and the kernels read the live count from the device.
+    (its capacity) and the kernels read the live count from the device.  The
+    descriptor of a tail is kept while its tensors keep their addresses and
+    strides (one-token appends only change the token count).
     """
-    desc = _lib.Segment()
     if cache._tail_count_dev is not None:
         pk, pv = cache._tail_key, cache._tail_value
     elif cache._pending_key is None:
-        return desc
+        return _lib.Segment()
     else:
         pk, pv = cache._pending_key, cache._pending_value
+    key = (pk.data_ptr(), pv.data_ptr(), pk.stride(), pv.stride())
+    held = cache._tail_desc
+    if held is None or held[0] != key:
+        desc = _lib.Segment()
+        desc.key_kind = _lib.KEY_DENSE
+        desc.value_kind = _lib.VALUE_DENSE
+        keep: list = []
+        desc.key[0], desc.key_bh[0] = _dense_block(pk, keep)
+        desc.value[0], desc.value_bh[0] = _dense_block(pv, keep)
+        if keep:
+            raise RuntimeError("held tail is not in the tail buffer layout")
+        held = cache._tail_desc = (key, desc)
+    desc = _lib.Segment.from_buffer_copy(held[1])
     desc.tokens = pk.shape[-2]
-    desc.key_kind = _lib.KEY_DENSE
-    desc.value_kind = _lib.VALUE_DENSE
-    keep: list = []
-    desc.key[0], desc.key_bh[0] = _dense_block(pk, keep)
-    desc.value[0], desc.value_bh[0] = _dense_block(pv, keep)
-    if keep:
-        raise RuntimeError("held tail is not in the tail buffer layout")
     return desc
 
 

@@ -414,15 +414,18 @@ def test_decode_checks_the_page_and_dense_contracts_against_the_host_descriptors
     plan = cache.decode_plan(q.device)
     assert plan.fast_first == 1 and plan.fast_count == (700 - 32) // 128 and plan.rest_dense >= 0
     first, count = plan.fast_first, plan.fast_count
-    try:
+    try:  # (the plan keeps call layouts derived from these fields: they are dropped after each change)
         plan.fast_first = 0  # entry 0 is the dense sink
+        plan.call_layouts.clear()
         with pytest.raises(ValueError, match="descriptor 0 is not a page the fast page kernel reads"):
             dart.decode_attention(q, cache, fast=True)
         plan.fast_first, plan.fast_count = first, count - 1  # the last page falls to the dense kernel
+        plan.call_layouts.clear()
         with pytest.raises(ValueError, match=f"descriptor {first + count - 1} is not a dense segment"):
             dart.decode_attention(q, cache, fast=True)
     finally:
         plan.fast_first, plan.fast_count = first, count
+        plan.call_layouts.clear()
     out = torch.empty(1, 8, 128, dtype=torch.float32, device=DEV)
     dart.decode_attention(q, cache, out_f32=out, fast=True)
     torch.cuda.synchronize()
