@@ -114,6 +114,32 @@ __device__ __forceinline__ float src_round(float x) {
   return x;
 }
 
+// Four quotients q of the exact chain (each x - min rounded, divided by the
+// group scale, rounded) to their codes clamp(rint(q), 0, qmax), one byte each
+// (byte j of the result), with v_cvt_pk_u8_f32: it rounds half to even and
+// clamps to [0, 255] (checked against rint on the device over every bf16 value
+// in [-4, 300] and the fp32 neighbours of half-integers).  The chain never
+// gives q < 0 (x >= min), and q < qmax + 1/2: the scale s is range / qmax
+// rounded (relative error at most 2^-9 for bf16, less for fp16 and fp32), so
+// q <= qmax (1 + 2^-8) + one rounding, below qmax + 1/2 for qmax 3 and 15; for
+// qmax 255 the instruction's own clamp is the chain's.
+__device__ __forceinline__ uint32_t codes_as_bytes(const float (&q)[4]) {
+  uint32_t r = __builtin_amdgcn_cvt_pk_u8_f32(q[0], 0u, 0u);
+  r = __builtin_amdgcn_cvt_pk_u8_f32(q[1], 1u, r);
+  r = __builtin_amdgcn_cvt_pk_u8_f32(q[2], 2u, r);
+  return __builtin_amdgcn_cvt_pk_u8_f32(q[3], 3u, r);
+}
+// Four byte codes below 16 (byte j) -> nibbles j in bits 4j .. 4j + 3.
+__device__ __forceinline__ uint32_t nibbles_from_bytes(uint32_t b) {
+  const uint32_t t = (b | (b >> 4)) & 0x00ff00ffu;  // c0 | c1 << 4 at bit 0, c2 | c3 << 4 at bit 16
+  return (t | (t >> 8)) & 0xffffu;
+}
+// Four byte codes below 4 (byte j) -> 2-bit fields j in bits 2j, 2j + 1.
+__device__ __forceinline__ uint32_t pairs_from_bytes(uint32_t b) {
+  const uint32_t t = (b | (b >> 6)) & 0x000f000fu;  // c0 | c1 << 2 at bit 0, c2 | c3 << 2 at bit 16
+  return (t | (t >> 12)) & 0xffu;
+}
+
 // fp32 a / b rounded to nearest, given y = RN(1 / b): q = RN(a y) is within
 // one ulp of a / b, the residual a - b q is exact with an fma, and
 // RN(q + (a - b q) y) is the correctly rounded quotient (Markstein's
@@ -225,15 +251,17 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
         dev_store_meta(p.zero, ro * p.groups + g, mn, p.meta_dtype);
         flag_nonfinite(p.nonfinite, mn, mx);
       }
-      uint32_t packed[2] = {0u, 0u};  // codes 0..3 and 4..7 for 8-bit, else all in [0]
+      // codes 0..3 and 4..7 as bytes (codes_as_bytes), then packed to BITS-bit fields
+      uint32_t packed[2];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float diff = src_round<SRC>(x[u][j] - mn);
-        const float q = __builtin_rintf(src_round<SRC>(div_rn(diff, s, y)));
-        const uint32_t code = (uint32_t)fminf(fmaxf(q, 0.0f), qmax);
-        if (BITS == 8) packed[j / 4] |= code << (8 * (j % 4));
-        else packed[0] |= code << (j * BITS);
+      for (int h = 0; h < 2; ++h) {
+        float q[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = src_round<SRC>(div_rn(src_round<SRC>(x[u][4 * h + j] - mn), s, y));
+        packed[h] = codes_as_bytes(q);
       }
+      if (BITS == 4) packed[0] = nibbles_from_bytes(packed[0]) | (nibbles_from_bytes(packed[1]) << 16);
+      if (BITS == 2) packed[0] = pairs_from_bytes(packed[0]) | (pairs_from_bytes(packed[1]) << 8);
       uint8_t* out = p.values + ro * p.packed_bytes + (int64_t)li[u] * BITS;
       if (BITS == 2) *(uint16_t*)out = (uint16_t)packed[0];
       else if (BITS == 4) *(uint32_t*)out = packed[0];
@@ -957,7 +985,6 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
     constexpr int kCodePitch = row_bytes + 16;
     static_assert(kFastKeyD * (BITS == 2 ? 2 : 1) * kCodePitch <= (int)sizeof(tile), "packed rows must fit the tile");
     const int sl = slot[c];
-    const float qmax = mixed ? (sl >= 0 ? 15.0f : 3.0f) : (float)((1 << BITS) - 1);
     const float mn = ch_mn[c], s = ch_s[c], y = ch_y[c];
     uint32_t lo[nw], hi[nw];
 #pragma unroll
@@ -968,13 +995,22 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
       for (int j = 0; j < tpd; ++j) xs[j] = tile_x<SRC>(tile, min(tb + j, T - 1), c);  // padding repeats the last token
       lo[w] = 0;
       hi[w] = 0;
+      // four tokens' codes at a time as bytes (codes_as_bytes: qmax is 3 or
+      // 15 here, or the byte range for 8-bit keys), then packed
 #pragma unroll
-      for (int j = 0; j < tpd; ++j) {
-        const float diff = src_round<SRC>(xs[j] - mn);
-        const float q = __builtin_rintf(src_round<SRC>(div_rn(diff, s, y)));
-        const uint32_t code = (uint32_t)fminf(fmaxf(q, 0.0f), qmax);
-        lo[w] |= (code & ((1u << BITS) - 1)) << (BITS * j);
-        if (BITS == 2) hi[w] |= (code >> 2) << (2 * j);
+      for (int g = 0; g < tpd / 4; ++g) {
+        float q[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = src_round<SRC>(div_rn(src_round<SRC>(xs[4 * g + j] - mn), s, y));
+        const uint32_t b = codes_as_bytes(q);
+        if (BITS == 8) {
+          lo[w] = b;
+        } else if (BITS == 4) {
+          lo[w] |= nibbles_from_bytes(b) << (16 * g);
+        } else {
+          lo[w] |= pairs_from_bytes(b & 0x03030303u) << (8 * g);
+          hi[w] |= pairs_from_bytes((b >> 2) & 0x03030303u) << (8 * g);
+        }
       }
     }
     __syncthreads();  // the tile is read for the last time above
