@@ -430,3 +430,34 @@ def test_decode_checks_the_page_and_dense_contracts_against_the_host_descriptors
     dart.decode_attention(q, cache, out_f32=out, fast=True)
     torch.cuda.synchronize()
     assert rel_err(out.unsqueeze(2), ref32) <= 2e-3
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_codes_round_half_to_even_on_exact_half_quotients(bits, dtype):
+    """Groups whose scale is exactly 1 (min 0, max qmax) and whose elements are half-integers: every
+    quotient is an exact tie, so the codes pin the kernels' rounding (half to even, then the clamp to
+    [0, qmax]) against the oracle, for value rows, uniform key pages and Dart key pages."""
+    from oracle import dart_oracle as O
+    dart = _dkv()
+    qmax = (1 << bits) - 1
+    halves = torch.arange(0, qmax, dtype=torch.float32) + 0.5
+    groups = 2 * -(-qmax // 62)
+    body = halves.repeat(-(-groups * 62 // qmax))[: groups * 62].reshape(groups, 62)
+    ends = torch.tensor([0.0, float(qmax)]).expand(groups, 2)
+    x = torch.cat([ends, body], 1).to(dtype)  # each group of 64: min 0, max qmax (scale exactly 1), then ties
+    q = dart.quantize(x.to(DEV), bits=bits, group_size=64, metadata_dtype=torch.float32)
+    ref = O.quantize(x, bits=bits, group_size=64, metadata_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert bits_equal(q.values.cpu(), ref.values) and bits_equal(q.scale.cpu(), ref.scale)
+    # keys along the tokens: a [1, 1, 128, 128] page whose channels each run through the same values
+    keys = torch.cat([x[0], x[-1]])[:128].reshape(128, 1).expand(128, 128).contiguous().reshape(1, 1, 128, 128)
+    kq = dart.quantize(keys.to(DEV), bits=bits, group_size=128, metadata_dtype=torch.float32, axis=2)
+    kref = O.quantize(keys, bits=bits, group_size=128, metadata_dtype=torch.float32, axis=2)
+    torch.cuda.synchronize()
+    assert bits_equal(kq.values.cpu(), kref.values)
+    if bits == 2:
+        mk = dart.quantize_key_mixed(keys.to(DEV), group_size=128, promote_ratio=0.25)
+        mref = O.quantize_key_mixed(keys, group_size=128, promote_ratio=0.25)
+        torch.cuda.synchronize()
+        assert bits_equal(mk.low_values.cpu(), mref.low_values) and bits_equal(mk.high_values.cpu(), mref.high_values)
