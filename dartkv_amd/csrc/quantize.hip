@@ -150,6 +150,39 @@ __device__ __forceinline__ float div_rn(float a, float b, float y) {
   return __builtin_fmaf(r, y, q);
 }
 
+// Two values rounded to the source dtype at once: for bf16 one packed
+// conversion (v_cvt_pk_bf16_f32, nearest-even like the single one) and two
+// unpacks instead of two conversions and two unpacks.
+template <int SRC>
+__device__ __forceinline__ void src_round2(float& a, float& b) {
+  if (SRC == kBF16) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+    a = __builtin_bit_cast(float, u << 16);
+    b = __builtin_bit_cast(float, u & 0xffff0000u);
+  } else {
+    a = src_round<SRC>(a);
+    b = src_round<SRC>(b);
+  }
+}
+
+// The exact chain's quotients of four elements: round(round(x - mn) / s),
+// the divisions by div_rn against y = RN(1 / s).
+template <int SRC>
+__device__ __forceinline__ void chain_quotients4(const float* x, float mn, float s, float y, float (&q)[4]) {
+  float d[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) d[j] = x[j] - mn;
+  src_round2<SRC>(d[0], d[1]);
+  src_round2<SRC>(d[2], d[3]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) q[j] = div_rn(d[j], s, y);
+  src_round2<SRC>(q[0], q[1]);
+  src_round2<SRC>(q[2], q[3]);
+}
+
+
 // The group scale of dev_group_scale (round(round(max - min) / qmax) in the
 // source dtype, range clamped below by eps) with the division by qmax as
 // div_rn against y = RN(1 / qmax).  For qmax 3, 15 and 255 that equals the
@@ -256,8 +289,7 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         float q[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) q[j] = src_round<SRC>(div_rn(src_round<SRC>(x[u][4 * h + j] - mn), s, y));
+        chain_quotients4<SRC>(&x[u][4 * h], mn, s, y, q);
         packed[h] = codes_as_bytes(q);
       }
       if (BITS == 4) packed[0] = nibbles_from_bytes(packed[0]) | (nibbles_from_bytes(packed[1]) << 16);
@@ -1000,8 +1032,7 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
 #pragma unroll
       for (int g = 0; g < tpd / 4; ++g) {
         float q[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) q[j] = src_round<SRC>(div_rn(src_round<SRC>(xs[4 * g + j] - mn), s, y));
+        chain_quotients4<SRC>(&xs[4 * g], mn, s, y, q);
         const uint32_t b = codes_as_bytes(q);
         if (BITS == 8) {
           lo[w] = b;
