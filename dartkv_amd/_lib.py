@@ -26,7 +26,7 @@ KEY_DENSE, KEY_UNIFORM, KEY_MIXED = 0, 1, 2
 VALUE_DENSE, VALUE_UNIFORM = 0, 1
 SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
@@ -115,12 +115,23 @@ class DecodePrepArgs(ctypes.Structure):
     ]
 
 
+class CopyBlock(ctypes.Structure):
+    _fields_ = [
+        ("src", ctypes.c_void_p), ("dst", ctypes.c_void_p),
+        ("B", ctypes.c_int64), ("H", ctypes.c_int64), ("T", ctypes.c_int64), ("row_bytes", ctypes.c_int64),
+        ("src_sb", ctypes.c_int64), ("src_sh", ctypes.c_int64), ("src_st", ctypes.c_int64),
+        ("dst_sb", ctypes.c_int64), ("dst_sh", ctypes.c_int64), ("dst_st", ctypes.c_int64),
+    ]
+
+
+COPY_MAX_BLOCKS = 8
+
 EXPORTED = (
     "dkv_last_error", "dkv_abi_version", "dkv_quantize_rows", "dkv_quantize_row_blocks", "dkv_quantize_value_rows",
     "dkv_quantize_key_pages",
     "dkv_dequantize_rows",
     "dkv_dequantize_mixed", "dkv_decode_workspace_bytes", "dkv_decode_attention", "dkv_decode_attention_noalloc",
-    "dkv_decode_scratch_bytes", "dkv_decode_prep",
+    "dkv_decode_scratch_bytes", "dkv_decode_prep", "dkv_copy_token_blocks",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -156,10 +167,11 @@ def load() -> ctypes.CDLL:
         lib.dkv_decode_scratch_bytes.argtypes = []
         lib.dkv_decode_scratch_bytes.restype = i64
         lib.dkv_decode_prep.argtypes = [ctypes.POINTER(DecodePrepArgs), vp]
+        lib.dkv_copy_token_blocks.argtypes = [ctypes.POINTER(CopyBlock), i64, vp]
         for name in ("dkv_quantize_rows", "dkv_quantize_row_blocks", "dkv_quantize_value_rows", "dkv_quantize_key_pages",
                      "dkv_dequantize_rows",
                      "dkv_dequantize_mixed", "dkv_decode_attention", "dkv_decode_attention_noalloc",
-                     "dkv_decode_prep"):
+                     "dkv_decode_prep", "dkv_copy_token_blocks"):
             getattr(lib, name).restype = ctypes.c_int
         if lib.dkv_abi_version() != ABI_VERSION:
             raise RuntimeError("libdartkv_hip.so ABI version mismatch; rebuild it")
@@ -202,3 +214,26 @@ def stream_ptr(device: torch.device) -> int:
 
 def ptr(t: Optional[torch.Tensor]) -> int:
     return 0 if t is None else t.data_ptr()
+
+
+def copy_token_blocks(pairs, device: torch.device) -> None:
+    """dst.copy_(src) for each (dst, src) pair of [B, H, T, D] tensors of one dtype on ``device``, up to
+    COPY_MAX_BLOCKS pairs per launch (dkv_copy_token_blocks); the last dimension must be contiguous."""
+    for dst, src in pairs:
+        if dst.shape != src.shape or dst.dtype != src.dtype or dst.dim() != 4:
+            raise ValueError("copy_token_blocks: pairs must be [B, H, T, D] tensors of one shape and dtype")
+        if dst.stride(3) != 1 or src.stride(3) != 1:
+            raise ValueError("copy_token_blocks: the last dimension must be contiguous")
+    lib = load()
+    stream = stream_ptr(device)
+    for at in range(0, len(pairs), COPY_MAX_BLOCKS):
+        chunk = pairs[at:at + COPY_MAX_BLOCKS]
+        blocks = (CopyBlock * len(chunk))()
+        for blk, (dst, src) in zip(blocks, chunk):
+            e = src.element_size()
+            blk.src, blk.dst = src.data_ptr(), dst.data_ptr()
+            blk.B, blk.H, blk.T, _ = src.shape
+            blk.row_bytes = src.shape[3] * e
+            blk.src_sb, blk.src_sh, blk.src_st = src.stride(0) * e, src.stride(1) * e, src.stride(2) * e
+            blk.dst_sb, blk.dst_sh, blk.dst_st = dst.stride(0) * e, dst.stride(1) * e, dst.stride(2) * e
+        check(lib.dkv_copy_token_blocks(blocks, len(chunk), stream), "dkv_copy_token_blocks")

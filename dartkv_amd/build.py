@@ -20,7 +20,7 @@ from concurrent.futures import ThreadPoolExecutor
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libdartkv_hip.so")
-SOURCES = ["capi.hip", "quantize.hip", "decode.hip", "decode_fast.hip", "decode_uniform.hip", "prep.hip"]
+SOURCES = ["capi.hip", "quantize.hip", "decode.hip", "decode_fast.hip", "decode_uniform.hip", "prep.hip", "copy.hip"]
 ARCH = os.environ.get("DKV_OFFLOAD_ARCH", "gfx950")
 
 

@@ -133,15 +133,17 @@ _flag_store = threading.local()
 
 
 def _nonfinite_flags(device: torch.device) -> torch.Tensor:
-    """int32 [2] device flags (keys, values) for the quantizers' non-finite reports, one pair per thread
-    and device and shared by that thread's caches (an append's scope reads them before the next append
-    can start on the thread).  They are zero between appends."""
+    """int32 [2] flags (keys, values) for the quantizers' non-finite reports on ``device``, one pair per
+    thread and device and shared by that thread's caches (an append's scope reads them before the next
+    append can start on the thread).  They live in pinned host memory, which the kernels write directly:
+    reading them after the append's launches takes a stream synchronization and no device-to-host copy.
+    They are zero between appends."""
     flags = getattr(_flag_store, "flags", None)
     if flags is None:
         flags = _flag_store.flags = {}
     t = flags.get(device)
     if t is None:
-        t = flags[device] = torch.zeros(2, dtype=torch.int32, device=device)
+        t = flags[device] = torch.zeros(2, dtype=torch.int32, pin_memory=True)
     return t
 
 
@@ -237,6 +239,7 @@ class DartKVCache:
         self._tail_value: Optional[torch.Tensor] = None
         self._tail_count_dev: Optional[torch.Tensor] = None  # held tail length on the device (graph replay)
         self._finite_scope: Optional[_FiniteScope] = None
+        self._copy_queue: Optional[list] = None  # an append's dense token copies, launched once at its end
         self._tail_desc = None  # (tail tensors' addresses and strides, their descriptor without a token count)
         self._sealed_pairs_cache: Optional[Tuple[int, list]] = None
         self._directory_cache: dict = {}
@@ -296,19 +299,30 @@ class DartKVCache:
         sink = min(max(0, self.config.sink_tokens - self._seen_tokens), chunk)
         with self._finite_inputs():
             at_keys, at_values = len(self._keys), len(self._values)
-            if sink < chunk:
-                keys, values = key_states[..., sink:, :], value_states[..., sink:, :]
-                if not self._device_tail_append(keys, values):
-                    if self._tail_count_dev is not None and torch.cuda.is_current_stream_capturing():
-                        raise RuntimeError("a captured append may only extend the held tail by one token")
-                    self._append_tokens(keys, values)
-                    self._sync_device_tail()
-            if sink:
-                # the dense sink tokens precede this append's pages (every earlier token is a sink
-                # token too); they are copied after the quantize launches, which then start sooner
-                self._keys.insert(at_keys, key_states[..., :sink, :].clone())
-                self._values.insert(at_values, value_states[..., :sink, :].clone())
-                self._sealed_version += 1
+            self._copy_queue = []
+            try:
+                if sink < chunk:
+                    keys, values = key_states[..., sink:, :], value_states[..., sink:, :]
+                    if not self._device_tail_append(keys, values):
+                        if self._tail_count_dev is not None and torch.cuda.is_current_stream_capturing():
+                            raise RuntimeError("a captured append may only extend the held tail by one token")
+                        self._append_tokens(keys, values)
+                        self._sync_device_tail()
+                if sink:
+                    # the dense sink tokens precede this append's pages (every earlier token is a sink
+                    # token too); they are copied after the quantize launches, which then start sooner
+                    ks, vs = key_states[..., :sink, :], value_states[..., :sink, :]
+                    kd = torch.empty(ks.shape, dtype=ks.dtype, device=ks.device)
+                    vd = torch.empty(vs.shape, dtype=vs.dtype, device=vs.device)
+                    self._copy_tokens((kd, ks), (vd, vs))
+                    self._keys.insert(at_keys, kd)
+                    self._values.insert(at_values, vd)
+                    self._sealed_version += 1
+                copies = self._copy_queue
+            finally:
+                self._copy_queue = None
+            if copies:
+                _lib.copy_token_blocks(copies, self._device)
         self._seen_tokens += chunk
         self._layout_version += 1
         self._invalidate_page_descriptors()
@@ -610,10 +624,17 @@ class DartKVCache:
             cap = self._tail_capacity()
             self._tail_key = torch.empty(B, H, cap, D, dtype=keys.dtype, device=keys.device)
             self._tail_value = torch.empty(B, H, cap, D, dtype=values.dtype, device=values.device)
-        self._tail_key[..., :n, :].copy_(keys)
-        self._tail_value[..., :n, :].copy_(values)
+        self._copy_tokens((self._tail_key[..., :n, :], keys), (self._tail_value[..., :n, :], values))
         self._pending_key = self._tail_key[..., :n, :]
         self._pending_value = self._tail_value[..., :n, :]
+
+    def _copy_tokens(self, *pairs) -> None:
+        """dst <- src for (dst, src) [B, H, T, D] token blocks: inside an append they wait for the one
+        copy launch at the append's end (dkv_copy_token_blocks)."""
+        if self._copy_queue is not None:
+            self._copy_queue.extend(pairs)
+        else:
+            _lib.copy_token_blocks(list(pairs), self._device)
 
     def _extend_tail(self, key_states: torch.Tensor, value_states: torch.Tensor) -> bool:
         """The decode-step append in few host steps: tokens that only extend the held tail in its
@@ -679,8 +700,8 @@ class DartKVCache:
         sealable = (max(0, total - c.local_tokens) // c.page_size) * c.page_size
         if sealable == 0 and self._pending_in_tail() and total <= self._tail_capacity():
             # the new tokens only extend the held tail
-            self._tail_key[..., pending:total, :].copy_(keys)
-            self._tail_value[..., pending:total, :].copy_(values)
+            self._copy_tokens((self._tail_key[..., pending:total, :], keys),
+                              (self._tail_value[..., pending:total, :], values))
             self._pending_key = self._tail_key[..., :total, :]
             self._pending_value = self._tail_value[..., :total, :]
             return
@@ -757,9 +778,12 @@ class DartKVCache:
             self._finite_scope = None
             self._value_job = None
             if not ok and scope.flags is not None:
-                scope.flags.zero_()  # launches before the error may have set them
+                # launches before the error may set them: clear them once those have run
+                torch.cuda.current_stream(self._device).synchronize()
+                scope.flags.zero_()
         if scope.flags is None:
             return
+        torch.cuda.current_stream(self._device).synchronize()
         bad_keys, bad_values = scope.flags.tolist()
         if bad_keys or bad_values:
             scope.flags.zero_()
@@ -769,8 +793,8 @@ class DartKVCache:
             raise ValueError("quantize expects all values to be finite")
 
     def _flag_ptr(self, which: int) -> int:
-        """Device address of the non-finite flag of keys (0) or values (1) for a launch inside the
-        append's scope, which then checks it; 0 (no check) outside a scope."""
+        """Address (pinned host memory the kernels write) of the non-finite flag of keys (0) or values (1)
+        for a launch inside the append's scope, which then checks it; 0 (no check) outside a scope."""
         scope = self._finite_scope
         if scope is None:
             return 0

@@ -47,7 +47,7 @@ extern "C" {
 /* Thread-local description of the last error on this thread. */
 const char* dkv_last_error(void);
 
-/* ABI version (11); bumps when a struct or an entry point below changes. */
+/* ABI version (12); bumps when a struct or an entry point below changes. */
 int dkv_abi_version(void);
 
 /*
@@ -99,9 +99,11 @@ typedef struct dkv_value_rows_args {
   void* scale;
   void* zero;
   int64_t meta_dtype;
-  /* Optional (NULL: no check): a device uint32 set to 1 when a group holds a
-   * NaN or an infinity (the reference raises ValueError for such inputs,
-   * src/dart/quantization.py:159-160); never cleared by the library. */
+  /* Optional (NULL: no check): a uint32 the device can write (device memory,
+   * or pinned host memory, read after a stream synchronization without a
+   * copy) set to 1 when a group holds a NaN or an infinity (the reference
+   * raises ValueError for such inputs, src/dart/quantization.py:159-160);
+   * never cleared by the library. */
   uint32_t* nonfinite;
   /* Output placement: source row blk * block_rows + i goes to output row
    * blk * out_block_rows + out_row0 + i (out_block_rows 0: block_rows, the
@@ -165,13 +167,34 @@ typedef struct dkv_key_pages_args {
    * one after the other (src/dart/cache.py:472-479); given both, the library
    * runs the value kernel alongside the key path's serial channel selection. */
   const dkv_value_rows_args* values;
-  /* Optional (NULL: no check): a device uint32 set to 1 when a key group holds
-   * a NaN or an infinity (reference src/dart/mixed.py:187-188 and
+  /* Optional (NULL: no check): a uint32 the device can write (as in
+   * dkv_value_rows_args) set to 1 when a key group holds a NaN or an
+   * infinity (reference src/dart/mixed.py:187-188 and
    * src/dart/quantization.py:159-160 raise ValueError); never cleared. */
   uint32_t* nonfinite;
 } dkv_key_pages_args;
 
 int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stream);
+
+/*
+ * Copy the token rows of up to DKV_COPY_MAX_BLOCKS dense blocks in one
+ * launch: block j sets dst[b][h][t] = src[b][h][t] (row_bytes bytes) for
+ * b < B, h < H, t < T; the strides are in bytes, and a block's source and
+ * destination must not overlap.  Blocks of zero rows are skipped.  This is
+ * how an append keeps its dense tokens: reference src/dart/cache.py:183-185
+ * (the sink tokens' clone) and :417-418, :451-467 (the pending tail's clone).
+ */
+#define DKV_COPY_MAX_BLOCKS 8
+
+typedef struct dkv_copy_block {
+  const void* src;
+  void* dst;
+  int64_t B, H, T, row_bytes;
+  int64_t src_sb, src_sh, src_st;
+  int64_t dst_sb, dst_sh, dst_st;
+} dkv_copy_block;
+
+int dkv_copy_token_blocks(const dkv_copy_block* blocks, int64_t n_blocks, void* stream);
 
 /*
  * Dequantize `rows` rows produced by dkv_quantize_rows (same layout) into

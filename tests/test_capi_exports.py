@@ -42,6 +42,13 @@ def test_library_loads_and_reports_errors_without_gpu():
     assert rc == _lib.DKV_ERR_INVALID
     assert b"non-negative" in lib.dkv_last_error()
     assert lib.dkv_decode_workspace_bytes(2, 4, 8, 3) == 2 * 4 * 3 * 10 * 4
+    assert lib.dkv_copy_token_blocks(None, 9, None) == _lib.DKV_ERR_INVALID
+    assert b"n_blocks" in lib.dkv_last_error()
+    assert lib.dkv_copy_token_blocks(None, 0, None) == _lib.DKV_OK  # nothing to copy, nothing launched
+    blk = (_lib.CopyBlock * 1)()
+    blk[0].B, blk[0].H, blk[0].T, blk[0].row_bytes = 1, 1, 4, 256
+    assert lib.dkv_copy_token_blocks(blk, 1, None) == _lib.DKV_ERR_INVALID
+    assert b"NULL" in lib.dkv_last_error()
 
 
 def test_ctypes_structs_match_the_header(tmp_path):
@@ -49,7 +56,8 @@ def test_ctypes_structs_match_the_header(tmp_path):
     import ctypes
     from dartkv_amd import _lib
     structs = {"dkv_segment": _lib.Segment, "dkv_decode_args": _lib.DecodeArgs,
-               "dkv_key_pages_args": _lib.KeyPagesArgs, "dkv_value_rows_args": _lib.ValueRowsArgs}
+               "dkv_key_pages_args": _lib.KeyPagesArgs, "dkv_value_rows_args": _lib.ValueRowsArgs,
+               "dkv_copy_block": _lib.CopyBlock}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dartkv.h"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
