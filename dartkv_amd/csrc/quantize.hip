@@ -808,13 +808,14 @@ __device__ __forceinline__ float tile_x(const uint16_t* tile, int t, int c) {
 // (tokens at or past T add an exact zero).  The 16 reads are issued before
 // the first add.  mode 0: |x|; 1: rnd(rnd(x - m)^2); 2: x.  Also folds the
 // tokens into mn / mx when MINMAX (tokens past T repeat the last one, which
-// leaves min and max unchanged).
-template <int SRC, bool MINMAX>
+// leaves min and max unchanged).  FULL: T is the full page (no clamping, and
+// the reads take constant offsets from one address).
+template <int SRC, bool MINMAX, bool FULL>
 __device__ __forceinline__ float key_chunk_sum(const uint16_t* tile, int c, int tb, int T, int mode, float m,
                                                float& mn, float& mx) {
   float xs[16];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) xs[j] = tile_x<SRC>(tile, min(tb + j, T - 1), c);
+  for (int j = 0; j < 16; ++j) xs[j] = tile_x<SRC>(tile, FULL ? tb + j : min(tb + j, T - 1), c);
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
@@ -829,7 +830,7 @@ __device__ __forceinline__ float key_chunk_sum(const uint16_t* tile, int c, int 
       const float d = src_round<SRC>(x - m);
       term = src_round<SRC>(d * d);
     }
-    acc = acc + (tb + j < T ? term : 0.f);
+    acc = acc + ((FULL || tb + j < T) ? term : 0.f);
   }
   return acc;
 }
@@ -851,7 +852,9 @@ __device__ __forceinline__ float key_cascade_mean(const float* csum, int c, int 
 }
 
 // BITS: code width of the low codes (2 for mixed keys, else the uniform width).
-template <int SRC, int BITS>
+// FULL: every page holds kFastKeyT tokens (token indices need no clamping,
+// and the tile reads take constant offsets: about 3 VALU less per read).
+template <int SRC, int BITS, bool FULL>
 __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k, int mode) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[kFastKeyT * kFastKeyD];
   __shared__ float csum[8 * kFastKeyD];
@@ -865,7 +868,7 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
   const dkv_key_pages_args& a = k.a;
   const int bh = blockIdx.x, page = blockIdx.y;
   const int b = bh / (int)a.H, h = bh % (int)a.H;
-  const int T = (int)a.page_tokens, meta = (int)a.meta_dtype;
+  const int T = FULL ? kFastKeyT : (int)a.page_tokens, meta = (int)a.meta_dtype;
   const bool mixed = a.key_mode == DKV_KEY_MIXED;
   const int K = mixed ? (int)a.promoted : 0;
   constexpr int row_bytes = kFastKeyT * BITS / 8;  // one group of up to 128 tokens per channel row
@@ -880,7 +883,7 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
     uint4 w[kSteps];
 #pragma unroll
     for (int j = 0; j < kSteps; ++j) {
-      const int i = tid + j * kThreads, t = min(i >> 4, T - 1), c8 = i & 15;
+      const int i = tid + j * kThreads, t = FULL ? i >> 4 : min(i >> 4, T - 1), c8 = i & 15;
       w[j] = *(const uint4*)(src + (int64_t)t * a.st + 8 * c8);
     }
     // rows past T hold copies of row T - 1 (reads clamp to T - 1 anyway); an
@@ -905,7 +908,7 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
     for (int q = 0; q < 4; ++q) {
       const int tb = 64 * half + 16 * q;
       if (tb < T) {
-        const float sum = key_chunk_sum<SRC, true>(tile, c, tb, T, magnitude ? 0 : 2, 0.f, mn, mx);
+        const float sum = key_chunk_sum<SRC, true, FULL>(tile, c, tb, T, magnitude ? 0 : 2, 0.f, mn, mx);
         if (select) csum[(tb >> 4) * kFastKeyD + c] = sum;
       }
     }
@@ -922,7 +925,7 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int tb = 64 * half + 16 * q;
-        if (tb < T) csum[(tb >> 4) * kFastKeyD + c] = key_chunk_sum<SRC, false>(tile, c, tb, T, 1, m, mn, mx);
+        if (tb < T) csum[(tb >> 4) * kFastKeyD + c] = key_chunk_sum<SRC, false, FULL>(tile, c, tb, T, 1, m, mn, mx);
       }
       __syncthreads();
       if (half == 0) score[c] = key_cascade_mean<SRC>(csum, c, T);
@@ -1024,7 +1027,8 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
       const int tb = (half * bpp + 4 * w) * per_byte;
       float xs[tpd];
 #pragma unroll
-      for (int j = 0; j < tpd; ++j) xs[j] = tile_x<SRC>(tile, min(tb + j, T - 1), c);  // padding repeats the last token
+      for (int j = 0; j < tpd; ++j)
+        xs[j] = tile_x<SRC>(tile, FULL ? tb + j : min(tb + j, T - 1), c);  // padding repeats the last token
       lo[w] = 0;
       hi[w] = 0;
       // four tokens' codes at a time as bytes (codes_as_bytes: qmax is 3 or
@@ -1101,7 +1105,9 @@ __global__ void __launch_bounds__(64) key_select_pages(KeyParams k, int row_byte
 // Workgroups [0, sel_blocks) select (one wave per page, as key_select_pages);
 // the others quantize value rows (workgroup b - sel_blocks of the gx x gy grid
 // of quantize_rows_vec).  A selection wave mostly waits on its LDS steps;
-// the value rows use each SIMD meanwhile.
+// the value rows use each SIMD meanwhile.  (Spreading the selection
+// workgroups among the value rows' was slower: a selection wave's chain of
+// dependent steps stretches when VALU-bound row waves share its SIMD.)
 constexpr int kSelectWaves = kThreads / 64;
 // Shared launches pay off while every selection wave is resident at once (one
 // wave per page, 256 CUs x 32 waves); past that the selections queue in rounds
@@ -1386,7 +1392,13 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
                                                                        (a.high_page_stride % 4) == 0));
   if (use_fast) {
     const dim3 grid((unsigned)(a.B * a.H), (unsigned)a.n_pages);
-#define DKV_KEYF(T, B, M) hipLaunchKernelGGL((quantize_key_pages_fast<T, B>), grid, dim3(kThreads), 0, s, k, M)
+#define DKV_KEYF(T, B, M)                                                                                 \
+  do {                                                                                                    \
+    if (a.page_tokens == kFastKeyT)                                                                       \
+      hipLaunchKernelGGL((quantize_key_pages_fast<T, B, true>), grid, dim3(kThreads), 0, s, k, M);        \
+    else                                                                                                  \
+      hipLaunchKernelGGL((quantize_key_pages_fast<T, B, false>), grid, dim3(kThreads), 0, s, k, M);       \
+  } while (0)
 #define DKV_KEYF_BITS(T, M)                   \
   do {                                        \
     if (fast_bits == 2) DKV_KEYF(T, 2, M);    \
@@ -1399,7 +1411,7 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
     else DKV_KEYF_BITS(kF16, M);                       \
   } while (0)
     // a data-dependent selection over more than a few pages: scores, one
-    // lane per page selects, codes
+    // wave per page selects, codes
     const bool select = a.key_mode == DKV_KEY_MIXED && Kp > 0 && Kp < a.D && a.selection != DKV_SELECT_GIVEN;
     if (select && a.B * a.H * a.n_pages > 256) {
       const int64_t items = a.B * a.H * a.n_pages;
