@@ -168,7 +168,13 @@ __device__ __forceinline__ void src_round2(float& a, float& b) {
 }
 
 // The exact chain's quotients of four elements: round(round(x - mn) / s),
-// the divisions by div_rn against y = RN(1 / s).
+// y = RN(1 / s).  For fp32 sources the division is div_rn.  For bf16 and fp16
+// sources (d and s 16-bit values) it is one product: rint(round_src(RN(d y)))
+// equals rint(round_src(RN(d / s))) for every 16-bit d >= 0 and s >= 3.8e-7
+// (the smallest scale the eps clamp allows) with d / s < 256, checked
+// exhaustively on the host (tests/quotient/chain_quotient.c); the rounded
+// quotients differ in rare cases, never in the integer they round to, and
+// only that integer (the code) is kept.
 template <int SRC>
 __device__ __forceinline__ void chain_quotients4(const float* x, float mn, float s, float y, float (&q)[4]) {
   float d[4];
@@ -177,7 +183,7 @@ __device__ __forceinline__ void chain_quotients4(const float* x, float mn, float
   src_round2<SRC>(d[0], d[1]);
   src_round2<SRC>(d[2], d[3]);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) q[j] = div_rn(d[j], s, y);
+  for (int j = 0; j < 4; ++j) q[j] = SRC == kF32 ? div_rn(d[j], s, y) : d[j] * y;
   src_round2<SRC>(q[0], q[1]);
   src_round2<SRC>(q[2], q[3]);
 }
