@@ -8,7 +8,8 @@
  * d >= 0 and s >= SMIN (the smallest scale the eps clamp of the group range allows) with d / s < 256,
  * this program checks that rint(round_src(RN(d * y))) == rint(round_src(RN(d / s))), and, as a control,
  * that the product alone is not always equal to the quotient before rounding (the check would be vacuous
- * otherwise).  Prints "ok <pairs> <differing products>" and exits 0, or the first counterexamples.
+ * otherwise).  Prints "ok <dtype> <pairs> <differing products>" per dtype and exits 0, or the first
+ * counterexamples.
  * Built by tests/test_chain_quotient.py with clang (for _Float16) and -ffp-contract=off.
  */
 #include <math.h>
