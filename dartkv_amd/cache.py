@@ -240,6 +240,7 @@ class DartKVCache:
         self._tail_count_dev: Optional[torch.Tensor] = None  # held tail length on the device (graph replay)
         self._finite_scope: Optional[_FiniteScope] = None
         self._copy_queue: Optional[list] = None  # an append's dense token copies, launched once at its end
+        self._tail_job: Optional[tuple] = None  # _tail_copy_job of the current tail buffers
         self._tail_desc = None  # (tail tensors' addresses and strides, their descriptor without a token count)
         self._sealed_pairs_cache: Optional[Tuple[int, list]] = None
         self._directory_cache: dict = {}
@@ -663,8 +664,18 @@ class DartKVCache:
                 or total > tk.shape[2] or (total - c.local_tokens) >= c.page_size):
             return False
         tv = self._tail_value
-        torch._foreach_copy_((tk.narrow(2, pending, n), tv.narrow(2, pending, n)),
-                             (key_states.detach(), value_states.detach()))
+        job = self._tail_job
+        if job is None or job[0] is not tk or job[1] is not tv:
+            job = self._tail_job = _tail_copy_job(tk, tv)
+        _, _, blocks, kb, vb, e, st, kbase, vbase = job
+        kb.src, kb.dst, kb.T = key_states.data_ptr(), kbase + pending * st, n
+        vb.src, vb.dst, vb.T = value_states.data_ptr(), vbase + pending * st, n
+        sb, sh, s_t, _ = key_states.stride()
+        kb.src_sb, kb.src_sh, kb.src_st = sb * e, sh * e, s_t * e
+        sb, sh, s_t, _ = value_states.stride()
+        vb.src_sb, vb.src_sh, vb.src_st = sb * e, sh * e, s_t * e
+        _lib.check(_lib.load().dkv_copy_token_blocks(blocks, 2, _lib.stream_ptr(self._device)),
+                   "dkv_copy_token_blocks")
         self._pending_key = tk.narrow(2, 0, total)
         self._pending_value = tv.narrow(2, 0, total)
         self._seen_tokens += n
@@ -1142,6 +1153,20 @@ def _run_fields(segments: list, names: tuple, page_major: bool) -> list:
         # [B, H, n * rows, ...] -> [n, B, H, rows, ...]
         return [pool.field(name, first._at, n * step).unflatten(2, (n, step)).movedim(2, 0) for name in names]
     return [torch.stack([getattr(s, name) for s in segments], 0) for name in names]
+
+
+def _tail_copy_job(tk: torch.Tensor, tv: torch.Tensor) -> tuple:
+    """A two-block dkv_copy_token_blocks description that writes tokens into the tail buffers ``tk`` and
+    ``tv`` ([B, H, capacity, D], one dtype): (tk, tv, blocks, key block, value block, element size, token
+    stride in bytes, tk address, tv address).  Per call only the sources, the first row and the token
+    count change."""
+    blocks = (_lib.CopyBlock * 2)()
+    e = tk.element_size()
+    for blk, t in zip(blocks, (tk, tv)):
+        blk.B, blk.H, _, D = t.shape
+        blk.row_bytes = D * e
+        blk.dst_sb, blk.dst_sh, blk.dst_st = t.stride(0) * e, t.stride(1) * e, t.stride(2) * e
+    return (tk, tv, blocks, blocks[0], blocks[1], e, tk.stride(2) * e, tk.data_ptr(), tv.data_ptr())
 
 
 def _value_rows_job(src: torch.Tensor, bits: int, group: int, meta: torch.dtype, pool: Optional[PagePool],
