@@ -296,13 +296,57 @@ __global__ void __launch_bounds__(64 * kDenseMergeWaves, MG <= 4 ? 4 : 2) decode
               [] __device__() { __syncthreads(); });
 }
 
-// One block per (batch, query head): the merge alone.
+// One block per (batch, query head): the merge alone.  With at most
+// kMergeRegSplits records per query head, each channel's thread issues the
+// loads of all its records before the weights are known, and wave 0 forms the
+// weights (a wave maximum, then the split sums added in split order), so the
+// kernel waits on one round of loads instead of two; every sum runs in
+// merge_heads' order, so the results are the same bits.
+constexpr int kMergeRegSplits = 32;
+
 __global__ void __launch_bounds__(kThreads) decode_merge(DecodeParams p) {
   extern __shared__ float wsh[];  // [S] weights, [S] sums
   __shared__ float mx[1], den[1];
   const int bq = blockIdx.x;  // b * Hq + hq
-  merge_heads(p, bq / (int)p.a.Hq, bq % (int)p.a.Hq, 1, wsh, wsh + p.split_stride, mx, den, (int)threadIdx.x,
-              (int)blockDim.x, [] __device__() { __syncthreads(); });
+  const dkv_decode_args& a = p.a;
+  const int S = p.split_stride, D = (int)a.D, tid = (int)threadIdx.x;
+  if (S > kMergeRegSplits || D > kThreads) {
+    merge_heads(p, bq / (int)a.Hq, bq % (int)a.Hq, 1, wsh, wsh + S, mx, den, tid, (int)blockDim.x,
+                [] __device__() { __syncthreads(); });
+    return;
+  }
+  const float* ws = (const float*)a.workspace + (int64_t)bq * S * (D + 2);
+  float r[kMergeRegSplits];
+  if (tid < D) {
+#pragma unroll
+    for (int s = 0; s < kMergeRegSplits; ++s) r[s] = s < S ? ws[(int64_t)s * (D + 2) + 2 + tid] : 0.f;
+  }
+  if (tid < 64) {
+    const float m = tid < S ? ws[(int64_t)tid * (D + 2)] : -INFINITY;
+    const float l = tid < S ? ws[(int64_t)tid * (D + 2) + 1] : 0.f;
+    float M = m;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    const float w = m == -INFINITY ? 0.f : expf(m - M);
+    if (tid < S) wsh[tid] = w;
+    const float lw = l * w;
+    float L = 0.f;
+    for (int s = 0; s < S; ++s) L += __shfl(lw, s, 64);
+    if (tid == 0) den[0] = fmaxf(L, 1e-20f);
+  }
+  __syncthreads();
+  if (tid < D) {
+    float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMergeRegSplits; s += 2) {
+      if (s < S) o0 += r[s] * wsh[s];
+      if (s + 1 < S) o1 += r[s + 1] * wsh[s + 1];
+    }
+    const float o = (o0 + o1) / den[0];
+    const int b = bq / (int)a.Hq, hq = bq % (int)a.Hq;
+    dev_store(a.out, (int64_t)b * a.out_sb + (int64_t)hq * a.out_sh + tid, o, (int)a.q_dtype);
+    if (a.out_f32) a.out_f32[(int64_t)bq * D + tid] = o;
+  }
 }
 
 }  // namespace
