@@ -15,7 +15,7 @@ from __future__ import annotations
 import ctypes
 import math
 import os
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -162,7 +162,8 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     plan = cache.decode_plan(query.device)
     tail = tail_segment(cache) if plan.tail_is_pending else _lib.Segment()
     Hq = q3.shape[1]
-    use_fast = (_fast_enabled() if fast is None else fast) and plan.fast_count > 0 and Hq // kv_heads in (1, 2, 4)
+    use_fast = ((_fast_enabled() if fast is None else fast) and plan.fast_count > 0
+                and Hq // kv_heads in _fast_rows(plan))
     dense_ok = tail.tokens == 0 or _dense16_ok(tail)
     chunks = -(-max(plan.rest_dense, tail.tokens) // 32)
     key = (Hq, q3.dtype, q3.stride(0), q3.stride(1), use_fast, n_splits, factor, static_scratch, tail.tokens > 0,
@@ -249,6 +250,12 @@ def segment_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optiona
     return out.to(query.dtype)
 
 
+def _fast_rows(plan) -> Tuple[int, ...]:
+    """Query rows per KV head the MFMA page kernel takes for this plan's pages: 1, 2, 4, and 8 on Dart
+    (promoted) pages."""
+    return (1, 2, 4, 8) if plan.fast_promoted > 0 else (1, 2, 4)
+
+
 def _multi_token_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,
                            out_f32: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Several query tokens per head over the packed cache.
@@ -258,13 +265,16 @@ def _multi_token_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Op
     row of h's KV group.  A [B, Hq, c, D] slice of the query read as a
     [B, Hq * c, D] query keeps that grouping (row h * c + i belongs to KV head
     h // G), and the single-token HIP decode path runs it unchanged: the MFMA
-    page kernel while G * c <= 4 rows per KV head, the general kernel up to 16.
-    ``out_f32`` ([B, Hq, Q, D] float32) receives the result before the cast.
+    page kernel while G * c fits its rows per KV head (4, or 8 on Dart pages:
+    the dequantized pages serve all rows of a launch), the general kernel up to
+    16.  ``out_f32`` ([B, Hq, Q, D] float32) receives the result before the cast.
     """
     batch, kv_heads, head_dim = cache.shape[0], cache.shape[1], cache.shape[3]
     Hq, Q = query.shape[1], query.shape[-2]
     groups = Hq // kv_heads
-    chunk = max(1, 4 // groups) if groups <= 4 else max(1, 16 // groups)
+    plan = cache.decode_plan(query.device)
+    rows = max(_fast_rows(plan)) if plan.fast_count > 0 and _fast_enabled() else 4
+    chunk = max(1, rows // groups) if groups <= rows else max(1, 16 // groups)
     if out_f32 is not None and (out_f32.shape != (batch, Hq, Q, head_dim) or out_f32.dtype != torch.float32):
         raise ValueError("out_f32 must be a float32 [B, Hq, Q, D] tensor")
     out = torch.empty(batch, Hq, Q, head_dim, dtype=query.dtype, device=query.device)

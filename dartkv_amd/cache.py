@@ -509,6 +509,7 @@ class DartKVCache:
         if self._pending_value is not None:
             self._pending_value = self._pending_value.to(target)
         self._tail_key = self._tail_value = None
+        self._tail_job = None
         self._tail_count_dev = None
         self._device = target
         self._layout_version += 1
@@ -521,6 +522,7 @@ class DartKVCache:
         self._pending_key = self._pending_value = None
         self._key_pool = self._value_pool = None
         self._tail_key = self._tail_value = None
+        self._tail_job = None
         self._shape = None
         self._dtype = None
         self._device = None
@@ -561,6 +563,7 @@ class DartKVCache:
             else:
                 self._tail_key = self._tail_key.index_select(0, index)
                 self._tail_value = self._tail_value.index_select(0, index)
+                self._tail_job = None
         if in_tail:
             n = self._pending_key.shape[-2]
             self._pending_key, self._pending_value = self._tail_key[..., :n, :], self._tail_value[..., :n, :]

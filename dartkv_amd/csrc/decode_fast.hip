@@ -3,8 +3,11 @@
 // Scope: head_dim 128, 128-token pages, keys with Dart promotion (2-bit codes
 // for every channel plus the upper 2 bits of NP promoted channels, one key
 // group per page), 2-bit values with groups of vg (16 | vg, vg | 128)
-// channels, fp16 metadata, bf16 or fp16 cache, up to 4 query heads per KV
-// head.  Everything else goes through the general kernel (decode.hip).
+// channels, fp16 metadata, bf16 or fp16 cache, 1, 2, 4 or 8 query rows per KV
+// head (8 rows: two row groups of 4, each with its own Q K MFMAs on the same
+// dequantized B operands; the multi-token path maps two tokens of a
+// 4-head group here).  Everything else goes through the general kernel
+// (decode.hip).
 //
 // One wave owns one split: a contiguous range of pages of one (batch, kv
 // head).  Per page the wave
@@ -57,7 +60,11 @@ struct LdsMap {
   int kl, vc, kh, ki, ks, kz, vs, vz, klut, klut16, vlut, pidx, q16, qp, pt, zero, bytes;
 };
 
-__host__ __device__ inline LdsMap lds_map(int np, int gv) {
+// rg: row groups of 4 query rows (1, or 2 for 8 rows per KV head).  With two,
+// the promoted channels' query rows live in the softmax-weight region (which
+// is free from the weights' last read in P V until the softmax writes them)
+// and the query takes 8 rows.
+__host__ __device__ inline LdsMap lds_map(int np, int gv, int rg) {
   LdsMap m;
   int o = 0;
   // Fields whose offsets depend only on NP come first, so they are
@@ -72,13 +79,16 @@ __host__ __device__ inline LdsMap lds_map(int np, int gv) {
   o = (o + 255) / 256 * 256;               // (the 4-bit tables are addressed by byte: 256-aligned)
   m.klut16 = o; o += np * 32;              // 4-bit key tables [NP][16] fp16
   m.pidx = o; o += 64;                     // promoted channels [NP] uint8 (a copy: ki is refilled early)
-  m.q16 = o; o += 1024;                    // query [4][128 ch] fp16
+  m.q16 = o; o += 1024 * rg;               // query [4 rg][128 ch] fp16
   // A-operand sources; row strides put the rows one read touches in distinct
   // banks, and the zero block 16 banks after an aligned row start.
   o = (o + 127) / 128 * 128;
-  m.qp = o; o += 4 * kQpStride;            // query of the promoted channels [4][NP] fp16
-  o = (o + 127) / 128 * 128;
-  m.pt = o; o += 4 * kPtStride;            // softmax weights [4][128 tok] fp16
+  if (rg == 1) {
+    m.qp = o; o += 4 * kQpStride;          // query of the promoted channels [4][NP] fp16
+    o = (o + 127) / 128 * 128;
+  }
+  m.pt = o; o += 4 * rg * kPtStride;       // softmax weights [4 rg][128 tok] fp16
+  if (rg != 1) m.qp = m.pt;                // [8][NP] fits: 8 kQpStride <= 8 kPtStride
   o = (o + 127) / 128 * 128 + 64;
   m.zero = o; o += 256;                    // zeros read by A-operand lanes without data
   o = (o + 15) / 16 * 16;
@@ -233,9 +243,13 @@ __device__ __forceinline__ void lut_block_operands(const uint32_t x[4], const ui
 }
 
 
-// GQ: query heads per KV head; NP: promoted channels (16, 32, 48 or 64);
-// BF16: cache dtype bf16 (else fp16).  All compile-time, so every block loop
-// unrolls with immediate offsets and the table builds carry no dtype tests.
+// GQ: query rows per KV head (1, 2, 4 or 8); NP: promoted channels (16, 32,
+// 48 or 64); BF16: cache dtype bf16 (else fp16).  All compile-time, so every
+// block loop unrolls with immediate offsets and the table builds carry no
+// dtype tests.  Rows come in RG groups of GH: each group has its own Q K
+// MFMAs (the slot layout holds 4 rows), with 8 rows the groups' A operands are
+// read from LDS (two register sets would not fit), and P V takes all rows in
+// one MFMA (rows 4g + i: lane group kq = g holds group g's outputs).
 template <int GQ, int NP, bool BF16>
 __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -246,8 +260,10 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   const int total_workers = p.B * p.Hkv * p.splits;
   constexpr int np = NP;
   constexpr bool bf16 = BF16;
+  constexpr int RG = GQ > 4 ? 2 : 1, GH = GQ > 4 ? 4 : GQ;
+  static_assert(GQ == 1 || GQ == 2 || GQ == 4 || GQ == 8, "1, 2, 4 or 8 query rows per KV head");
   const int gv = p.gv;
-  const LdsMap M = lds_map(np, gv);
+  const LdsMap M = lds_map(np, gv, RG);
   uint8_t* lds = smem + wave * M.bytes;
   if (worker >= total_workers) {  // a dense-rest worker, or none
     dense_worker<GQ, BF16>(p, worker - total_workers, lane, (float*)lds);
@@ -263,11 +279,17 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   // ---- per-lane constants ----
   const int sh = 2 * (n & 3);             // bit offset of this lane's codes in each byte
   const int qd = 8 * (n >> 2);            // byte offset of this lane's two code dwords in a 32-byte row
-  const int slot = n >> 2, head = n & 3;  // slot-layout A row n = 4 * slot + head
-  int aq[4];                              // promoted-query A sources (row at the lane's slot, else zeros)
+  const int slot = n >> 2, head = n & 3;  // slot-layout A row n = 4 * slot + head (row 4g + head of group g)
+  int aq[RG][4];                          // promoted-query A sources (row at the lane's slot, else zeros)
+  int qsrc[RG][4];                        // with 8 rows: the Q K A sources, read per MFMA
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    aq[i] = (i == slot && head < GQ) ? M.qp + kQpStride * head + 2 * kq : M.zero + 2 * kq;
+  for (int g = 0; g < RG; ++g) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      aq[g][i] = (i == slot && head < GH) ? M.qp + kQpStride * (4 * g + head) + 2 * kq : M.zero + 2 * kq;
+      qsrc[g][i] = i == slot ? M.q16 + 2 * ((4 * g + head) * kD + kq) : M.zero + 2 * kq;
+    }
+  }
   // P V A source (heads in rows): weights of head n, or zeros
   const int apv = n < GQ ? M.pt + kPtStride * n + 8 * kq : M.zero + 8 * kq;
   // P V block blk, K index 4kq + m is token 16 blk + kq + 4m: the four lane
@@ -278,14 +300,17 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   const int vcode = M.vc + 32 * kq + 2 * n;                           // value codes of the lane's channels
 
   // ---- running state ----
-  // S (slot layout): lane (n, kq) holds heads 0..3 of tokens 32(n/4) + 16t + 4kq + n%4.
-  // O (heads in rows): lanes kq = 0 hold heads 0..3 of channels 8n + j in O[j].
-  float m_run[4], l_part[4];
+  // S (slot layout): lane (n, kq) holds rows 4g + 0..3 of tokens 32(n/4) + 16t + 4kq + n%4 in S[g][t].
+  // O (rows in rows): lanes kq = g hold rows 4g + 0..3 of channels 8n + j in O[j].
+  float m_run[RG][4], l_part[RG][4];
   float4v O[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m_run[i] = -INFINITY;
-    l_part[i] = 0.f;
+  for (int g = 0; g < RG; ++g) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      m_run[g][i] = -INFINITY;
+      l_part[g][i] = 0.f;
+    }
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) O[j] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -293,22 +318,23 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   int qexp;  // the query's power-of-two scale (query_exponent)
   {
     uint16_t* q16 = (uint16_t*)(lds + M.q16);
-    float qv[4 * kD / 64];
+    float qv[4 * RG * kD / 64];
     dev_load_n(p.query, p.q_dtype, qv, [&](int r) -> int64_t {
       const int i = lane + 64 * r, h = i / kD, c = i % kD;
       return h < GQ ? (int64_t)b * p.q_sb + (int64_t)(kvh * GQ + h) * p.q_sh + c : -1;
     });
     qexp = query_exponent(qv);
 #pragma unroll
-    for (int r = 0; r < 4 * kD / 64; ++r)
+    for (int r = 0; r < 4 * RG * kD / 64; ++r)
       q16[lane + 64 * r] = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(qv[r], -qexp));
     *(uint32_t*)(lds + M.zero + 4 * lane) = 0u;
   }
   lds_sync();
   // Q K A operands for channel blocks cb = 0..31 (natural channel order), kept
-  // in registers for the whole split: q[head][4cb + kq] at half `slot`.
-  half4 qa[kD / 4];
-  {
+  // in registers for the whole split: q[head][4cb + kq] at half `slot` (with
+  // one row group; with two they are read from q16 per MFMA, qsrc).
+  half4 qa[RG == 1 ? kD / 4 : 1];
+  if constexpr (RG == 1) {
     const uint16_t* q16 = (const uint16_t*)(lds + M.q16);
 #pragma unroll
     for (int cb = 0; cb < kD / 4; ++cb) {
@@ -358,8 +384,9 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
     lds_sync();
 
     // ---- S = Q K; tile t covers tokens 32(n/4) + 16t + 4 slot + n%4 ----
-    float4v S[2];
-    S[0] = S[1] = float4v{0.f, 0.f, 0.f, 0.f};
+    float4v S[RG][2];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) S[g][0] = S[g][1] = float4v{0.f, 0.f, 0.f, 0.f};
     // 2-bit codes of every channel (promoted channels have zero tables), one
     // pair of channel blocks (2u, 2u + 1) per step: each block's code dwords of
     // both tiles are one 8-byte read and the pair's tables one 16-byte read;
@@ -386,8 +413,17 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
         const half4 b1e = lookup4((wc[2 * u].y >> sh) & 0x03030303u, t[u].x, t[u].y);
         const half4 b0o = lookup4((wc[2 * u + 1].x >> sh) & 0x03030303u, t[u].z, t[u].w);
         const half4 b1o = lookup4((wc[2 * u + 1].y >> sh) & 0x03030303u, t[u].z, t[u].w);
-        S[0] = mma2(qa[2 * u], qa[2 * u + 1], b0e, b0o, S[0]);
-        S[1] = mma2(qa[2 * u], qa[2 * u + 1], b1e, b1o, S[1]);
+        if constexpr (RG == 1) {
+          S[0][0] = mma2(qa[2 * u], qa[2 * u + 1], b0e, b0o, S[0][0]);
+          S[0][1] = mma2(qa[2 * u], qa[2 * u + 1], b1e, b1o, S[0][1]);
+        } else {
+#pragma unroll
+          for (int g = 0; g < RG; ++g) {
+            const half4 a0 = load_a(lds, qsrc[g], 16 * u), a1 = load_a(lds, qsrc[g], 16 * u + 8);
+            S[g][0] = mma2(a0, a1, b0e, b0o, S[g][0]);
+            S[g][1] = mma2(a0, a1, b1e, b1o, S[g][1]);
+          }
+        }
         if (u % 2 == 0 && u / 2 < 4) {
           // value table k = u / 2 of this lane: token lane + 64 (k & 1), group k >> 1
           // (groups beyond gv rebuild an existing table with identical contents)
@@ -429,18 +465,24 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
         wh[pb] = *(const uint2*)(lds + M.kh + 32 * j + qd);
       };
       load_pb(0);
-      half4 pa, pend0, pend1;  // even block's operands, waiting for the odd one (np / 4 is even)
+      half4 pa[RG], pend0, pend1;  // even block's operands, waiting for the odd one (np / 4 is even)
 #pragma unroll
       for (int pb = 0; pb < np / 4; ++pb) {
         if (pb + 1 < np / 4) load_pb(pb + 1);
-        const half4 a = load_a(lds, aq, 8 * pb);
+        half4 a[RG];
+#pragma unroll
+        for (int g = 0; g < RG; ++g) a[g] = load_a(lds, aq[g], 8 * pb);
         const half4 b0 = gather16(wl[pb].x, wh[pb].x, rl, rh, kq32, tab16, 128 * pb, m6, m18);
         const half4 b1 = gather16(wl[pb].y, wh[pb].y, rl, rh, kq32, tab16, 128 * pb, m6, m18);
         if (pb & 1) {
-          S[0] = mma2(pa, a, pend0, b0, S[0]);
-          S[1] = mma2(pa, a, pend1, b1, S[1]);
+#pragma unroll
+          for (int g = 0; g < RG; ++g) {
+            S[g][0] = mma2(pa[g], a[g], pend0, b0, S[g][0]);
+            S[g][1] = mma2(pa[g], a[g], pend1, b1, S[g][1]);
+          }
         } else {
-          pa = a;
+#pragma unroll
+          for (int g = 0; g < RG; ++g) pa[g] = a[g];
           pend0 = b0;
           pend1 = b1;
         }
@@ -454,35 +496,50 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
 
     // ---- online softmax in base 2 ----
     {
-      float x[2][4];
+      float x[RG][2][4];
       bool over = false;
 #pragma unroll
-      for (int i = 0; i < GQ; ++i) {
-        x[0][i] = S[0][i] * c2;
-        x[1][i] = S[1][i] * c2;
-        over |= fmaxf(x[0][i], x[1][i]) > m_run[i] + kSlack;
+      for (int g = 0; g < RG; ++g) {
+#pragma unroll
+        for (int i = 0; i < GH; ++i) {
+          x[g][0][i] = S[g][0][i] * c2;
+          x[g][1][i] = S[g][1][i] * c2;
+          over |= fmaxf(x[g][0][i], x[g][1][i]) > m_run[g][i] + kSlack;
+        }
       }
       if (__ballot(over) != 0ull) {
+        float alpha[RG][4];
 #pragma unroll
-        for (int i = 0; i < GQ; ++i) {
-          const float m_new = uniform(fmaxf(m_run[i], wave_max64(fmaxf(x[0][i], x[1][i]))));
-          const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_new);
+        for (int g = 0; g < RG; ++g) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) O[j][i] *= alpha;
-          l_part[i] *= alpha;
-          m_run[i] = m_new;
+          for (int i = 0; i < GH; ++i) {
+            const float m_new = uniform(fmaxf(m_run[g][i], wave_max64(fmaxf(x[g][0][i], x[g][1][i]))));
+            alpha[g][i] = __builtin_amdgcn_exp2f(m_run[g][i] - m_new);
+            l_part[g][i] *= alpha[g][i];
+            m_run[g][i] = m_new;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < GH; ++i) {
+          // O row 4g + i sits in lane group kq = g (rows past GQ are zero)
+          const float al = RG == 1 ? alpha[0][i] : (kq == 1 ? alpha[RG - 1][i] : alpha[0][i]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) O[j][i] *= al;
         }
       }
       uint16_t* pt = (uint16_t*)(lds + M.pt);
       const int tok = 32 * (n >> 2) + 4 * kq + (n & 3);  // tile 0; tile 1 is tok + 16
       const int wpos = kpos(tok);
 #pragma unroll
-      for (int i = 0; i < GQ; ++i) {
-        const float p0 = __builtin_amdgcn_exp2f(x[0][i] - m_run[i]);
-        const float p1 = __builtin_amdgcn_exp2f(x[1][i] - m_run[i]);
-        l_part[i] += p0 + p1;
-        pt[i * (kPtStride / 2) + wpos] = __builtin_bit_cast(uint16_t, (_Float16)p0);
-        pt[i * (kPtStride / 2) + wpos + 16] = __builtin_bit_cast(uint16_t, (_Float16)p1);
+      for (int g = 0; g < RG; ++g) {
+#pragma unroll
+        for (int i = 0; i < GH; ++i) {
+          const float p0 = __builtin_amdgcn_exp2f(x[g][0][i] - m_run[g][i]);
+          const float p1 = __builtin_amdgcn_exp2f(x[g][1][i] - m_run[g][i]);
+          l_part[g][i] += p0 + p1;
+          pt[(4 * g + i) * (kPtStride / 2) + wpos] = __builtin_bit_cast(uint16_t, (_Float16)p0);
+          pt[(4 * g + i) * (kPtStride / 2) + wpos + 16] = __builtin_bit_cast(uint16_t, (_Float16)p1);
+        }
       }
     }
     lds_sync();
@@ -529,17 +586,20 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
 
   // ---- partial state ----
 #pragma unroll
-  for (int i = 0; i < GQ; ++i) {
-    const float l = wave_sum64(l_part[i]);
-    const int hq = kvh * GQ + i;
-    float* rec = p.ws + (((int64_t)b * p.Hq + hq) * p.split_stride + split) * (kD + 2);
-    if (lane == 0) {
-      rec[0] = (tab16 & 255u) == 0 ? m_run[i] * kLn2 : NAN;
-      rec[1] = l;
-    }
-    if (kq == 0) {
+  for (int g = 0; g < RG; ++g) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) rec[2 + 8 * n + j] = O[j][i];
+    for (int i = 0; i < GH; ++i) {
+      const float l = wave_sum64(l_part[g][i]);
+      const int hq = kvh * GQ + 4 * g + i;
+      float* rec = p.ws + (((int64_t)b * p.Hq + hq) * p.split_stride + split) * (kD + 2);
+      if (lane == 0) {
+        rec[0] = (tab16 & 255u) == 0 ? m_run[g][i] * kLn2 : NAN;
+        rec[1] = l;
+      }
+      if (kq == g) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) rec[2 + 8 * n + j] = O[j][i];
+      }
     }
   }
 }
@@ -550,8 +610,9 @@ namespace dkv {
 
 int fast_decode_max_loads(int np, int gv) { return n_small_loads(np, gv) + n_key_loads(np); }
 
-size_t fast_decode_lds_bytes(int np, int gv) { return (size_t)kWaves * lds_map(np, gv).bytes; }
-size_t fast_decode_wave_lds_bytes(int np, int gv) { return (size_t)lds_map(np, gv).bytes; }
+size_t fast_decode_lds_bytes(int np, int gv, int gq) {
+  return (size_t)kWaves * lds_map(np, gv, gq > 4 ? 2 : 1).bytes;
+}
 
 int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, int vg, int splits, int split_stride,
                        hipStream_t stream, const FusedRest* fused) {
@@ -578,7 +639,7 @@ int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, i
   set_fused(p, fused);
   const int64_t workers = (int64_t)p.B * p.Hkv * splits + p.dense_workers;
   const unsigned blocks = (unsigned)((workers + kWaves - 1) / kWaves);
-  const size_t lds = fast_decode_lds_bytes(np, p.gv);
+  const size_t lds = fast_decode_lds_bytes(np, p.gv, p.GQ);
   const dim3 grid(blocks), block(256);
 #define DKV_FAST_LAUNCH(G, N)                                                                  \
   do {                                                                                         \
@@ -600,8 +661,9 @@ int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, i
     case 1: DKV_FAST_NP(1); break;
     case 2: DKV_FAST_NP(2); break;
     case 4: DKV_FAST_NP(4); break;
+    case 8: DKV_FAST_NP(8); break;
     default:
-      set_error("fast decode supports 1, 2 or 4 query heads per KV head");
+      set_error("fast decode supports 1, 2, 4 or 8 query rows per KV head");
       return DKV_ERR_UNSUPPORTED;
   }
 #undef DKV_FAST_NP

@@ -20,8 +20,7 @@ struct FusedRest {
 int fast_decode_max_loads(int np, int gv);
 
 // LDS bytes one fast-kernel workgroup needs, and one of its waves.
-size_t fast_decode_lds_bytes(int np, int gv);
-size_t fast_decode_wave_lds_bytes(int np, int gv);
+size_t fast_decode_lds_bytes(int np, int gv, int gq);
 
 // Launch the fast kernel over descriptor entries [first, first + count) of
 // a.segments (all full 128-token pages with the fast layout), writing splits

@@ -111,9 +111,11 @@ def _seg_fields(seg):
 
 
 @pytest.mark.parametrize("Hkv,Hq,Q,dtype", [
-    (8, 32, 3, torch.bfloat16),   # G 4: one token per launch (MFMA page kernel)
-    (4, 8, 5, torch.bfloat16),    # G 2: two tokens per launch
-    (4, 4, 4, torch.float16),     # G 1: four tokens per launch
+    (8, 32, 3, torch.bfloat16),   # G 4: two tokens per launch, then one (MFMA page kernel, 8 and 4 rows)
+    (8, 32, 4, torch.float16),    # G 4: two launches of two tokens
+    (4, 8, 5, torch.bfloat16),    # G 2: four tokens per launch, then one
+    (4, 4, 4, torch.float16),     # G 1: four tokens in one launch
+    (2, 16, 3, torch.bfloat16),   # G 8: one token per launch (8 rows)
     (2, 6, 2, torch.bfloat16),    # G 3: general kernel
 ])
 def test_multi_token_attention_vs_oracle(Hkv, Hq, Q, dtype):
@@ -281,17 +283,21 @@ def _oracle_and_cache(B, Hkv, Hq, T, dtype, seed, **over):
     return cache, q.to(DEV), ref32
 
 
-@pytest.mark.parametrize("B,Hkv,Hq,T,dtype,vg", [
-    (1, 8, 32, 1024, torch.bfloat16, 64),    # config 2
-    (3, 4, 16, 2000, torch.bfloat16, 64),
-    (2, 2, 4, 1500, torch.float16, 32),      # GQA 2, fp16 cache, value group 32
-    (2, 4, 4, 700, torch.bfloat16, 128),     # GQA 1, value group 128
+@pytest.mark.parametrize("B,Hkv,Hq,T,dtype,vg,ratio", [
+    (1, 8, 32, 1024, torch.bfloat16, 64, 0.25),    # config 2
+    (3, 4, 16, 2000, torch.bfloat16, 64, 0.25),
+    (2, 2, 4, 1500, torch.float16, 32, 0.25),      # GQA 2, fp16 cache, value group 32
+    (2, 4, 4, 700, torch.bfloat16, 128, 0.25),     # GQA 1, value group 128
+    (2, 4, 32, 1300, torch.bfloat16, 64, 0.25),    # GQA 8: two row groups
+    (1, 2, 16, 900, torch.float16, 32, 0.25),      # GQA 8, fp16 cache, value group 32
+    (1, 2, 16, 800, torch.bfloat16, 64, 0.5),      # GQA 8, 64 promoted channels
+    (2, 2, 16, 600, torch.bfloat16, 16, 0.125),    # GQA 8, 16 promoted channels, value group 16
 ])
-def test_fast_page_kernel_vs_oracle_and_general(B, Hkv, Hq, T, dtype, vg):
+def test_fast_page_kernel_vs_oracle_and_general(B, Hkv, Hq, T, dtype, vg, ratio):
     dart = _dkv()
-    cache, q, ref32 = _oracle_and_cache(B, Hkv, Hq, T, dtype, seed=7 + T, value_group_size=vg)
+    cache, q, ref32 = _oracle_and_cache(B, Hkv, Hq, T, dtype, seed=7 + T, value_group_size=vg, promote_ratio=ratio)
     plan = cache.decode_plan(q.device)
-    print("case", B, Hkv, Hq, T, dtype, vg, "fast pages", plan.fast_count, "of", plan.count, flush=True)
+    print("case", B, Hkv, Hq, T, dtype, vg, ratio, "fast pages", plan.fast_count, "of", plan.count, flush=True)
     assert plan.fast_count == (T - 32) // 128
     out_fast = torch.empty(B, Hq, 128, dtype=torch.float32, device=DEV)
     out_gen = torch.empty_like(out_fast)
