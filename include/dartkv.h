@@ -261,14 +261,16 @@ typedef struct dkv_segment {
  * head_dim 128, Dart keys with fast_promoted promoted channels (a multiple of
  * 16, at most 64, one key group per page), 2-bit values in groups of
  * fast_value_group channels (a multiple of 16 dividing 128), fp16 metadata and a
- * bf16 or fp16 cache, every field 16-byte aligned; the caller guarantees this.
+ * bf16 or fp16 cache, every field 16-byte aligned, and Hq / Hkv of 1, 2, 4
+ * or 8; the caller guarantees this (except the head ratio, which is checked).
  * Those pages are processed by the MFMA page kernel over `fast_splits` splits;
  * the other entries and the tail by the general kernel over `n_splits` splits.
  * With fast_promoted == 0 the run is instead uniform pages: keys quantized
  * with fast_key_bits bits along the tokens (one key group per page), values
  * with fast_value_bits bits along the channels in groups of fast_value_group
  * (2, 4 or 8 bits each), split over half pages (fast_splits at most
- * 2 * fast_count).  For Dart pages fast_key_bits and fast_value_bits are 0 or 2.
+ * 2 * fast_count) and Hq / Hkv of 1, 2 or 4.  For Dart pages fast_key_bits
+ * and fast_value_bits are 0 or 2.
  *
  * Dense rest: when rest_dense_tokens > 0 the caller guarantees that every entry
  * outside the fast range and the tail are dense segments in the cache dtype
