@@ -243,13 +243,27 @@ __device__ __forceinline__ void lut_block_operands(const uint32_t x[4], const ui
 }
 
 
+// Slot-layout A operand from its one non-zero value: v (16 bits) at half
+// `slot` of the four, zeros elsewhere, by two byte permutes with lane-constant
+// selectors (slot_sel; all zero bytes for a lane without a row).
+__device__ __forceinline__ half4 slot_a(uint32_t v, uint2 sel) {
+  return __builtin_bit_cast(half4, make_uint2(perm(0u, v, sel.x), perm(0u, v, sel.y)));
+}
+__device__ __forceinline__ uint2 slot_sel(int slot, bool row) {
+  const uint32_t z = 0x0c0c0c0cu, at_lo = 0x0c0c0100u, at_hi = 0x01000c0cu;  // 0x0c: a zero byte
+  if (!row) return make_uint2(z, z);
+  return make_uint2(slot == 0 ? at_lo : slot == 1 ? at_hi : z, slot == 2 ? at_lo : slot == 3 ? at_hi : z);
+}
+
 // GQ: query rows per KV head (1, 2, 4 or 8); NP: promoted channels (16, 32,
 // 48 or 64); BF16: cache dtype bf16 (else fp16).  All compile-time, so every
 // block loop unrolls with immediate offsets and the table builds carry no
 // dtype tests.  Rows come in RG groups of GH: each group has its own Q K
 // MFMAs (the slot layout holds 4 rows), with 8 rows the groups' A operands are
-// read from LDS (two register sets would not fit), and P V takes all rows in
-// one MFMA (rows 4g + i: lane group kq = g holds group g's outputs).
+// formed per MFMA from one 2-byte LDS read each (two register sets would not
+// fit; four reads per operand, three of zeros, stalled on LDS issue), and P V
+// takes all rows in one MFMA (rows 4g + i: lane group kq = g holds group g's
+// outputs).
 template <int GQ, int NP, bool BF16>
 __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -280,15 +294,18 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   const int sh = 2 * (n & 3);             // bit offset of this lane's codes in each byte
   const int qd = 8 * (n >> 2);            // byte offset of this lane's two code dwords in a 32-byte row
   const int slot = n >> 2, head = n & 3;  // slot-layout A row n = 4 * slot + head (row 4g + head of group g)
-  int aq[RG][4];                          // promoted-query A sources (row at the lane's slot, else zeros)
-  int qsrc[RG][4];                        // with 8 rows: the Q K A sources, read per MFMA
+  int aq[4];                              // one row group: promoted-query A sources (row at the lane's slot, else zeros)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    aq[i] = (i == slot && head < GH) ? M.qp + kQpStride * head + 2 * kq : M.zero + 2 * kq;
+  // two row groups: the non-zero A value's LDS address per group (query and
+  // promoted query), placed by slot_a
+  const uint2 asel = slot_sel(slot, true);
+  int qsrc[RG], psrc[RG];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      aq[g][i] = (i == slot && head < GH) ? M.qp + kQpStride * (4 * g + head) + 2 * kq : M.zero + 2 * kq;
-      qsrc[g][i] = i == slot ? M.q16 + 2 * ((4 * g + head) * kD + kq) : M.zero + 2 * kq;
-    }
+    qsrc[g] = M.q16 + 2 * ((4 * g + head) * kD + kq);
+    psrc[g] = M.qp + kQpStride * (4 * g + head) + 2 * kq;
   }
   // P V A source (heads in rows): weights of head n, or zeros
   const int apv = n < GQ ? M.pt + kPtStride * n + 8 * kq : M.zero + 8 * kq;
@@ -419,7 +436,8 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
         } else {
 #pragma unroll
           for (int g = 0; g < RG; ++g) {
-            const half4 a0 = load_a(lds, qsrc[g], 16 * u), a1 = load_a(lds, qsrc[g], 16 * u + 8);
+            const half4 a0 = slot_a(*(const uint16_t*)(lds + qsrc[g] + 16 * u), asel);
+            const half4 a1 = slot_a(*(const uint16_t*)(lds + qsrc[g] + 16 * u + 8), asel);
             S[g][0] = mma2(a0, a1, b0e, b0o, S[g][0]);
             S[g][1] = mma2(a0, a1, b1e, b1o, S[g][1]);
           }
@@ -470,8 +488,12 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
       for (int pb = 0; pb < np / 4; ++pb) {
         if (pb + 1 < np / 4) load_pb(pb + 1);
         half4 a[RG];
+        if constexpr (RG == 1) {
+          a[0] = load_a(lds, aq, 8 * pb);
+        } else {
 #pragma unroll
-        for (int g = 0; g < RG; ++g) a[g] = load_a(lds, aq[g], 8 * pb);
+          for (int g = 0; g < RG; ++g) a[g] = slot_a(*(const uint16_t*)(lds + psrc[g] + 8 * pb), asel);
+        }
         const half4 b0 = gather16(wl[pb].x, wh[pb].x, rl, rh, kq32, tab16, 128 * pb, m6, m18);
         const half4 b1 = gather16(wl[pb].y, wh[pb].y, rl, rh, kq32, tab16, 128 * pb, m6, m18);
         if (pb & 1) {
