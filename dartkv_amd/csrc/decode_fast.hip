@@ -261,9 +261,9 @@ __device__ __forceinline__ uint2 slot_sel(int slot, bool row) {
 // dtype tests.  Rows come in RG groups of GH: each group has its own Q K
 // MFMAs (the slot layout holds 4 rows), with 8 rows the groups' A operands are
 // formed per MFMA from one 2-byte LDS read each (two register sets would not
-// fit; four reads per operand, three of zeros, stalled on LDS issue), and P V
-// takes all rows in one MFMA (rows 4g + i: lane group kq = g holds group g's
-// outputs).
+// fit; four reads per operand, three of zeros, stalled on LDS issue), as are
+// the promoted pass's for any row count, and P V takes all rows in one MFMA
+// (rows 4g + i: lane group kq = g holds group g's outputs).
 template <int GQ, int NP, bool BF16>
 __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -294,13 +294,9 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
   const int sh = 2 * (n & 3);             // bit offset of this lane's codes in each byte
   const int qd = 8 * (n >> 2);            // byte offset of this lane's two code dwords in a 32-byte row
   const int slot = n >> 2, head = n & 3;  // slot-layout A row n = 4 * slot + head (row 4g + head of group g)
-  int aq[4];                              // one row group: promoted-query A sources (row at the lane's slot, else zeros)
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    aq[i] = (i == slot && head < GH) ? M.qp + kQpStride * head + 2 * kq : M.zero + 2 * kq;
-  // two row groups: the non-zero A value's LDS address per group (query and
-  // promoted query), placed by slot_a
-  const uint2 asel = slot_sel(slot, true);
+  // the non-zero A value's LDS address per row group (query and promoted
+  // query), placed by slot_a; lanes of rows past GQ get zero operands
+  const uint2 asel = slot_sel(slot, head < GH);
   int qsrc[RG], psrc[RG];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
@@ -488,12 +484,8 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
       for (int pb = 0; pb < np / 4; ++pb) {
         if (pb + 1 < np / 4) load_pb(pb + 1);
         half4 a[RG];
-        if constexpr (RG == 1) {
-          a[0] = load_a(lds, aq, 8 * pb);
-        } else {
 #pragma unroll
-          for (int g = 0; g < RG; ++g) a[g] = slot_a(*(const uint16_t*)(lds + psrc[g] + 8 * pb), asel);
-        }
+        for (int g = 0; g < RG; ++g) a[g] = slot_a(*(const uint16_t*)(lds + psrc[g] + 8 * pb), asel);
         const half4 b0 = gather16(wl[pb].x, wh[pb].x, rl, rh, kq32, tab16, 128 * pb, m6, m18);
         const half4 b1 = gather16(wl[pb].y, wh[pb].y, rl, rh, kq32, tab16, 128 * pb, m6, m18);
         if (pb & 1) {
