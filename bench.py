@@ -483,6 +483,7 @@ def main() -> int:
     p.add_argument("--c4-only", action="store_true", help="run only the C4 leg and print its JSON")
     p.add_argument("--c2-only", action="store_true", help="run only the config-2 latency leg and print its JSON")
     p.add_argument("--no-c5-4b", action="store_true", help="skip the C5 4-bit uniform sub-leg of the 2b25 run")
+    p.add_argument("--no-multi-token", action="store_true", help="skip the multi-token / GQA-8 sub-leg of the C5 run")
     p.add_argument("--c4-steps", type=int, default=128)
     p.add_argument("--c4-prompt", type=int, default=8192)
     p.add_argument("--c4-eager", action="store_true", help="C4 without HIP graph capture of the decode step")
@@ -558,6 +559,7 @@ def main() -> int:
         "hbm_frac": c5["hbm_frac"],
         "decode_tok_s": c5["decode_tok_s"],
         "c5_4b": c5_4b,
+        "multi_token": c5["multi_token"],
         "c2_latency_us": None if c2 is None else c2["call_us"],
         "c2": c2,
         "prefill_c3": prefill,
@@ -609,6 +611,14 @@ def time_c5(args, bits: str, torch, dart, synthetic, stream) -> dict:
     # records around its launch on the decode stream
     plan = caches[0].decode_plan(torch.device("cuda:0"))
     fast_bytes = args.batch * args.kv_heads * plan.fast_count * page_bytes(args.head_dim, cfg)
+    if plan.fast_count and plan.rest_dense >= 0:
+        # every entry outside the page run is dense (the sink and the held tail): the page kernel's launch
+        # attends to them too (one wave per 32-token chunk), so their K/V bytes and the query are that
+        # launch's as well; the merge launch writes the output
+        sink = min(cfg["sink_tokens"], args.context)
+        tail = (args.context - sink) % cfg["page_size"]
+        fast_bytes += (args.batch * args.kv_heads * (sink + tail) * args.head_dim * 2 * 2
+                       + args.batch * args.q_heads * args.head_dim * 2)
     n = args.layers * args.steps
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
     for e0, e1 in events:  # create the handles before they go to the library
@@ -637,6 +647,7 @@ def time_c5(args, bits: str, torch, dart, synthetic, stream) -> dict:
     achieved = fast_bytes / (avg_kernel_ms * 1e-3) / 1e9 if avg_kernel_ms else None
     kernel = "decode_pages_fast" if plan.fast_promoted else "decode_pages_uniform"
     tok_s = args.batch / (ms_per_step * 1e-3)
+    multi = multi_token_leg(torch, dart, caches, a) if bits == "2b25" and not args.no_multi_token else None
     del caches, queries, step, events, plan
     torch.cuda.empty_cache()
     return {
@@ -658,7 +669,41 @@ def time_c5(args, bits: str, torch, dart, synthetic, stream) -> dict:
             "algorithmic_bytes_per_launch": fast_bytes,
             "avg_kernel_us": round(avg_kernel_ms * 1e3, 2),
         },
+        "multi_token": multi,
     }
+
+
+def multi_token_leg(torch, dart, caches, a, steps: int = 3) -> dict:
+    """Several query tokens per head over the resident C5 layer caches (fused_dart_attention with Q tokens:
+    each token one more query row of its KV group; the Dart page kernel takes 8 rows per KV head, so two
+    tokens of a GQA-4 group share each page read), and one token of a GQA-8 query (8 query heads per KV
+    head) over the same caches.  Microseconds per layer call (HIP events around `steps` passes over every
+    layer after one untimed pass) and the ratio to one token."""
+    gen = torch.Generator(device="cuda:0").manual_seed(11)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def per_call_us(queries) -> float:
+        for cache, q in zip(caches, queries):
+            dart.fused_dart_attention(q, cache)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            for cache, q in zip(caches, queries):
+                dart.fused_dart_attention(q, cache)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (steps * len(caches))
+
+    us = {}
+    for tokens in (1, 2, 4, 8):
+        us[tokens] = per_call_us([torch.randn(a.batch, a.q_heads, tokens, a.head_dim, generator=gen, device="cuda:0",
+                                              dtype=torch.bfloat16) for _ in caches])
+    gqa8 = per_call_us([torch.randn(a.batch, 8 * a.kv_heads, 1, a.head_dim, generator=gen, device="cuda:0",
+                                    dtype=torch.bfloat16) for _ in caches])
+    return {"workload": f"C5 caches, query tokens Q per head at GQA {a.q_heads // a.kv_heads}; one token at GQA 8",
+            "us_per_layer_call": {f"Q{t}": round(v, 1) for t, v in us.items()},
+            "ratio_to_Q1": {f"Q{t}": round(v / us[1], 3) for t, v in us.items()},
+            "gqa8_one_token_us": round(gqa8, 1)}
 
 
 
