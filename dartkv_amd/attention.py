@@ -251,9 +251,8 @@ def segment_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optiona
 
 
 def _fast_rows(plan) -> Tuple[int, ...]:
-    """Query rows per KV head the MFMA page kernel takes for this plan's pages: 1, 2, 4, and 8 on Dart
-    (promoted) pages."""
-    return (1, 2, 4, 8) if plan.fast_promoted > 0 else (1, 2, 4)
+    """Query rows per KV head the MFMA page kernels take (Dart and uniform pages alike)."""
+    return (1, 2, 4, 8)
 
 
 def _multi_token_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,

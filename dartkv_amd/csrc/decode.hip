@@ -490,8 +490,8 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
               "fast page range outside the descriptor table");
     DKV_CHECK(a.D == 128, DKV_ERR_UNSUPPORTED, "fast page path needs head_dim 128");
     const int64_t gq = a.Hq / a.Hkv;
-    DKV_CHECK(gq == 1 || gq == 2 || gq == 4 || (gq == 8 && a.fast_promoted > 0), DKV_ERR_UNSUPPORTED,
-              "fast page path needs 1, 2 or 4 query rows per KV head (8 on Dart pages)");
+    DKV_CHECK(gq == 1 || gq == 2 || gq == 4 || gq == 8, DKV_ERR_UNSUPPORTED,
+              "fast page path needs 1, 2, 4 or 8 query rows per KV head");
     DKV_CHECK(a.cache_dtype == dkv::kBF16 || a.cache_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED,
               "fast page path needs a bf16 or fp16 cache");
     DKV_CHECK(a.meta_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED, "fast page path needs fp16 metadata");

@@ -243,18 +243,6 @@ __device__ __forceinline__ void lut_block_operands(const uint32_t x[4], const ui
 }
 
 
-// Slot-layout A operand from its one non-zero value: v (16 bits) at half
-// `slot` of the four, zeros elsewhere, by two byte permutes with lane-constant
-// selectors (slot_sel; all zero bytes for a lane without a row).
-__device__ __forceinline__ half4 slot_a(uint32_t v, uint2 sel) {
-  return __builtin_bit_cast(half4, make_uint2(perm(0u, v, sel.x), perm(0u, v, sel.y)));
-}
-__device__ __forceinline__ uint2 slot_sel(int slot, bool row) {
-  const uint32_t z = 0x0c0c0c0cu, at_lo = 0x0c0c0100u, at_hi = 0x01000c0cu;  // 0x0c: a zero byte
-  if (!row) return make_uint2(z, z);
-  return make_uint2(slot == 0 ? at_lo : slot == 1 ? at_hi : z, slot == 2 ? at_lo : slot == 3 ? at_hi : z);
-}
-
 // GQ: query rows per KV head (1, 2, 4 or 8); NP: promoted channels (16, 32,
 // 48 or 64); BF16: cache dtype bf16 (else fp16).  All compile-time, so every
 // block loop unrolls with immediate offsets and the table builds carry no

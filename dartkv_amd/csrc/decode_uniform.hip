@@ -3,7 +3,9 @@
 // Scope: head_dim 128, 128-token pages, keys quantized uniformly with KB bits
 // along the tokens (one key group per page), values with VB bits along the
 // channels in groups of vg (16 | vg, vg | 128), KB, VB in {2, 4, 8}, fp16
-// metadata, bf16 or fp16 cache, up to 4 query heads per KV head.
+// metadata, bf16 or fp16 cache, 1, 2, 4 or 8 query rows per KV head (8: two
+// row groups of 4, each with its own Q K and P V MFMAs on the same
+// dequantized operands, the A operands formed from one LDS read each).
 //
 // Each wave owns a split: a contiguous range of half pages (64 tokens; half
 // page q is half q & 1 of page q >> 1) of one (batch, kv head).  It stages a
@@ -49,7 +51,8 @@ struct UMap {
 // keys; staging it per half would fetch the line again once L2 has dropped it.
 __host__ __device__ constexpr int key_rows_per_stage(int kb) { return kb <= 4 ? 2 : 1; }
 
-__host__ __device__ inline UMap umap(int kb, int vb, int gv) {
+// rg: row groups of 4 query rows (the query and the softmax weights take 4 rg rows).
+__host__ __device__ inline UMap umap(int kb, int vb, int gv, int rg) {
   UMap m;
   int o = 0;
   const int kf = key_rows_per_stage(kb);
@@ -61,9 +64,9 @@ __host__ __device__ inline UMap umap(int kb, int vb, int gv) {
   m.vz = o; o += 128 * gv;             // value zero  of the half [64 tok][Gv] fp16
   m.kt = o; o += kD * 8;               // key (s, s, z, z) per channel [128] (fp16 pairs)
   m.vt = o; o += kHalfTok * 8 * gv;    // value (s, s, z, z) of the half [64 tok][Gv]
-  m.q16 = o; o += 1024;                // query [4][128 ch] fp16 (split start only)
+  m.q16 = o; o += 1024 * rg;           // query [4 rg][128 ch] fp16 (split start only, and per MFMA with 2 groups)
   o = (o + 127) / 128 * 128;
-  m.pt = o; o += 4 * kPtRow;           // softmax weights [4][64 tok] fp16
+  m.pt = o; o += 4 * rg * kPtRow;      // softmax weights [4 rg][64 tok] fp16
   o = (o + 127) / 128 * 128 + 64;
   m.zero = o; o += 256;                // zeros read by A-operand lanes without data
   m.bytes = (o + 15) / 16 * 16;
@@ -149,13 +152,15 @@ __device__ __forceinline__ void build_sz_table(uint8_t* lds, int dst, int src_s,
 
 template <int GQ, int KB, int VB, bool BF16>
 __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
+  constexpr int RG = GQ > 4 ? 2 : 1, GH = GQ > 4 ? 4 : GQ;  // row groups of GH query rows
+  static_assert(GQ == 1 || GQ == 2 || GQ == 4 || GQ == 8, "1, 2, 4 or 8 query rows per KV head");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, kq = lane >> 4;
   const int worker = blockIdx.x * kWaves + wave;
   const int gv = p.gv;
-  const UMap M = umap(KB, VB, gv);
+  const UMap M = umap(KB, VB, gv, RG);
   uint8_t* lds = smem + wave * M.bytes;
   if (worker >= p.B * p.Hkv * p.splits) {  // a dense-rest worker, or none
     dense_worker<GQ, BF16>(p, worker - p.B * p.Hkv * p.splits, lane, (float*)lds);
@@ -177,39 +182,50 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
   const int vshift = VB * (n % vtpb);
   const int vch0 = code_index<VB>(n, 0);                   // first channel of the lane (tile 0)
   const int vg0 = vch0 / p.vg, vg1 = (vch0 + 64) / p.vg;   // value groups of tiles 0 and 1
-  int aq[4];  // P V A sources: the weight row of the lane's head at its slot, else zeros
+  int aq[4];  // one row group: P V A sources, the weight row of the lane's head at its slot, else zeros
 #pragma unroll
   for (int i = 0; i < 4; ++i) aq[i] = (i == slot && head < GQ) ? M.pt + kPtRow * head + 2 * kq : M.zero + 2 * kq;
+  // two row groups: the non-zero A value's LDS address per group (query, weights), placed by slot_a
+  const uint2 asel = slot_sel(slot, head < GH);
+  int qsrc[RG], wsrc[RG];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    qsrc[g] = M.q16 + 2 * ((4 * g + head) * kD + kq);
+    wsrc[g] = M.pt + kPtRow * (4 * g + head) + 2 * kq;
+  }
 
   // ---- running state ----
-  // S: lane (n, kq) holds heads 0..3 of half-page token code_index<KB>(n, kq).
-  // O[t]: lane (n, kq) holds heads 0..3 of channel 64 t + code_index<VB>(n, kq).
-  float m_run[4], l_part[4];
-  float4v O[2];
+  // S[g]: lane (n, kq) holds rows 4g + 0..3 of half-page token code_index<KB>(n, kq).
+  // O[g][t]: lane (n, kq) holds rows 4g + 0..3 of channel 64 t + code_index<VB>(n, kq).
+  float m_run[RG][4], l_part[RG][4];
+  float4v O[RG][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m_run[i] = -INFINITY;
-    l_part[i] = 0.f;
+  for (int g = 0; g < RG; ++g) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      m_run[g][i] = -INFINITY;
+      l_part[g][i] = 0.f;
+    }
+    O[g][0] = O[g][1] = float4v{0.f, 0.f, 0.f, 0.f};
   }
-  O[0] = O[1] = float4v{0.f, 0.f, 0.f, 0.f};
 
   int qexp;  // the query's power-of-two scale (query_exponent)
   {
     uint16_t* q16 = (uint16_t*)(lds + M.q16);
-    float qv[4 * kD / 64];
+    float qv[4 * RG * kD / 64];
     dev_load_n(p.query, p.q_dtype, qv, [&](int r) -> int64_t {
       const int i = lane + 64 * r, h = i / kD, c = i % kD;
       return h < GQ ? (int64_t)b * p.q_sb + (int64_t)(kvh * GQ + h) * p.q_sh + c : -1;
     });
     qexp = query_exponent(qv);
 #pragma unroll
-    for (int r = 0; r < 4 * kD / 64; ++r)
+    for (int r = 0; r < 4 * RG * kD / 64; ++r)
       q16[lane + 64 * r] = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(qv[r], -qexp));
     *(uint32_t*)(lds + M.zero + 4 * lane) = 0u;
   }
   lds_sync();
-  half4 qa[kD / 4];  // Q K A operands: q[head][4cb + kq] at half `slot`
-  {
+  half4 qa[RG == 1 ? kD / 4 : 1];  // one row group: Q K A operands, q[head][4cb + kq] at half `slot`
+  if constexpr (RG == 1) {
     const uint16_t* q16 = (const uint16_t*)(lds + M.q16);
 #pragma unroll
     for (int cb = 0; cb < kD / 4; ++cb) {
@@ -242,7 +258,9 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
     }
 
     // ---- S = Q K over the half's 64 tokens ----
-    float4v S = float4v{0.f, 0.f, 0.f, 0.f};
+    float4v S[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) S[g] = float4v{0.f, 0.f, 0.f, 0.f};
     {
       constexpr int kAhead = 2;
       uint32_t w[kD / 4];
@@ -260,8 +278,18 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
         if (cb + kAhead < kD / 4) load_cb(cb + kAhead);
         const uint32_t e = (w[cb] >> kshift) & kmask;
         const half4 b = dequant4<KB, BF16>(e, sz[cb]);
-        if (cb & 1) S = mma2(qa[cb - 1], qa[cb], pend, b, S);  // blocks cb - 1, cb in one K = 32 MFMA
-        else pend = b;
+        if (cb & 1) {  // blocks cb - 1, cb in one K = 32 MFMA
+          if constexpr (RG == 1) {
+            S[0] = mma2(qa[cb - 1], qa[cb], pend, b, S[0]);
+          } else {
+#pragma unroll
+            for (int g = 0; g < RG; ++g)
+              S[g] = mma2(slot_a(*(const uint16_t*)(lds + qsrc[g] + 8 * (cb - 1)), asel),
+                          slot_a(*(const uint16_t*)(lds + qsrc[g] + 8 * cb), asel), pend, b, S[g]);
+          }
+        } else {
+          pend = b;
+        }
       }
     }
     lds_sync();
@@ -272,43 +300,57 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
 
     // ---- online softmax in base 2 ----
     {
-      float x[4];
+      float x[RG][4];
       bool over = false;
 #pragma unroll
-      for (int i = 0; i < GQ; ++i) {
-        x[i] = S[i] * c2;
-        over |= x[i] > m_run[i] + kSlack;
+      for (int g = 0; g < RG; ++g) {
+#pragma unroll
+        for (int i = 0; i < GH; ++i) {
+          x[g][i] = S[g][i] * c2;
+          over |= x[g][i] > m_run[g][i] + kSlack;
+        }
       }
       if (__ballot(over) != 0ull) {
 #pragma unroll
-        for (int i = 0; i < GQ; ++i) {
-          const float m_new = uniform(fmaxf(m_run[i], wave_max64(x[i])));
-          const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_new);
-          O[0][i] *= alpha;
-          O[1][i] *= alpha;
-          l_part[i] *= alpha;
-          m_run[i] = m_new;
+        for (int g = 0; g < RG; ++g) {
+#pragma unroll
+          for (int i = 0; i < GH; ++i) {
+            const float m_new = uniform(fmaxf(m_run[g][i], wave_max64(x[g][i])));
+            const float alpha = __builtin_amdgcn_exp2f(m_run[g][i] - m_new);
+            O[g][0][i] *= alpha;
+            O[g][1][i] *= alpha;
+            l_part[g][i] *= alpha;
+            m_run[g][i] = m_new;
+          }
         }
       }
       uint16_t* pt = (uint16_t*)(lds + M.pt);
       const int tok = code_index<KB>(n, kq);
 #pragma unroll
-      for (int i = 0; i < GQ; ++i) {
-        const float pv = __builtin_amdgcn_exp2f(x[i] - m_run[i]);
-        l_part[i] += pv;
-        pt[i * (kPtRow / 2) + tok] = __builtin_bit_cast(uint16_t, (_Float16)pv);
+      for (int g = 0; g < RG; ++g) {
+#pragma unroll
+        for (int i = 0; i < GH; ++i) {
+          const float pv = __builtin_amdgcn_exp2f(x[g][i] - m_run[g][i]);
+          l_part[g][i] += pv;
+          pt[(4 * g + i) * (kPtRow / 2) + tok] = __builtin_bit_cast(uint16_t, (_Float16)pv);
+        }
       }
     }
     lds_sync();
 
     // ---- O += P V: token group tg = tokens 4 tg .. 4 tg + 3, lane's token 4 tg + kq ----
     {
-      half4 a[kHalfTok / 4];
+      half4 a[RG][kHalfTok / 4];
       uint32_t w0[kHalfTok / 4], w1[kHalfTok / 4];
       uint2 sz0[kHalfTok / 4], sz1[kHalfTok / 4];
       auto load_tg = [&](int tg) {
         const int t = 4 * tg + kq;
-        a[tg] = load_a(lds, aq, 8 * tg);
+        if constexpr (RG == 1) {
+          a[0][tg] = load_a(lds, aq, 8 * tg);
+        } else {
+#pragma unroll
+          for (int g = 0; g < RG; ++g) a[g][tg] = slot_a(*(const uint16_t*)(lds + wsrc[g] + 8 * tg), asel);
+        }
         w0[tg] = lds_u32(lds, M.vc + 16 * VB * t + vdw);
         w1[tg] = lds_u32(lds, M.vc + 16 * VB * t + 8 * VB + vdw);
         sz0[tg] = *(const uint2*)(lds + M.vt + 8 * (t * gv + vg0));
@@ -322,8 +364,11 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
         const half4 b0 = dequant4<VB, BF16>((w0[tg] >> vshift) & vmask, sz0[tg]);
         const half4 b1 = dequant4<VB, BF16>((w1[tg] >> vshift) & vmask, sz1[tg]);
         if (tg & 1) {  // token groups tg - 1, tg in one K = 32 MFMA per tile
-          O[0] = mma2(a[tg - 1], a[tg], p0, b0, O[0]);
-          O[1] = mma2(a[tg - 1], a[tg], p1, b1, O[1]);
+#pragma unroll
+          for (int g = 0; g < RG; ++g) {
+            O[g][0] = mma2(a[g][tg - 1], a[g][tg], p0, b0, O[g][0]);
+            O[g][1] = mma2(a[g][tg - 1], a[g][tg], p1, b1, O[g][1]);
+          }
         } else {
           p0 = b0;
           p1 = b1;
@@ -337,16 +382,19 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
   // ---- partial state ----
   const int ch = code_index<VB>(n, kq);
 #pragma unroll
-  for (int i = 0; i < GQ; ++i) {
-    const float l = wave_sum64(l_part[i]);
-    const int hq = kvh * GQ + i;
-    float* rec = p.ws + (((int64_t)b * p.Hq + hq) * p.split_stride + split) * (kD + 2);
-    if (lane == 0) {
-      rec[0] = m_run[i] * kLn2;
-      rec[1] = l;
+  for (int g = 0; g < RG; ++g) {
+#pragma unroll
+    for (int i = 0; i < GH; ++i) {
+      const float l = wave_sum64(l_part[g][i]);
+      const int hq = kvh * GQ + 4 * g + i;
+      float* rec = p.ws + (((int64_t)b * p.Hq + hq) * p.split_stride + split) * (kD + 2);
+      if (lane == 0) {
+        rec[0] = m_run[g][i] * kLn2;
+        rec[1] = l;
+      }
+      rec[2 + ch] = O[g][0][i];
+      rec[2 + 64 + ch] = O[g][1][i];
     }
-    rec[2 + ch] = O[0][i];
-    rec[2 + 64 + ch] = O[1][i];
   }
 }
 
@@ -356,7 +404,7 @@ namespace dkv {
 
 // The kernel waits until at most one half page's key or value loads are in
 // flight; vm_wait takes counts below 16.
-size_t uniform_decode_wave_lds_bytes(int kb, int vb, int gv) { return (size_t)umap(kb, vb, gv).bytes; }
+size_t uniform_decode_wave_lds_bytes(int kb, int vb, int gv) { return (size_t)umap(kb, vb, gv, 1).bytes; }
 
 int uniform_decode_max_loads(int kb, int vb) {
   return n_key_loads_u(kb) > n_value_loads_u(vb) ? n_key_loads_u(kb) : n_value_loads_u(vb);
@@ -387,13 +435,13 @@ int launch_uniform_decode(const dkv_decode_args& a, int first, int count, int kb
   set_fused(p, fused);
   const int64_t workers = (int64_t)p.B * p.Hkv * splits + p.dense_workers;
   const dim3 grid((unsigned)((workers + kWaves - 1) / kWaves)), block(256);
-  const size_t lds = (size_t)kWaves * umap(kb, vb, p.gv).bytes;
+  const size_t lds = (size_t)kWaves * umap(kb, vb, p.gv, p.GQ > 4 ? 2 : 1).bytes;
   if ((kb != 2 && kb != 4 && kb != 8) || (vb != 2 && vb != 4 && vb != 8)) {
     set_error("uniform page decode supports 2, 4 and 8-bit codes");
     return DKV_ERR_UNSUPPORTED;
   }
-  if (p.GQ != 1 && p.GQ != 2 && p.GQ != 4) {
-    set_error("uniform page decode supports 1, 2 or 4 query heads per KV head");
+  if (p.GQ != 1 && p.GQ != 2 && p.GQ != 4 && p.GQ != 8) {
+    set_error("uniform page decode supports 1, 2, 4 or 8 query rows per KV head");
     return DKV_ERR_UNSUPPORTED;
   }
 #define DKV_U_LAUNCH(G, K, V)                                                                            \
@@ -416,7 +464,8 @@ int launch_uniform_decode(const dkv_decode_args& a, int first, int count, int kb
   switch (p.GQ) {
     case 1: DKV_U_K(1); break;
     case 2: DKV_U_K(2); break;
-    default: DKV_U_K(4); break;
+    case 4: DKV_U_K(4); break;
+    default: DKV_U_K(8); break;
   }
 #undef DKV_U_K
 #undef DKV_U_V

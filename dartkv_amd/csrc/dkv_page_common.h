@@ -207,6 +207,18 @@ __device__ __forceinline__ half4 load_a(const uint8_t* lds, const int a[4], int 
   return r;
 }
 
+// Slot-layout A operand from its one non-zero value: v (16 bits) at half
+// `slot` of the four, zeros elsewhere, by two byte permutes with lane-constant
+// selectors (slot_sel; all zero bytes for a lane without a row).
+__device__ __forceinline__ half4 slot_a(uint32_t v, uint2 sel) {
+  return __builtin_bit_cast(half4, make_uint2(perm(0u, v, sel.x), perm(0u, v, sel.y)));
+}
+__device__ __forceinline__ uint2 slot_sel(int slot, bool row) {
+  const uint32_t z = 0x0c0c0c0cu, at_lo = 0x0c0c0100u, at_hi = 0x01000c0cu;  // 0x0c: a zero byte
+  if (!row) return make_uint2(z, z);
+  return make_uint2(slot == 0 ? at_lo : slot == 1 ? at_hi : z, slot == 2 ? at_lo : slot == 3 ? at_hi : z);
+}
+
 __device__ __forceinline__ float wave_max64(float v) {
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

@@ -110,6 +110,37 @@ def _seg_fields(seg):
     return {"values": seg.values, "scale": seg.scale, "zero": seg.zero_point}
 
 
+@pytest.mark.parametrize("Hkv,Hq,Q,dtype,uniform", [
+    (8, 32, 3, torch.bfloat16, False),   # G 4: two tokens per launch, then one (MFMA page kernel, 8 and 4 rows)
+    (4, 16, 3, torch.bfloat16, True),    # G 4 on uniform 4-bit pages: two tokens, then one
+    (2, 4, 5, torch.float16, True),      # G 2 on uniform pages: four tokens, then one
+])
+def test_multi_token_attention_vs_oracle_by_page_kind(Hkv, Hq, Q, dtype, uniform):
+    """As below, on Dart pages and on uniform pages (promote ratio 0, 4-bit keys and values)."""
+    dart = _dkv()
+    from dartkv_amd.attention import _multi_token_attention
+    from oracle import dart_oracle as O
+    from dartkv_amd import synthetic
+    k, v, _ = synthetic.outlier_kv(2, Hkv, 700, 128, query_heads=Hq, dtype=dtype, seed=60 + Q)
+    cfg = dict(bits=4 if uniform else 2, page_size=128, key_group_size=128, value_group_size=64,
+               promote_ratio=0.0 if uniform else 0.25, sink_tokens=32, hold_partial_pages=True,
+               metadata_dtype=torch.float16)
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    oc.append(k, v)
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    cache.append(k.to(DEV), v.to(DEV))
+    assert cache.decode_plan(torch.device(DEV)).fast_count == (700 - 32) // 128
+    q = torch.randn(2, Hq, Q, 128, generator=torch.Generator().manual_seed(Q + 20)).to(dtype)
+    _, ref32 = O.streamed_attention(q, oc, return_fp32=True)
+    print("case", Hkv, Hq, Q, dtype, uniform, flush=True)
+    out32 = torch.empty(2, Hq, Q, 128, dtype=torch.float32, device=DEV)
+    _multi_token_attention(q.to(DEV), cache, out_f32=out32)
+    torch.cuda.synchronize()
+    err = rel_err(out32, ref32)
+    print("rel err", err, flush=True)
+    assert err <= tolerance(dtype)
+
+
 @pytest.mark.parametrize("Hkv,Hq,Q,dtype", [
     (8, 32, 3, torch.bfloat16),   # G 4: two tokens per launch, then one (MFMA page kernel, 8 and 4 rows)
     (8, 32, 4, torch.float16),    # G 4: two launches of two tokens
@@ -337,6 +368,9 @@ def test_fast_page_kernel_split_counts_agree():
     (4, 2, 2, 4, 4, 700, torch.bfloat16, 128),    # GQA 1, mixed widths
     (2, 8, 1, 2, 8, 900, torch.float16, 16),
     (8, 4, 2, 3, 12, 1100, torch.bfloat16, 64),
+    (4, 4, 2, 2, 16, 800, torch.bfloat16, 64),    # GQA 8: two row groups
+    (8, 8, 1, 4, 32, 700, torch.float16, 32),     # GQA 8, 8-bit, fp16 cache
+    (2, 2, 1, 2, 16, 900, torch.bfloat16, 16),    # GQA 8, 2-bit, value group 16
 ])
 def test_uniform_page_kernel_vs_oracle_and_general(kb, vb, B, Hkv, Hq, T, dtype, vg):
     """Uniform pages (no promoted channels): the arithmetic page kernel against the oracle and the general
