@@ -269,8 +269,8 @@ typedef struct dkv_segment {
  * with fast_key_bits bits along the tokens (one key group per page), values
  * with fast_value_bits bits along the channels in groups of fast_value_group
  * (2, 4 or 8 bits each), split over half pages (fast_splits at most
- * 2 * fast_count) and Hq / Hkv of 1, 2 or 4.  For Dart pages fast_key_bits
- * and fast_value_bits are 0 or 2.
+ * 2 * fast_count), also with Hq / Hkv of 1, 2, 4 or 8.  For Dart pages
+ * fast_key_bits and fast_value_bits are 0 or 2.
  *
  * Dense rest: when rest_dense_tokens > 0 the caller guarantees that every entry
  * outside the fast range and the tail are dense segments in the cache dtype
