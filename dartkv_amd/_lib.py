@@ -29,6 +29,8 @@ SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 ABI_VERSION = 12
 
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
+# element types the kernels read and write (sources, outputs, metadata)
+FLOAT_DTYPES = (torch.float64, torch.float32, torch.float16, torch.bfloat16)
 
 
 def dtype_code(dtype: torch.dtype) -> int:

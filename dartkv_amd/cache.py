@@ -603,8 +603,6 @@ class DartKVCache:
             raise TypeError("key_states and value_states must be floating-point tensors")
         shape = (key_states.shape[0], key_states.shape[1], key_states.shape[3])
         if self._shape is None:
-            if key_states.dtype == torch.float64:
-                raise TypeError("dartkv_amd caches float16, bfloat16 and float32 tensors")
             self._shape = shape
             self._dtype = key_states.dtype
             self._device = key_states.device

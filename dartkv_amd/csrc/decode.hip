@@ -125,7 +125,7 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
       }
     }
     __syncthreads();
-    const bool dense16 = seg.key_kind == DKV_KEY_DENSE && cache_dt != kF32 && (D % 8) == 0 &&
+    const bool dense16 = seg.key_kind == DKV_KEY_DENSE && (cache_dt == kBF16 || cache_dt == kF16) && (D % 8) == 0 &&
                          (seg.key[0] % 16) == 0 && ((seg.key_bh[0] * 2) % 16) == 0;
     for (int t0 = 0; t0 < seg.tokens; t0 += kThreads) {
       const int nt = min(kThreads, seg.tokens - t0);
@@ -197,7 +197,7 @@ __global__ void __launch_bounds__(kThreads) decode_split_general(DecodeParams p)
         if (c >= D) break;
         float pv[MG];
         DKV_FOR_HEAD(h) pv[h] = 0.f;
-        if (seg.value_kind == DKV_VALUE_DENSE && cache_dt != kF32) {
+        if (seg.value_kind == DKV_VALUE_DENSE && (cache_dt == kBF16 || cache_dt == kF16)) {
           // dense 16-bit values: 8 loads in flight per thread, coalesced across channels
           const uint16_t* vcol = (const uint16_t*)seg.value[0] + bh * seg.value_bh[0] + (int64_t)t0 * D + c;
           int t = 0;
@@ -396,6 +396,8 @@ int scratch_address(void** out) {
 }
 }  // namespace
 
+static bool float_dtype(int64_t dt) { return dt == dkv::kF32 || dt == dkv::kF16 || dt == dkv::kBF16 || dt == dkv::kF64; }
+
 extern "C" int64_t dkv_decode_scratch_bytes(void) { return kScratchBytes; }
 
 extern "C" int dkv_decode_attention_noalloc(const dkv_decode_args* args, void* stream) {
@@ -484,6 +486,8 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
   DKV_CHECK(a.n_segments >= 0 && (a.n_segments == 0 || a.segments != nullptr), DKV_ERR_INVALID, "segments missing");
   DKV_CHECK(a.n_segments + (a.tail.tokens > 0 ? 1 : 0) > 0, DKV_ERR_INVALID, "cache is empty");
   DKV_CHECK(a.B <= 65535 && a.Hkv <= 65535, DKV_ERR_UNSUPPORTED, "batch or KV heads too large");
+  DKV_CHECK(float_dtype(a.q_dtype) && float_dtype(a.cache_dtype) && float_dtype(a.meta_dtype), DKV_ERR_DTYPE,
+            "query, cache and metadata dtypes must be f64, f32, f16 or bf16");
   const int64_t fast_count = a.fast_count;
   if (fast_count > 0) {
     DKV_CHECK(a.fast_first >= 0 && a.fast_first + fast_count <= a.n_segments, DKV_ERR_INVALID,

@@ -30,11 +30,29 @@ constexpr int kThreads = 256;
 // (quantization.py:159-160, mixed.py:187-188).
 __device__ __forceinline__ float nmin(float a, float b) { return __builtin_elementwise_minimum(a, b); }
 __device__ __forceinline__ float nmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ double nmin(double a, double b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ double nmax(double a, double b) { return __builtin_elementwise_maximum(a, b); }
 
 // flag (may be NULL) := 1 when a group's min or max is not finite.  Every
 // writer stores the same value, with a vector store.
-__device__ __forceinline__ void flag_nonfinite(uint32_t* flag, float mn, float mx) {
+template <typename A>
+__device__ __forceinline__ void flag_nonfinite(uint32_t* flag, A mn, A mx) {
   if (flag != nullptr && !(__builtin_isfinite(mn) && __builtin_isfinite(mx))) *flag = 1u;
+}
+
+// The generic (any layout) kernels below run in A = float for fp32, fp16 and
+// bf16 sources (each op rounded to the source dtype) and in A = double for
+// float64 sources: the reference quantizes in the source dtype
+// (quantization.py:179-186), so a float64 tensor is quantized in float64.
+template <typename A>
+__device__ __forceinline__ A src_elem(const void* base, int64_t index, int dt);
+template <>
+__device__ __forceinline__ float src_elem<float>(const void* base, int64_t index, int dt) {
+  return dev_load(base, index, dt);
+}
+template <>
+__device__ __forceinline__ double src_elem<double>(const void* base, int64_t index, int) {
+  return ((const double*)base)[index];
 }
 
 // ---------------------------------------------------------------------------
@@ -62,22 +80,24 @@ __device__ __forceinline__ int64_t out_row(const RowsParams& p, int64_t r) {
   return (r / p.block_rows) * p.out_block_rows + p.out_row0 + r % p.block_rows;
 }
 
-__device__ __forceinline__ float row_elem(const RowsParams& p, int64_t r, int64_t i) {
+template <typename A>
+__device__ __forceinline__ A row_elem(const RowsParams& p, int64_t r, int64_t i) {
   if (i >= p.n) i = p.n - 1;  // replicate the last element (quantization.py:174-177)
   const int64_t row = (r / p.block_rows) * p.block_stride + (r % p.block_rows) * p.row_stride;
-  return dev_load(p.src, row + i * p.elem_stride, p.src_dtype);
+  return src_elem<A>(p.src, row + i * p.elem_stride, p.src_dtype);
 }
 
-__device__ __forceinline__ void group_stats(const RowsParams& p, int64_t r, int64_t g, float qmax, float* mn_out,
-                                            float* scale_out) {
-  float mn = row_elem(p, r, g * p.group), mx = mn;
+template <typename A>
+__device__ __forceinline__ void group_stats(const RowsParams& p, int64_t r, int64_t g, A qmax, A* mn_out,
+                                            A* scale_out) {
+  A mn = row_elem<A>(p, r, g * p.group), mx = mn;
   for (int64_t j = 1; j < p.group; ++j) {
-    const float x = row_elem(p, r, g * p.group + j);
+    const A x = row_elem<A>(p, r, g * p.group + j);
     mn = nmin(mn, x);
     mx = nmax(mx, x);
   }
   flag_nonfinite(p.nonfinite, mn, mx);
-  const float s = dev_group_scale(mn, mx, qmax, p.src_dtype);
+  const A s = dev_group_scale(mn, mx, qmax, p.src_dtype);
   const int64_t o = out_row(p, r);
   dev_store_meta(p.scale, o * p.groups + g, s, p.meta_dtype);
   dev_store_meta(p.zero, o * p.groups + g, mn, p.meta_dtype);
@@ -86,20 +106,21 @@ __device__ __forceinline__ void group_stats(const RowsParams& p, int64_t r, int6
 }
 
 // Groups that start on a byte boundary: one thread per (row, group).
+template <typename A>
 __global__ void __launch_bounds__(kThreads) quantize_rows_aligned(RowsParams p) {
   const int64_t item = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (item >= p.rows * p.groups) return;
   const int64_t r = item / p.groups, g = item % p.groups;
-  const float qmax = (float)((1 << p.bits) - 1);
-  float mn, s;
-  group_stats(p, r, g, qmax, &mn, &s);
+  const A qmax = (A)((1 << p.bits) - 1);
+  A mn, s;
+  group_stats<A>(p, r, g, qmax, &mn, &s);
   uint8_t* out = p.values + out_row(p, r) * p.packed_bytes;
   const int64_t first = g * p.group;
   for (int64_t b = first / p.per_byte; b < (first + p.group) / p.per_byte; ++b) {
     uint32_t byte = 0;
     for (int j = 0; j < p.per_byte; ++j) {
       const int64_t i = b * p.per_byte + j;
-      byte |= dev_group_code(row_elem(p, r, i), mn, s, qmax, p.src_dtype) << (j * p.bits);
+      byte |= dev_group_code(row_elem<A>(p, r, i), mn, s, qmax, p.src_dtype) << (j * p.bits);
     }
     out[b] = (uint8_t)byte;
   }
@@ -314,13 +335,14 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int 
 }
 
 // Any group size: one thread per row walks the packed bytes in order.
+template <typename A>
 __global__ void __launch_bounds__(kThreads) quantize_rows_serial(RowsParams p) {
   const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (r >= p.rows) return;
-  const float qmax = (float)((1 << p.bits) - 1);
+  const A qmax = (A)((1 << p.bits) - 1);
   const int64_t padded = p.groups * p.group;
   uint8_t* out = p.values + out_row(p, r) * p.packed_bytes;
-  float mn = 0.0f, s = 1.0f;
+  A mn = 0, s = 1;
   int64_t cur = -1;
   for (int64_t b = 0; b < p.packed_bytes; ++b) {
     uint32_t byte = 0;
@@ -329,10 +351,10 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_serial(RowsParams p) {
       if (i >= padded) break;
       const int64_t g = i / p.group;
       if (g != cur) {
-        group_stats(p, r, g, qmax, &mn, &s);
+        group_stats<A>(p, r, g, qmax, &mn, &s);
         cur = g;
       }
-      byte |= dev_group_code(row_elem(p, r, i), mn, s, qmax, p.src_dtype) << (j * p.bits);
+      byte |= dev_group_code(row_elem<A>(p, r, i), mn, s, qmax, p.src_dtype) << (j * p.bits);
     }
     out[b] = (uint8_t)byte;
   }
@@ -403,44 +425,69 @@ __device__ __forceinline__ void wave_select_topk(const float* score, int n, int 
   });
 }
 
-__device__ __forceinline__ float key_elem(const KeyParams& k, int64_t b, int64_t h, int64_t page, int64_t t,
-                                          int64_t c) {
+template <typename A>
+__device__ __forceinline__ A key_elem(const KeyParams& k, int64_t b, int64_t h, int64_t page, int64_t t, int64_t c) {
   const dkv_key_pages_args& a = k.a;
   if (t >= a.page_tokens) t = a.page_tokens - 1;  // replicate the last token (mixed.py:196-197)
   const int64_t tok = page * a.page_tokens + t;
-  return dev_load(a.src, b * a.sb + h * a.sh + tok * a.st + c * a.sd, (int)a.src_dtype);
+  return src_elem<A>(a.src, b * a.sb + h * a.sh + tok * a.st + c * a.sd, (int)a.src_dtype);
 }
 
+// One op of the generic kernels' arithmetic, rounded to nearest in A (and, for
+// A = float, then to the 16-bit source dtype by a_round).
+__device__ __forceinline__ float a_add(float x, float y) { return __fadd_rn(x, y); }
+__device__ __forceinline__ double a_add(double x, double y) { return __dadd_rn(x, y); }
+__device__ __forceinline__ float a_sub(float x, float y) { return __fsub_rn(x, y); }
+__device__ __forceinline__ double a_sub(double x, double y) { return __dsub_rn(x, y); }
+__device__ __forceinline__ float a_mul(float x, float y) { return __fmul_rn(x, y); }
+__device__ __forceinline__ double a_mul(double x, double y) { return __dmul_rn(x, y); }
+__device__ __forceinline__ float a_div(float x, float y) { return __fdiv_rn(x, y); }
+__device__ __forceinline__ double a_div(double x, double y) { return __ddiv_rn(x, y); }
+__device__ __forceinline__ float a_abs(float x) { return fabsf(x); }
+__device__ __forceinline__ double a_abs(double x) { return fabs(x); }
+__device__ __forceinline__ float a_round(float x, int dt) { return dev_round_to(x, dt); }
+__device__ __forceinline__ double a_round(double x, int) { return x; }
+
 // Token mean of f(x) over the page's real tokens with ATen's CPU cascade order
-// (fp32 accumulate, 4 levels), then one division and one rounding to the
-// source dtype.  mode 0: |x|; mode 1: rnd(rnd(x - mean)^2).
-__device__ float channel_mean(const KeyParams& k, int64_t b, int64_t h, int64_t page, int64_t c, int mode,
-                              float center) {
+// (4 levels, accumulated in fp32 for fp32/fp16/bf16 sources and in double for
+// float64 ones: ATen's accumulate type of each), then one division and one
+// rounding to the source dtype.  mode 0: |x|; mode 1: rnd(rnd(x - center)^2);
+// mode 2: x.
+template <typename A>
+__device__ A channel_mean(const KeyParams& k, int64_t b, int64_t h, int64_t page, int64_t c, int mode, A center) {
   const int64_t n = k.a.page_tokens;
   const int dt = (int)k.a.src_dtype;
   const int lp = cascade_level_power(n);
   const int64_t step = (int64_t)1 << lp, mask = step - 1;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  A acc[4] = {0, 0, 0, 0};
   int64_t i = 0;
-  auto term = [&](int64_t t) -> float {
-    const float x = key_elem(k, b, h, page, t, c);
-    if (mode == 0) return fabsf(x);
-    const float d = dev_round_to(__fsub_rn(x, center), dt);
-    return dev_round_to(__fmul_rn(d, d), dt);
+  auto term = [&](int64_t t) -> A {
+    const A x = key_elem<A>(k, b, h, page, t, c);
+    if (mode == 0) return a_abs(x);
+    if (mode == 2) return x;
+    const A d = a_round(a_sub(x, center), dt);
+    return a_round(a_mul(d, d), dt);
   };
   for (; i + step <= n;) {
-    for (int64_t j = 0; j < step; ++j, ++i) acc[0] = __fadd_rn(acc[0], term(i));
+    for (int64_t j = 0; j < step; ++j, ++i) acc[0] = a_add(acc[0], term(i));
     for (int j = 1; j < 4; ++j) {
-      acc[j] = __fadd_rn(acc[j], acc[j - 1]);
-      acc[j - 1] = 0.f;
+      acc[j] = a_add(acc[j], acc[j - 1]);
+      acc[j - 1] = 0;
       if ((i & (mask << (j * lp))) != 0) break;
     }
   }
-  for (; i < n; ++i) acc[0] = __fadd_rn(acc[0], term(i));
-  for (int j = 1; j < 4; ++j) acc[0] = __fadd_rn(acc[0], acc[j]);
-  return dev_round_to(__fdiv_rn(acc[0], (float)n), dt);
+  for (; i < n; ++i) acc[0] = a_add(acc[0], term(i));
+  for (int j = 1; j < 4; ++j) acc[0] = a_add(acc[0], acc[j]);
+  return a_round(a_div(acc[0], (A)n), dt);
 }
 
+// Shared memory of quantize_key_pages_kernel<A> for head_dim D.
+template <typename A>
+size_t key_generic_smem(int64_t D) {
+  return (size_t)D * (sizeof(float) + 2 * sizeof(int32_t) + sizeof(SelItem) + (sizeof(A) == 8 ? sizeof(double) : 0));
+}
+
+template <typename A>
 __global__ void __launch_bounds__(kThreads) quantize_key_pages_kernel(KeyParams k) {
   extern __shared__ unsigned char smem[];
   const dkv_key_pages_args& a = k.a;
@@ -450,8 +497,11 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_kernel(KeyParams 
   const int dt = (int)a.src_dtype, meta = (int)a.meta_dtype;
   const bool mixed = a.key_mode == DKV_KEY_MIXED;
   const int64_t K = mixed ? a.promoted : 0;
+  constexpr bool kDouble = sizeof(A) == 8;
 
-  float* score = (float*)smem;                       // [D]
+  // [D] double scores (float64 sources only), then [D] float selection keys
+  double* dscore = (double*)smem;
+  float* score = (float*)(smem + (kDouble ? D * sizeof(double) : 0));
   int32_t* slot = (int32_t*)(score + D);              // [D] promoted slot or -1
   int32_t* sel = slot + D;                            // [D] selected channel per slot
   SelItem* work = (SelItem*)(sel + D);                // [D]
@@ -460,33 +510,37 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_kernel(KeyParams 
 
   if (mixed && K > 0 && K < D && a.selection != DKV_SELECT_GIVEN) {
     for (int64_t c = threadIdx.x; c < D; c += kThreads) {
+      A sc;
       if (a.selection == DKV_SELECT_MAGNITUDE) {
-        score[c] = channel_mean(k, b, h, page, c, 0, 0.f);
+        sc = channel_mean<A>(k, b, h, page, c, 0, A(0));
       } else {
         // variance: mean(rnd(rnd(x - mean(x))^2)) (mixed.py:159-160)
-        float m = 0.f;
-        {
-          const int64_t n = a.page_tokens;
-          const int lp = cascade_level_power(n);
-          const int64_t step = (int64_t)1 << lp, mask = step - 1;
-          float acc[4] = {0.f, 0.f, 0.f, 0.f};
-          int64_t i = 0;
-          for (; i + step <= n;) {
-            for (int64_t j = 0; j < step; ++j, ++i) acc[0] = __fadd_rn(acc[0], key_elem(k, b, h, page, i, c));
-            for (int j = 1; j < 4; ++j) {
-              acc[j] = __fadd_rn(acc[j], acc[j - 1]);
-              acc[j - 1] = 0.f;
-              if ((i & (mask << (j * lp))) != 0) break;
-            }
-          }
-          for (; i < n; ++i) acc[0] = __fadd_rn(acc[0], key_elem(k, b, h, page, i, c));
-          for (int j = 1; j < 4; ++j) acc[0] = __fadd_rn(acc[0], acc[j]);
-          m = dev_round_to(__fdiv_rn(acc[0], (float)n), dt);
-        }
-        score[c] = channel_mean(k, b, h, page, c, 1, m);
+        sc = channel_mean<A>(k, b, h, page, c, 1, channel_mean<A>(k, b, h, page, c, 2, A(0)));
+      }
+      if (kDouble) {
+        dscore[c] = (double)sc;
+      } else {
+        score[c] = (float)sc;
       }
     }
     __syncthreads();
+    if (kDouble) {
+      // The selection compares scores only, so each double score is replaced
+      // by its rank among the page's scores (D for NaN, which ranks first):
+      // equal scores get equal ranks and the order is kept, so the selection
+      // on the ranks (exact in float) makes the same steps as on the doubles.
+      for (int64_t c = threadIdx.x; c < D; c += kThreads) {
+        const double v = dscore[c];
+        int64_t r = 0;
+        if (v != v) {
+          r = D;
+        } else {
+          for (int64_t j = 0; j < D; ++j) r += dscore[j] < v ? 1 : 0;
+        }
+        score[c] = (float)r;
+      }
+      __syncthreads();
+    }
     if (threadIdx.x == 0) select_topk(score, (int)D, (int)K, work, sel);
     __syncthreads();
   } else if (mixed && K > 0) {
@@ -514,17 +568,17 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_kernel(KeyParams 
 
   for (int64_t c = threadIdx.x; c < D; c += kThreads) {
     const int32_t s_idx = slot[c];
-    const float qmax = mixed ? (s_idx >= 0 ? 15.0f : 3.0f) : (float)((1 << a.bits) - 1);
+    const A qmax = mixed ? (s_idx >= 0 ? A(15) : A(3)) : (A)((1 << a.bits) - 1);
     const int64_t meta_base = (bh * D + c) * G;
-    float mn = 0.f, s = 1.f;
+    A mn = 0, s = 1;
     if (mixed) {
       uint8_t* lrow = low + (bh * D + c) * G * k.nb;
       uint8_t* hrow = s_idx >= 0 ? high + (bh * K + s_idx) * G * k.nb : nullptr;
       for (int64_t g = 0; g < G; ++g) {
-        mn = key_elem(k, b, h, page, g * group, c);
-        float mx = mn;
+        mn = key_elem<A>(k, b, h, page, g * group, c);
+        A mx = mn;
         for (int64_t j = 1; j < group; ++j) {
-          const float x = key_elem(k, b, h, page, g * group + j, c);
+          const A x = key_elem<A>(k, b, h, page, g * group + j, c);
           mn = nmin(mn, x);
           mx = nmax(mx, x);
         }
@@ -537,7 +591,7 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_kernel(KeyParams 
           for (int j = 0; j < 4; ++j) {
             const int64_t w = p * 4 + j;
             if (w >= group) break;
-            const uint32_t code = dev_group_code(key_elem(k, b, h, page, g * group + w, c), mn, s, qmax, dt);
+            const uint32_t code = dev_group_code(key_elem<A>(k, b, h, page, g * group + w, c), mn, s, qmax, dt);
             lo |= (code & 3u) << (2 * j);
             hi |= (code >> 2) << (2 * j);
           }
@@ -556,10 +610,10 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_kernel(KeyParams 
           if (i >= padded) break;
           const int64_t g = i / group;
           if (g != cur) {
-            mn = key_elem(k, b, h, page, g * group, c);
-            float mx = mn;
+            mn = key_elem<A>(k, b, h, page, g * group, c);
+            A mx = mn;
             for (int64_t q = 1; q < group; ++q) {
-              const float x = key_elem(k, b, h, page, g * group + q, c);
+              const A x = key_elem<A>(k, b, h, page, g * group + q, c);
               mn = nmin(mn, x);
               mx = nmax(mx, x);
             }
@@ -569,7 +623,7 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_kernel(KeyParams 
             dev_store_meta(zero, meta_base + g, mn, meta);
             cur = g;
           }
-          byte |= dev_group_code(key_elem(k, b, h, page, i, c), mn, s, qmax, dt) << (j * bits);
+          byte |= dev_group_code(key_elem<A>(k, b, h, page, i, c), mn, s, qmax, dt) << (j * bits);
         }
         row[p] = (uint8_t)byte;
       }
@@ -1159,9 +1213,8 @@ __global__ void __launch_bounds__(kThreads) dequantize_rows_kernel(const uint8_t
   const int per_byte = 8 / bits;
   const uint32_t code = (values[r * packed_bytes + i / per_byte] >> ((i % per_byte) * bits)) & ((1u << bits) - 1u);
   const int64_t g = i / group;
-  const float v = dev_dequant(code, dev_load_meta(scale, r * groups + g, meta), dev_load_meta(zero, r * groups + g, meta),
-                              meta, out_dt);
-  dev_store(out, r * out_stride + i, v, out_dt);
+  dev_dequant_store(out, r * out_stride + i, code, dev_load_meta(scale, r * groups + g, meta),
+                    dev_load_meta(zero, r * groups + g, meta), meta, out_dt);
 }
 
 __global__ void __launch_bounds__(kThreads) dequantize_mixed_kernel(const uint8_t* low, const uint8_t* high,
@@ -1188,11 +1241,11 @@ __global__ void __launch_bounds__(kThreads) dequantize_mixed_kernel(const uint8_
   const int32_t s = inv[c];
   if (s >= 0) code |= ((high[((bh * K + s) * G + g) * nb + w / 4] >> ((w % 4) * 2)) & 3u) << 2;
   const int64_t mi = (bh * D + c) * G + g;
-  const float v = dev_dequant(code, dev_load_meta(scale, mi, meta), dev_load_meta(zero, mi, meta), meta, out_dt);
-  dev_store(out, (bh * T + t) * D + c, v, out_dt);
+  dev_dequant_store(out, (bh * T + t) * D + c, code, dev_load_meta(scale, mi, meta), dev_load_meta(zero, mi, meta),
+                    meta, out_dt);
 }
 
-bool valid_float_dtype(int64_t dt) { return dt == kF32 || dt == kF16 || dt == kBF16; }
+bool valid_float_dtype(int64_t dt) { return dt == kF32 || dt == kF16 || dt == kBF16 || dt == kF64; }
 bool valid_meta_dtype(int64_t dt) { return dt == kF32 || dt == kF16 || dt == kBF16 || dt == kF64; }
 bool valid_bits(int64_t b) { return b == 2 || b == 4 || b == 8; }
 
@@ -1214,7 +1267,7 @@ static int prepare_rows(const void* src, int src_dtype, int64_t blocks, int64_t 
                         void* scale, void* zero, int meta_dtype, uint32_t* nonfinite, int64_t out_block_rows,
                         int64_t out_row0, RowsLaunch& L) {
   const int64_t rows = blocks * block_rows;
-  DKV_CHECK(valid_float_dtype(src_dtype), DKV_ERR_DTYPE, "quantize expects a floating-point tensor (f32/f16/bf16)");
+  DKV_CHECK(valid_float_dtype(src_dtype), DKV_ERR_DTYPE, "quantize expects a floating-point tensor (f64/f32/f16/bf16)");
   DKV_CHECK(valid_meta_dtype(meta_dtype), DKV_ERR_DTYPE, "metadata dtype must be floating point");
   DKV_CHECK(valid_bits(bits), DKV_ERR_INVALID, "bits must be one of (2, 4, 8), got %d", bits);
   DKV_CHECK(group > 0, DKV_ERR_INVALID, "group_size must be a positive integer, got %lld", (long long)group);
@@ -1247,7 +1300,7 @@ static int prepare_rows(const void* src, int src_dtype, int64_t blocks, int64_t 
   L.rows = rows;
   L.bits = bits;
   L.src_dtype = src_dtype;
-  const int esize = src_dtype == kF32 ? 4 : 2;
+  const int esize = src_dtype == kF64 ? 8 : src_dtype == kF32 ? 4 : 2;
   L.vec = elem_stride == 1 && n % 8 == 0 && group % 8 == 0 && group <= 512 && (group & (group - 1)) == 0 &&
           n % group == 0 && ((uintptr_t)src % 16) == 0 && (row_stride * esize) % 16 == 0 &&
           (block_stride * esize) % 16 == 0 &&
@@ -1285,11 +1338,19 @@ static void launch_rows(const RowsLaunch& L, hipStream_t s) {
 #undef DKV_ROWS_LAUNCH
   } else if (p.group % p.per_byte == 0) {
     const int64_t items = L.rows * p.groups;
-    hipLaunchKernelGGL(quantize_rows_aligned, dim3((unsigned)((items + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                       s, p);
+    const dim3 grid((unsigned)((items + kThreads - 1) / kThreads));
+    if (L.src_dtype == kF64) {
+      hipLaunchKernelGGL(quantize_rows_aligned<double>, grid, dim3(kThreads), 0, s, p);
+    } else {
+      hipLaunchKernelGGL(quantize_rows_aligned<float>, grid, dim3(kThreads), 0, s, p);
+    }
   } else {
-    hipLaunchKernelGGL(quantize_rows_serial, dim3((unsigned)((L.rows + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                       s, p);
+    const dim3 grid((unsigned)((L.rows + kThreads - 1) / kThreads));
+    if (L.src_dtype == kF64) {
+      hipLaunchKernelGGL(quantize_rows_serial<double>, grid, dim3(kThreads), 0, s, p);
+    } else {
+      hipLaunchKernelGGL(quantize_rows_serial<float>, grid, dim3(kThreads), 0, s, p);
+    }
   }
 }
 
@@ -1337,7 +1398,7 @@ extern "C" int dkv_quantize_value_rows(const dkv_value_rows_args* args, void* st
 extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stream) {
   DKV_CHECK(args != nullptr, DKV_ERR_INVALID, "args is NULL");
   const dkv_key_pages_args& a = *args;
-  DKV_CHECK(valid_float_dtype(a.src_dtype), DKV_ERR_DTYPE, "key_states must be floating point (f32/f16/bf16)");
+  DKV_CHECK(valid_float_dtype(a.src_dtype), DKV_ERR_DTYPE, "key_states must be floating point (f64/f32/f16/bf16)");
   DKV_CHECK(valid_meta_dtype(a.meta_dtype), DKV_ERR_DTYPE, "metadata_dtype must be floating point");
   DKV_CHECK(a.B > 0 && a.H > 0 && a.D > 0 && a.page_tokens > 0 && a.n_pages >= 0, DKV_ERR_INVALID,
             "key_states sequence and head dimensions must be non-empty");
@@ -1470,10 +1531,15 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
     if (with_values) launch_rows(VL, s);
     return dkv_check_launch("dkv_quantize_key_pages");
   }
-  const size_t shmem = (size_t)a.D * (sizeof(float) + 2 * sizeof(int32_t) + sizeof(SelItem));
+  const bool f64 = a.src_dtype == kF64;
+  const size_t shmem = f64 ? key_generic_smem<double>(a.D) : key_generic_smem<float>(a.D);
   DKV_CHECK(shmem <= 64 * 1024, DKV_ERR_UNSUPPORTED, "head_dim %lld is too large", (long long)a.D);
-  hipLaunchKernelGGL(quantize_key_pages_kernel, dim3((unsigned)(a.B * a.H), (unsigned)a.n_pages), dim3(kThreads),
-                     shmem, s, k);
+  const dim3 grid((unsigned)(a.B * a.H), (unsigned)a.n_pages);
+  if (f64) {
+    hipLaunchKernelGGL(quantize_key_pages_kernel<double>, grid, dim3(kThreads), shmem, s, k);
+  } else {
+    hipLaunchKernelGGL(quantize_key_pages_kernel<float>, grid, dim3(kThreads), shmem, s, k);
+  }
   if (with_values) launch_rows(VL, s);
   return dkv_check_launch("dkv_quantize_key_pages");
 }
@@ -1482,7 +1548,7 @@ extern "C" int dkv_dequantize_rows(const uint8_t* values, const void* scale, con
                                    int64_t rows, int64_t n, int bits, int64_t group, void* out, int out_dtype,
                                    int64_t out_row_stride, void* stream) {
   DKV_CHECK(valid_meta_dtype(meta_dtype), DKV_ERR_DTYPE, "metadata dtype must be floating point");
-  DKV_CHECK(valid_float_dtype(out_dtype), DKV_ERR_DTYPE, "output dtype must be f32/f16/bf16");
+  DKV_CHECK(valid_float_dtype(out_dtype), DKV_ERR_DTYPE, "output dtype must be f64/f32/f16/bf16");
   DKV_CHECK(valid_bits(bits), DKV_ERR_INVALID, "bits must be one of (2, 4, 8)");
   DKV_CHECK(group > 0 && n > 0 && rows >= 0, DKV_ERR_INVALID, "bad dequantize shape");
   if (rows == 0) return DKV_OK;
@@ -1500,7 +1566,7 @@ extern "C" int dkv_dequantize_mixed(const uint8_t* low, const uint8_t* high, con
                                     const void* zero, int meta_dtype, int64_t B, int64_t H, int64_t D, int64_t tokens,
                                     int64_t group, int64_t promoted, void* out, int out_dtype, void* stream) {
   DKV_CHECK(valid_meta_dtype(meta_dtype), DKV_ERR_DTYPE, "metadata dtype must be floating point");
-  DKV_CHECK(valid_float_dtype(out_dtype), DKV_ERR_DTYPE, "output dtype must be f32/f16/bf16");
+  DKV_CHECK(valid_float_dtype(out_dtype), DKV_ERR_DTYPE, "output dtype must be f64/f32/f16/bf16");
   DKV_CHECK(B > 0 && H > 0 && D > 0 && tokens > 0 && group > 0, DKV_ERR_INVALID, "bad dequantize shape");
   DKV_CHECK(promoted >= 0 && promoted <= D, DKV_ERR_INVALID, "bad promoted channel count");
   DKV_CHECK(D <= 16384 && B * H <= 65535, DKV_ERR_UNSUPPORTED, "shape too large for dkv_dequantize_mixed");

@@ -88,7 +88,7 @@ class MixedQuantizedKey:
             return self.to(gpu).dequantize(dtype=dtype).cpu()
         _lib.require_device(self.low_values)
         B, H, T, D = self.original_shape
-        kernel_dtype = out_dtype if out_dtype in (torch.float32, torch.float16, torch.bfloat16) else torch.float32
+        kernel_dtype = out_dtype if out_dtype in _lib.FLOAT_DTYPES else torch.float32
         out = torch.empty(B, H, T, D, dtype=kernel_dtype, device=self.low_values.device)
         fields = [t.contiguous() for t in (self.low_values, self.high_values, self.channel_indices, self.scale,
                                            self.zero_point)]
@@ -186,8 +186,6 @@ def quantize_key_mixed(
     meta = metadata_dtype or (key_states.dtype if key_states.dtype in (torch.float16, torch.bfloat16) else torch.float32)
     if meta not in (torch.float16, torch.bfloat16, torch.float32, torch.float64):
         raise TypeError("metadata_dtype must be floating point")
-    if key_states.dtype == torch.float64:
-        raise TypeError("dartkv_amd quantizes float16, bfloat16 and float32 tensors")
     _lib.require_device(key_states)
     B, H, T, D = key_states.shape
     K = promoted_count(D, promote_ratio)

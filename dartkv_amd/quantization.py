@@ -96,7 +96,7 @@ class QuantizedTensor:
         zero = self.zero_point.reshape(rows, -1)
         if not (values.is_contiguous() and scale.is_contiguous() and zero.is_contiguous()):
             values, scale, zero = values.contiguous(), scale.contiguous(), zero.contiguous()
-        kernel_dtype = out_dtype if out_dtype in (torch.float32, torch.float16, torch.bfloat16) else torch.float32
+        kernel_dtype = out_dtype if out_dtype in _lib.FLOAT_DTYPES else torch.float32
         out = torch.empty(rows, n, dtype=kernel_dtype, device=self.values.device)
         lib = _lib.load()
         rc = lib.dkv_dequantize_rows(values.data_ptr(), scale.data_ptr(), zero.data_ptr(),
@@ -151,8 +151,6 @@ def quantize(
     if not isinstance(axis, int) or not -data.ndim <= axis < data.ndim:
         raise ValueError(f"axis must be in [-{data.ndim}, {data.ndim}), got {axis}")
     axis = axis % data.ndim
-    if data.dtype == torch.float64:
-        raise TypeError("dartkv_amd quantizes float16, bfloat16 and float32 tensors")
     _lib.require_device(data)
     moved = data.movedim(axis, -1).contiguous()
     n = moved.shape[-1]

@@ -8,7 +8,12 @@
  * thread-local message.  Nothing here allocates device memory: callers pass
  * outputs and workspace.
  *
- * Element types (the *_dtype arguments) use DKV_DTYPE_*.
+ * Element types (the *_dtype arguments) use DKV_DTYPE_*.  Sources, outputs,
+ * caches and queries may be float64, float32, float16 or bfloat16 (the page
+ * kernels of dkv_decode_attention take bf16 / fp16 caches; everything else
+ * takes all four).  As in the reference, quantization runs in the source
+ * dtype: a float64 source in IEEE double with eps 1e-6, its float64 scale and
+ * minimum converted to a 16-bit metadata dtype through float32, as torch does.
  *
  * Layouts are the reference's tensor layouts (reference src/dart/quantization.py,
  * src/dart/mixed.py), so a reference-side binding can hand over the storage

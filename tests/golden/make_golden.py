@@ -92,6 +92,28 @@ def main() -> None:
                         })
                         case += 1
 
+    # float64 sources: the reference quantizes them in float64 with eps 1e-6
+    # (quantization.py:182-186) and metadata float32 by default.  The inputs get
+    # low-order bits a float32 value cannot hold.
+    for shape in shapes:
+        base = torch.randn(*shape, generator=gen, dtype=torch.float64)
+        base = base * (torch.rand(shape[-1], generator=gen, dtype=torch.float64) * 8 + 0.01)
+        base[..., 0] = 0.0
+        for bits, group, axis, meta in ((2, 4, -1, None), (4, 5, -2, torch.float64), (8, 32, 0, torch.float32),
+                                        (2, 64, -1, torch.float16), (4, 4, -1, torch.bfloat16),
+                                        (2, 128, -2, torch.float64)):
+            q = dart.quantize(base, bits=bits, group_size=group, metadata_dtype=meta, axis=axis)
+            tag = f"u{case}"
+            manifest["uniform"].append({
+                "tag": tag, "bits": bits, "group": group, "axis": axis,
+                "meta": None if meta is None else str(meta).replace("torch.", ""),
+                "input": put(tag + ".in", base, limit=1 << 20), "values": put(tag + ".values", q.values),
+                "scale": put(tag + ".scale", q.scale), "zero": put(tag + ".zero", q.zero_point),
+                "deq": put(tag + ".deq", q.dequantize()),
+                "padded_dim": q.padded_dim, "packed_dim": q.packed_dim,
+            })
+            case += 1
+
     # ---- mixed keys (mixed.py:119-244) ----
     case = 0
     for dtype in (torch.bfloat16, torch.float16, torch.float32):
@@ -120,6 +142,30 @@ def main() -> None:
                 "deq": put(tag + ".deq", mk.dequantize()), "padded_tokens": mk.padded_tokens,
             })
             case += 1
+    # float64 keys (channel scores are float64 means, accumulated in double)
+    gen64 = torch.Generator().manual_seed(4321)
+    for (B, H, T, D, group, ratio, strategy, meta) in (
+        (1, 8, 128, 128, 128, 0.25, "magnitude", torch.float16),
+        (2, 2, 17, 16, 8, 0.25, "magnitude", torch.float64),
+        (1, 2, 96, 128, 128, 0.25, "variance", torch.float32),
+        (1, 3, 40, 64, 32, 0.5, "variance", torch.float64),
+        (1, 2, 64, 128, 64, 0.02, "magnitude", torch.float64),
+    ):
+        keys, _, _ = syn.outlier_kv(B, H, T, D, dtype=torch.float32, seed=500 + case, outliers=min(8, D // 4))
+        keys = keys.to(torch.float64) * (1 + 1e-9 * torch.randn(keys.shape, generator=gen64, dtype=torch.float64))
+        mk = dart.quantize_key_mixed(keys, group_size=group, promote_ratio=ratio, strategy=strategy,
+                                     metadata_dtype=meta)
+        tag = f"m{case}"
+        manifest["mixed"].append({
+            "tag": tag, "group": group, "ratio": ratio, "strategy": strategy,
+            "meta": str(meta).replace("torch.", ""), "shape": [B, H, T, D], "seed": 500 + case,
+            "outliers": min(8, D // 4), "dtype": "float64",
+            "input": put(tag + ".in", keys, limit=1 << 21), "low": put(tag + ".low", mk.low_values),
+            "high": put(tag + ".high", mk.high_values), "idx": put(tag + ".idx", mk.channel_indices),
+            "scale": put(tag + ".scale", mk.scale), "zero": put(tag + ".zero", mk.zero_point),
+            "deq": put(tag + ".deq", mk.dequantize()), "padded_tokens": mk.padded_tokens,
+        })
+        case += 1
 
     # ---- cache lifecycles (cache.py:168-542) + streamed attention (attention.py:32-87) ----
     def seg_fields(seg):
@@ -150,11 +196,24 @@ def main() -> None:
         ("uniform_mix_bits", dict(bits=4, key_bits=2, value_bits=8, page_size=16, key_group_size=8,
                                   value_group_size=32, sink_tokens=1, hold_partial_pages=True,
                                   metadata_dtype=torch.bfloat16), 2, 2, 8, 64, torch.bfloat16, [40, 1, 20], True),
+        # float64 caches: float64 sink and tail, pages quantized in float64
+        ("f64_mixed", dict(bits=2, page_size=8, key_group_size=8, value_group_size=8, sink_tokens=3,
+                           promote_ratio=0.25, hold_partial_pages=True, metadata_dtype=torch.float64),
+         1, 2, 4, 16, torch.float64, [21, 1, 1, 9, 1], True),
+        ("f64_uniform", dict(bits=4, page_size=8, key_group_size=4, value_group_size=6, sink_tokens=3,
+                             metadata_dtype=torch.float32), 2, 2, 4, 12, torch.float64, [13, 5, 1, 9, 1, 1], True),
+        ("f64_meta16", dict(bits=2, page_size=16, key_group_size=16, value_group_size=8, sink_tokens=2,
+                            promote_ratio=0.25, metadata_dtype=torch.float16), 1, 2, 8, 32, torch.float64,
+         [40, 1, 7], True),
     ]
+    gen_lc = torch.Generator().manual_seed(8642)
     for name, cfg_kwargs, B, Hkv, Hq, D, dtype, updates, store_inputs in lifecycles:
         total = sum(updates)
         keys, values, query = syn.outlier_kv(B, Hkv, total, D, query_heads=Hq, dtype=dtype,
                                              outliers=(8 if D >= 64 else 2) if name != "c1" else 0)
+        if dtype == torch.float64:
+            keys, values, query = (t * (1 + 1e-9 * torch.randn(t.shape, generator=gen_lc, dtype=torch.float64))
+                                   for t in (keys, values, query))
         cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg_kwargs))
         start = 0
         for n in updates:

@@ -2,7 +2,8 @@
 
 Bar: packed codes, channel indices, scales and zero points bit-exact;
 attention within max|a-b| / max|b| per (batch, head) of 2e-3 for bf16/fp16
-caches and 1e-5 for fp32 caches, on the fp32 output before the final cast.
+caches and 1e-5 for fp32 and float64 caches, on the fp32 output before the
+final cast.
 """
 
 from __future__ import annotations
@@ -34,7 +35,9 @@ def rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
 
 
 def tolerance(dtype: torch.dtype) -> float:
-    return 1e-5 if dtype == torch.float32 else 2e-3
+    """fp32 attention over 16-bit inputs: 2e-3; over fp32 and float64 caches (whose
+    attention also computes in fp32): 1e-5."""
+    return 2e-3 if dtype in (torch.float16, torch.bfloat16) else 1e-5
 
 
 def test_uniform_quantize_bit_exact_vs_golden(golden):
@@ -86,7 +89,7 @@ def test_mixed_key_bit_exact_vs_golden_including_tie_order(golden):
         keys = _input(golden, e, DTYPES[e["dtype"]]).to(DEV)
         print("case", e["tag"], tuple(keys.shape), keys.dtype, e["group"], e["ratio"], e["strategy"], flush=True)
         mk = dart.quantize_key_mixed(keys, group_size=e["group"], promote_ratio=e["ratio"], strategy=e["strategy"],
-                                     metadata_dtype=torch.float16)
+                                     metadata_dtype=DTYPES[e["meta"]])
         torch.cuda.synchronize()
         for field, actual in (("low", mk.low_values), ("high", mk.high_values), ("idx", mk.channel_indices),
                               ("scale", mk.scale), ("zero", mk.zero_point), ("deq", mk.dequantize())):
@@ -229,7 +232,7 @@ def test_uniform_append_pages_bit_exact_vs_oracle(bits, dtype):
 
 
 @pytest.mark.parametrize("name", ["c2", "c1", "nonheld", "held_mixed", "kitty_local", "kitty_value_local",
-                                  "uniform_mix_bits"])
+                                  "uniform_mix_bits", "f64_mixed", "f64_uniform", "f64_meta16"])
 def test_cache_pages_and_decode_vs_golden(golden, name):
     dart = _dkv()
     from tests.test_oracle_golden import _lifecycle_inputs
@@ -266,6 +269,60 @@ def test_cache_pages_and_decode_vs_golden(golden, name):
         assert err <= tolerance(keys.dtype), (name, err)
         fused = dart.fused_dart_attention(qd, cache, fallback=False)
         assert bits_equal(fused.cpu(), out.cpu())
+
+
+@pytest.mark.parametrize("meta,ratio,strategy", [
+    (torch.float16, 0.25, "magnitude"),
+    (torch.float64, 0.25, "variance"),
+    (torch.float32, 0.0, "magnitude"),
+])
+def test_float64_cache_vs_oracle(meta, ratio, strategy):
+    """A float64 cache (the reference caches float64 tensors: quantized in float64, attention in fp32,
+    output cast back): five 128-token pages per (batch, head) in one append, then one-token appends;
+    pages and materialized K/V bit-exact, one- and three-token attention within 1e-5."""
+    dart = _dkv()
+    from oracle import dart_oracle as O
+    from dartkv_amd import synthetic
+    g = torch.Generator().manual_seed(64)
+    k, v, q = synthetic.outlier_kv(2, 2, 703, 128, query_heads=8, dtype=torch.float64, seed=91)
+    k, v = (t * (1 + 1e-9 * torch.randn(t.shape, generator=g, dtype=torch.float64)) for t in (k, v))
+    q3 = torch.randn(2, 8, 3, 128, generator=g, dtype=torch.float64)
+    cfg = dict(bits=4 if ratio == 0.0 else 2, page_size=128, key_group_size=128, value_group_size=64,
+               promote_ratio=ratio, channel_selection=strategy, sink_tokens=32, hold_partial_pages=True,
+               metadata_dtype=meta)
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    kd, vd = k.to(DEV), v.to(DEV)
+    print("float64 cache", meta, ratio, strategy, flush=True)
+    for a, b in ((0, 700), (700, 701), (701, 702), (702, 703)):
+        oc.append(k[..., a:b, :], v[..., a:b, :])
+        cache.append(kd[..., a:b, :], vd[..., a:b, :])
+    torch.cuda.synchronize()
+    assert len(cache.iter_segments()) == len(oc.segments())
+    for (ks, vs), (oks, ovs) in zip(cache.iter_segments(), oc.segments()):
+        for x, y in zip(_seg_fields(ks).values(), _seg_fields(oks).values()):
+            assert bits_equal(x.cpu(), y)
+        for x, y in zip(_seg_fields(vs).values(), _seg_fields(ovs).values()):
+            assert bits_equal(x.cpu(), y)
+    mk, mv = cache.get()
+    omk, omv = oc.get()
+    assert bits_equal(mk.cpu(), omk) and bits_equal(mv.cpu(), omv)
+    ref32 = O.streamed_attention(q, oc, return_fp32=True)[1]
+    out32 = torch.empty(2, 8, 128, dtype=torch.float32, device=DEV)
+    out = dart.decode_attention(q.to(DEV), cache, out_f32=out32)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float64
+    err = rel_err(out32.unsqueeze(2), ref32)
+    print("float64 decode rel err", err, flush=True)
+    assert err <= 1e-5
+    assert bits_equal(out.cpu(), out32.unsqueeze(2).cpu().double())
+    ref3 = O.streamed_attention(q3, oc, return_fp32=True)[1]
+    out3 = dart.streamed_dart_attention(q3.to(DEV), cache)
+    torch.cuda.synchronize()
+    assert out3.dtype == torch.float64
+    err3 = rel_err(out3.float(), ref3)
+    print("float64 three-token rel err", err3, flush=True)
+    assert err3 <= 1e-5
 
 
 @pytest.mark.parametrize("seed", [0, 1, 2])

@@ -36,11 +36,11 @@ def test_uniform_quantize_matches_reference(golden):
 
 def test_mixed_key_matches_reference_including_tie_order(golden):
     entries = golden.manifest["mixed"]
-    assert len(entries) == 24
+    assert len(entries) == 29
     for e in entries:
         keys = _input(golden, e, DTYPES[e["dtype"]])
         mk = O.quantize_key_mixed(keys, group_size=e["group"], promote_ratio=e["ratio"],
-                                  strategy=e["strategy"], metadata_dtype=torch.float16)
+                                  strategy=e["strategy"], metadata_dtype=DTYPES[e["meta"]])
         for field, actual in (("low", mk.low_values), ("high", mk.high_values), ("idx", mk.channel_indices),
                               ("scale", mk.scale), ("zero", mk.zero_point), ("deq", mk.dequantize())):
             assert golden.matches(e[field], actual), (e["tag"], field)
@@ -76,7 +76,7 @@ def _seg_fields(seg):
 
 
 @pytest.mark.parametrize("name", ["c2", "c1", "nonheld", "held_mixed", "kitty_local", "kitty_value_local",
-                                  "uniform_mix_bits"])
+                                  "uniform_mix_bits", "f64_mixed", "f64_uniform", "f64_meta16"])
 def test_cache_lifecycle_and_streamed_attention_match_reference(golden, name):
     e = next(x for x in golden.manifest["cache"] if x["name"] == name)
     keys, values, query = _lifecycle_inputs(golden, e)
