@@ -223,22 +223,26 @@ __device__ __forceinline__ float rows_group_scale(float mn, float mx, float qmax
   return src_round<SRC>(d);
 }
 
-// Contiguous rows, groups of 8 * L elements (L = 1..64 lanes, a power of two)
-// that tile the row exactly: every lane owns 8 consecutive elements (one
-// 16-byte load for 16-bit sources), the L lanes of a group reduce min/max with
-// cross-lane shuffles, and every lane stores its 8 codes packed (2, 4 or 8
-// bytes).  A wave's loads and stores are contiguous.  The source dtype is a
-// template argument, so the per-element chain (subtract, round, divide,
+// Contiguous rows, groups of E * L elements (E = 8 or 16 elements per lane, L =
+// 1..64 lanes, a power of two) that tile the row exactly: every lane owns E
+// consecutive elements (16-byte loads for 16-bit sources), the L lanes of a
+// group reduce min/max with cross-lane shuffles, and every lane stores its E
+// codes packed.  A wave's loads and stores are contiguous.  The source dtype
+// is a template argument, so the per-element chain (subtract, round, divide,
 // round, rint, clamp) has no branches; the division is one reciprocal per
-// group and three operations per element.  Workgroup (bx, by) of a gx x gy
-// grid: y strides over row blocks, x over the lanes of one block, kRowChunks
-// chunks of kThreads lanes per step: a lane issues the loads of all its chunks
-// before it computes (one chunk per lane left each wave with one 16-byte load
-// in flight per lane, and the kernel waiting on memory latency).
+// group and three operations per element.  The per-group work (shuffles,
+// scale, reciprocal, metadata stores) is one instruction stream per lane
+// whatever E is, so 16 elements per lane spend about a quarter fewer VALU
+// instructions per element than 8.  Workgroup (bx, by) of a gx x gy grid: y
+// strides over row blocks, x over the lanes of one block, kRowChunks chunks of
+// kThreads lanes per step: a lane issues the loads of all its chunks before it
+// computes (one chunk per lane left each wave with one 16-byte load in flight
+// per lane, and the kernel waiting on memory latency).
 constexpr int kRowChunks = 2;
 
+// Elements i0 .. i0 + 7 of a source row as fp32.
 template <int SRC>
-__device__ __forceinline__ void load_row_chunk(const RowsParams& p, int64_t src_row, int64_t i0, float (&x)[8]) {
+__device__ __forceinline__ void load_row8(const RowsParams& p, int64_t src_row, int64_t i0, float* x) {
   if (SRC == kF32) {
     const float4* src = (const float4*)((const float*)p.src + src_row + i0);
     const float4 a = src[0], b = src[1];
@@ -255,11 +259,12 @@ __device__ __forceinline__ void load_row_chunk(const RowsParams& p, int64_t src_
   }
 }
 
-template <int BITS, int SRC>
+template <int BITS, int SRC, int E>
 __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per_group, int row_shift, int64_t bx,
                                               int64_t by, int64_t gx, int64_t gy) {
+  static_assert(E == 8 || E == 16, "8 or 16 elements per lane");
   // row_shift = log2(lanes per row) when that is a power of two (no 64-bit division)
-  const int64_t lanes_per_row = p.n / 8;
+  const int64_t lanes_per_row = p.n / E;
   const int64_t total = p.block_rows * lanes_per_row;
   const float qmax = (float)((1 << BITS) - 1);
   constexpr float inv_qmax = 1.0f / (float)((1 << BITS) - 1);  // RN(1 / qmax), folded at compile time
@@ -270,8 +275,8 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
   for (int64_t v0 = bx * kStep + threadIdx.x; v0 - lane < total; v0 += gx * kStep) {
     // whole waves stay in the loop so the shuffles see every lane of a group
     int64_t r[kRowChunks];   // row within the block
-    int li[kRowChunks];      // lane item within the row: elements 8 li .. 8 li + 7
-    float x[kRowChunks][8];
+    int li[kRowChunks];      // lane item within the row: elements E li .. E li + E - 1
+    float x[kRowChunks][E];
 #pragma unroll
     for (int u = 0; u < kRowChunks; ++u) {
       const int64_t v = v0 + u * kThreads;
@@ -280,10 +285,12 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
       if (v < total) {
         r[u] = row_shift >= 0 ? v >> row_shift : v / lanes_per_row;
         li[u] = (int)(v - r[u] * lanes_per_row);
-        load_row_chunk<SRC>(p, blk * p.block_stride + r[u] * p.row_stride, 8 * (int64_t)li[u], x[u]);
+        const int64_t row = blk * p.block_stride + r[u] * p.row_stride;
+#pragma unroll
+        for (int c = 0; c < E / 8; ++c) load_row8<SRC>(p, row, (int64_t)E * li[u] + 8 * c, &x[u][8 * c]);
       } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[u][j] = 0.f;
+        for (int j = 0; j < E; ++j) x[u][j] = 0.f;
       }
     }
 #pragma unroll
@@ -293,7 +300,7 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
       const bool active = v < total;
       float mn = x[u][0], mx = x[u][0];
 #pragma unroll
-      for (int j = 1; j < 8; ++j) {
+      for (int j = 1; j < E; ++j) {
         mn = nmin(mn, x[u][j]);
         mx = nmax(mx, x[u][j]);
       }
@@ -311,27 +318,38 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
         dev_store_meta(p.zero, ro * p.groups + g, mn, p.meta_dtype);
         flag_nonfinite(p.nonfinite, mn, mx);
       }
-      // codes 0..3 and 4..7 as bytes (codes_as_bytes), then packed to BITS-bit fields
-      uint32_t packed[2];
+      // codes four at a time as bytes (codes_as_bytes), then packed to BITS-bit fields
+      uint32_t bytes[E / 4];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < E / 4; ++h) {
         float q[4];
         chain_quotients4<SRC>(&x[u][4 * h], mn, s, y, q);
-        packed[h] = codes_as_bytes(q);
+        bytes[h] = codes_as_bytes(q);
       }
-      if (BITS == 4) packed[0] = nibbles_from_bytes(packed[0]) | (nibbles_from_bytes(packed[1]) << 16);
-      if (BITS == 2) packed[0] = pairs_from_bytes(packed[0]) | (pairs_from_bytes(packed[1]) << 8);
-      uint8_t* out = p.values + ro * p.packed_bytes + (int64_t)li[u] * BITS;
-      if (BITS == 2) *(uint16_t*)out = (uint16_t)packed[0];
-      else if (BITS == 4) *(uint32_t*)out = packed[0];
-      else *(uint2*)out = make_uint2(packed[0], packed[1]);
+      uint8_t* out = p.values + ro * p.packed_bytes + (int64_t)li[u] * (E * BITS / 8);
+      if (BITS == 2) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int h = 0; h < E / 4; ++h) w |= pairs_from_bytes(bytes[h]) << (8 * h);
+        if (E == 8) *(uint16_t*)out = (uint16_t)w;
+        else *(uint32_t*)out = w;
+      } else if (BITS == 4) {
+        uint32_t w[E / 8];
+#pragma unroll
+        for (int h = 0; h < E / 8; ++h) w[h] = nibbles_from_bytes(bytes[2 * h]) | (nibbles_from_bytes(bytes[2 * h + 1]) << 16);
+        if (E == 8) *(uint32_t*)out = w[0];
+        else *(uint2*)out = make_uint2(w[0], w[1]);
+      } else {
+        if (E == 8) *(uint2*)out = make_uint2(bytes[0], bytes[1]);
+        else *(uint4*)out = make_uint4(bytes[0], bytes[1], bytes[2], bytes[3]);
+      }
     }
   }
 }
 
-template <int BITS, int SRC>
+template <int BITS, int SRC, int E>
 __global__ void __launch_bounds__(kThreads) quantize_rows_vec(RowsParams p, int lanes_per_group, int row_shift) {
-  rows_vec_body<BITS, SRC>(p, lanes_per_group, row_shift, blockIdx.x, blockIdx.y, gridDim.x, gridDim.y);
+  rows_vec_body<BITS, SRC, E>(p, lanes_per_group, row_shift, blockIdx.x, blockIdx.y, gridDim.x, gridDim.y);
 }
 
 // Any group size: one thread per row walks the packed bytes in order.
@@ -1174,7 +1192,7 @@ constexpr int kSelectWaves = kThreads / 64;
 // and the value rows wait behind them, so the two run as separate launches.
 constexpr int64_t kSelectFuseMaxPages = 8192;
 
-template <int BITS, int SRC>
+template <int BITS, int SRC, int E>
 __global__ void __launch_bounds__(kThreads) select_pages_and_rows(KeyParams k, int row_bytes, int64_t items,
                                                                   int64_t sel_blocks, RowsParams p, int lpg,
                                                                   int row_shift, int64_t gx, int64_t gy) {
@@ -1186,7 +1204,7 @@ __global__ void __launch_bounds__(kThreads) select_pages_and_rows(KeyParams k, i
     return;
   }
   const int64_t b = (int64_t)blockIdx.x - sel_blocks;
-  rows_vec_body<BITS, SRC>(p, lpg, row_shift, b % gx, b / gx, gx, gy);
+  rows_vec_body<BITS, SRC, E>(p, lpg, row_shift, b % gx, b / gx, gx, gy);
 }
 
 __host__ inline size_t key_tiled_smem(int D, int T, int G, int K, int row_bytes) {
@@ -1256,6 +1274,7 @@ struct RowsLaunch {
   RowsParams p;
   int64_t rows;
   bool vec;                // quantize_rows_vec applies
+  int epl;                 // its elements per lane (8 or 16)
   int lpg, row_shift;      // its lanes per group and log2(lanes per row) (-1: not a power of two)
   int64_t gx, gy;          // its grid
   int bits, src_dtype;
@@ -1306,12 +1325,15 @@ static int prepare_rows(const void* src, int src_dtype, int64_t blocks, int64_t 
           (block_stride * esize) % 16 == 0 &&
           (src_dtype == kF32 || src_dtype == kF16 || src_dtype == kBF16) && ((uintptr_t)values % 8) == 0 &&
           (p.packed_bytes * bits) % 8 == 0 && (p.packed_bytes % 8) == 0;
-  L.lpg = (int)(group / 8);
-  const int64_t lpr = n / 8;
+  // 16 elements per lane where groups and rows split into 16s and each lane's
+  // 2 * bits bytes of codes are aligned for one store
+  L.epl = (group % 16 == 0 && n % 16 == 0 && ((uintptr_t)values % (2 * bits)) == 0) ? 16 : 8;
+  L.lpg = (int)(group / L.epl);
+  const int64_t lpr = n / L.epl;
   L.row_shift = (lpr & (lpr - 1)) == 0 ? __builtin_ctzll((unsigned long long)lpr) : -1;
   // x: workgroups over one block's lanes; y: row blocks (the kernel strides
   // over both, so the grid is capped at about 2^20 workgroups)
-  const int64_t lanes = block_rows * (n / 8);
+  const int64_t lanes = block_rows * lpr;
   L.gy = std::max<int64_t>(std::min<int64_t>(blocks, 65535), 1);
   L.gx = std::max<int64_t>(
       std::min<int64_t>((lanes + kThreads * kRowChunks - 1) / (kThreads * kRowChunks), (1 << 20) / L.gy), 1);
@@ -1322,9 +1344,15 @@ static void launch_rows(const RowsLaunch& L, hipStream_t s) {
   if (L.rows == 0) return;
   const RowsParams& p = L.p;
   if (L.vec) {
-#define DKV_ROWS_LAUNCH(B, T)                                                                                     \
-  hipLaunchKernelGGL((quantize_rows_vec<B, T>), dim3((unsigned)L.gx, (unsigned)L.gy), dim3(kThreads), 0, s, p, L.lpg, \
-                     L.row_shift)
+#define DKV_ROWS_LAUNCH(B, T)                                                                                      \
+  do {                                                                                                             \
+    if (L.epl == 16)                                                                                               \
+      hipLaunchKernelGGL((quantize_rows_vec<B, T, 16>), dim3((unsigned)L.gx, (unsigned)L.gy), dim3(kThreads), 0, s, \
+                         p, L.lpg, L.row_shift);                                                                   \
+    else                                                                                                           \
+      hipLaunchKernelGGL((quantize_rows_vec<B, T, 8>), dim3((unsigned)L.gx, (unsigned)L.gy), dim3(kThreads), 0, s,  \
+                         p, L.lpg, L.row_shift);                                                                   \
+  } while (0)
 #define DKV_ROWS_BITS(T)                    \
   do {                                      \
     if (L.bits == 2) DKV_ROWS_LAUNCH(2, T);   \
@@ -1488,9 +1516,15 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
         // the selection and the value rows share one launch
         const int64_t sel_blocks = (items + kSelectWaves - 1) / kSelectWaves;
         const dim3 sgrid((unsigned)(sel_blocks + VL.gx * VL.gy));
-#define DKV_SV(B, T)                                                                                                \
-  hipLaunchKernelGGL((select_pages_and_rows<B, T>), sgrid, dim3(kThreads), 0, s, k, row_bytes, items, sel_blocks, \
-                     VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy)
+#define DKV_SV(B, T)                                                                                           \
+  do {                                                                                                        \
+    if (VL.epl == 16)                                                                                         \
+      hipLaunchKernelGGL((select_pages_and_rows<B, T, 16>), sgrid, dim3(kThreads), 0, s, k, row_bytes, items,  \
+                         sel_blocks, VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy);                               \
+    else                                                                                                      \
+      hipLaunchKernelGGL((select_pages_and_rows<B, T, 8>), sgrid, dim3(kThreads), 0, s, k, row_bytes, items,   \
+                         sel_blocks, VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy);                               \
+  } while (0)
 #define DKV_SV_BITS(T)                    \
   do {                                    \
     if (VL.bits == 2) DKV_SV(2, T);       \
