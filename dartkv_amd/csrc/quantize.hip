@@ -150,16 +150,41 @@ __device__ __forceinline__ uint32_t codes_as_bytes(const float (&q)[4]) {
   r = __builtin_amdgcn_cvt_pk_u8_f32(q[2], 2u, r);
   return __builtin_amdgcn_cvt_pk_u8_f32(q[3], 3u, r);
 }
-// Four byte codes below 16 (byte j) -> nibbles j in bits 4j .. 4j + 3.
-__device__ __forceinline__ uint32_t nibbles_from_bytes(uint32_t b) {
-  const uint32_t t = (b | (b >> 4)) & 0x00ff00ffu;  // c0 | c1 << 4 at bit 0, c2 | c3 << 4 at bit 16
-  return (t | (t >> 8)) & 0xffffu;
+// Codes into byte planes, so packing needs no per-byte shuffling: the
+// v_cvt_pk_u8_f32 that forms a code (the same one instruction per code as
+// codes_as_bytes) writes it at the byte where the packed layout wants it.
+//
+// 2-bit fields, 16 codes per dword (code i at bits 2i, LSB first): plane t
+// holds code 4h + t at byte h, for quotients q of codes 4h .. 4h + 3.
+__device__ __forceinline__ void codes_to_planes2(const float (&q)[4], int h, uint32_t (&plane)[4]) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) plane[t] = __builtin_amdgcn_cvt_pk_u8_f32(q[t], (uint32_t)h, plane[t]);
 }
-// Four byte codes below 4 (byte j) -> 2-bit fields j in bits 2j, 2j + 1.
-__device__ __forceinline__ uint32_t pairs_from_bytes(uint32_t b) {
-  const uint32_t t = (b | (b >> 6)) & 0x000f000fu;  // c0 | c1 << 2 at bit 0, c2 | c3 << 2 at bit 16
-  return (t | (t >> 12)) & 0xffu;
+// The 16 fields from codes below 4: byte h = code 4h | code 4h+1 << 2 | ...
+__device__ __forceinline__ uint32_t pack2(const uint32_t (&plane)[4]) {
+  return plane[0] | (plane[1] << 2) | (plane[2] << 4) | (plane[3] << 6);
 }
+// Codes below 16 (Dart keys: 4-bit codes of promoted channels, 2-bit ones
+// elsewhere): the fields of their low two bits and of their high two bits.
+// (m & a) | (~m & b) is one v_bfi_b32; bits a shift carries into a
+// neighbouring field are overwritten by the outer selections.
+__device__ __forceinline__ uint32_t bit_select(uint32_t m, uint32_t a, uint32_t b) { return (m & a) | (~m & b); }
+__device__ __forceinline__ uint32_t pack2_low(const uint32_t (&plane)[4]) {
+  return bit_select(0x03030303u, plane[0],
+                    bit_select(0x0c0c0c0cu, plane[1] << 2, bit_select(0x30303030u, plane[2] << 4, plane[3] << 6)));
+}
+__device__ __forceinline__ uint32_t pack2_high(const uint32_t (&plane)[4]) {
+  return bit_select(0x03030303u, plane[0] >> 2,
+                    bit_select(0x0c0c0c0cu, plane[1], bit_select(0x30303030u, plane[2] << 2, plane[3] << 4)));
+}
+// 4-bit fields, 8 codes per dword (code i at bits 4i): plane t % 2 holds code
+// 4h + t at byte 2h + t / 2 (h = 0, 1), so the dword is even | odd << 4.
+__device__ __forceinline__ void codes_to_planes4(const float (&q)[4], int h, uint32_t (&plane)[2]) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    plane[t & 1] = __builtin_amdgcn_cvt_pk_u8_f32(q[t], (uint32_t)(2 * h + (t >> 1)), plane[t & 1]);
+}
+__device__ __forceinline__ uint32_t pack4(const uint32_t (&plane)[2]) { return plane[0] | (plane[1] << 4); }
 
 // fp32 a / b rounded to nearest, given y = RN(1 / b): q = RN(a y) is within
 // one ulp of a / b, the residual a - b q is exact with an fma, and
@@ -318,28 +343,44 @@ __device__ __forceinline__ void rows_vec_body(const RowsParams& p, int lanes_per
         dev_store_meta(p.zero, ro * p.groups + g, mn, p.meta_dtype);
         flag_nonfinite(p.nonfinite, mn, mx);
       }
-      // codes four at a time as bytes (codes_as_bytes), then packed to BITS-bit fields
-      uint32_t bytes[E / 4];
-#pragma unroll
-      for (int h = 0; h < E / 4; ++h) {
-        float q[4];
-        chain_quotients4<SRC>(&x[u][4 * h], mn, s, y, q);
-        bytes[h] = codes_as_bytes(q);
-      }
+      // codes four at a time, each written by its conversion at its byte of
+      // the packed layout (codes_to_planes2 / codes_to_planes4; 8-bit codes
+      // are bytes in order), then the fields combined; codes are at most qmax
       uint8_t* out = p.values + ro * p.packed_bytes + (int64_t)li[u] * (E * BITS / 8);
       if (BITS == 2) {
-        uint32_t w = 0;
+        uint32_t plane[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int h = 0; h < E / 4; ++h) w |= pairs_from_bytes(bytes[h]) << (8 * h);
+        for (int h = 0; h < E / 4; ++h) {
+          float q[4];
+          chain_quotients4<SRC>(&x[u][4 * h], mn, s, y, q);
+          codes_to_planes2(q, h, plane);
+        }
+        const uint32_t w = pack2(plane);
         if (E == 8) *(uint16_t*)out = (uint16_t)w;
         else *(uint32_t*)out = w;
       } else if (BITS == 4) {
         uint32_t w[E / 8];
 #pragma unroll
-        for (int h = 0; h < E / 8; ++h) w[h] = nibbles_from_bytes(bytes[2 * h]) | (nibbles_from_bytes(bytes[2 * h + 1]) << 16);
+        for (int k = 0; k < E / 8; ++k) {
+          uint32_t plane[2] = {0u, 0u};
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            float q[4];
+            chain_quotients4<SRC>(&x[u][8 * k + 4 * h], mn, s, y, q);
+            codes_to_planes4(q, h, plane);
+          }
+          w[k] = pack4(plane);
+        }
         if (E == 8) *(uint32_t*)out = w[0];
         else *(uint2*)out = make_uint2(w[0], w[1]);
       } else {
+        uint32_t bytes[E / 4];
+#pragma unroll
+        for (int h = 0; h < E / 4; ++h) {
+          float q[4];
+          chain_quotients4<SRC>(&x[u][4 * h], mn, s, y, q);
+          bytes[h] = codes_as_bytes(q);
+        }
         if (E == 8) *(uint2*)out = make_uint2(bytes[0], bytes[1]);
         else *(uint4*)out = make_uint4(bytes[0], bytes[1], bytes[2], bytes[3]);
       }
@@ -1107,22 +1148,36 @@ __global__ void __launch_bounds__(kThreads) quantize_key_pages_fast(KeyParams k,
 #pragma unroll
       for (int j = 0; j < tpd; ++j)
         xs[j] = tile_x<SRC>(tile, FULL ? tb + j : min(tb + j, T - 1), c);  // padding repeats the last token
-      lo[w] = 0;
       hi[w] = 0;
-      // four tokens' codes at a time as bytes (codes_as_bytes: qmax is 3 or
-      // 15 here, or the byte range for 8-bit keys), then packed
-#pragma unroll
-      for (int g = 0; g < tpd / 4; ++g) {
+      // four tokens' codes at a time, each conversion writing its code at its
+      // byte of the packed layout (qmax is 3 or 15 here, or the byte range
+      // for 8-bit keys), then the fields combined
+      if (BITS == 8) {
         float q[4];
-        chain_quotients4<SRC>(&xs[4 * g], mn, s, y, q);
-        const uint32_t b = codes_as_bytes(q);
-        if (BITS == 8) {
-          lo[w] = b;
-        } else if (BITS == 4) {
-          lo[w] |= nibbles_from_bytes(b) << (16 * g);
+        chain_quotients4<SRC>(xs, mn, s, y, q);
+        lo[w] = codes_as_bytes(q);
+      } else if (BITS == 4) {
+        uint32_t plane[2] = {0u, 0u};
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          float q[4];
+          chain_quotients4<SRC>(&xs[4 * g], mn, s, y, q);
+          codes_to_planes4(q, g, plane);
+        }
+        lo[w] = pack4(plane);
+      } else {
+        uint32_t plane[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float q[4];
+          chain_quotients4<SRC>(&xs[4 * g], mn, s, y, q);
+          codes_to_planes2(q, g, plane);
+        }
+        if (mixed) {  // codes up to 15: low and high two bits
+          lo[w] = pack2_low(plane);
+          hi[w] = pack2_high(plane);
         } else {
-          lo[w] |= pairs_from_bytes(b & 0x03030303u) << (8 * g);
-          hi[w] |= pairs_from_bytes((b >> 2) & 0x03030303u) << (8 * g);
+          lo[w] = pack2(plane);
         }
       }
     }
