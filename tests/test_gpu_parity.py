@@ -355,6 +355,38 @@ def test_config2_decode_vs_oracle(seed, dtype):
             assert bits_equal(a.cpu(), b)
 
 
+@pytest.mark.parametrize("kb,vb,vg,dtype", [
+    (2, 2, 64, torch.bfloat16),   # 16 value codes per lane
+    (4, 4, 32, torch.bfloat16),
+    (8, 8, 16, torch.float16),
+    (2, 8, 8, torch.bfloat16),    # value group 8: 8 value codes per lane
+    (4, 2, 8, torch.float16),
+    (8, 4, 8, torch.bfloat16),
+])
+def test_uniform_pages_bit_exact_vs_oracle(kb, vb, vg, dtype):
+    """Uniform key pages (one token group per 128-token page, the single-pass key kernel) and value rows
+    of every width, bit for bit against the oracle, for value groups that give 16 and 8 codes per lane."""
+    _dkv()
+    from dartkv_amd import synthetic
+    from oracle import dart_oracle as O
+    import dartkv_amd as dart
+    cfg = dict(bits=kb, key_bits=kb, value_bits=vb, page_size=128, key_group_size=128, value_group_size=vg,
+               promote_ratio=0.0, sink_tokens=32, hold_partial_pages=True, metadata_dtype=torch.float16)
+    k, v, _ = synthetic.outlier_kv(2, 4, 700, 128, dtype=dtype, seed=70 + kb + vb)
+    print("uniform pages", kb, vb, vg, dtype, flush=True)
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    oc.append(k, v)
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    cache.append(k.to(DEV), v.to(DEV))
+    torch.cuda.synchronize()
+    assert len(cache.iter_segments()) == len(oc.segments()) == 7
+    for (ks, vs), (oks, ovs) in zip(cache.iter_segments(), oc.segments()):
+        for x, y in zip(_seg_fields(ks).values(), _seg_fields(oks).values()):
+            assert bits_equal(x.cpu(), y)
+        for x, y in zip(_seg_fields(vs).values(), _seg_fields(ovs).values()):
+            assert bits_equal(x.cpu(), y)
+
+
 def _oracle_and_cache(B, Hkv, Hq, T, dtype, seed, **over):
     import dartkv_amd as dart
     from dartkv_amd import synthetic
