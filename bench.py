@@ -1,14 +1,15 @@
 """Benchmark: packed-KV single-token decode attention on a Qwen3-8B-shaped cache.
 
-Workload: batch 64, 32768-token context per
+Workload (config C5, the headline decode configuration): batch 64, 32768-token context per
 sequence, 8 KV heads, 32 query heads, head_dim 128, bf16 K/V with 8 outlier
 channels per KV head, page 128, key group 128, value group 64, 2-bit codes
 with 25 % key-channel promotion, 32 sink tokens, held tail; 36 layers of
 packed cache resident in HBM, each layer a separate cache.
 
 One step = one decode token for all 64 sequences through all 36 layers:
-36 calls of the decode attention (MFMA page kernel, dense sink/tail kernel,
-split merge); ``--bits 4b`` runs the 4-bit uniform variant.  ``value`` is
+36 calls of the decode attention (MFMA page kernel with the dense sink/tail
+chunks in its launch, split merge); ``--bits 4b`` runs the 4-bit uniform
+variant.  ``value`` is
 the algorithmic bytes those calls must read and write (packed pages, dense
 sink and tail, query, output) per second of the whole step.  ``roofline`` is
 the page kernel alone: its pages' bytes over its mean duration, timed with
