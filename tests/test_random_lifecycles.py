@@ -109,3 +109,73 @@ def test_random_lifecycle_vs_oracle(seed):
     e1, e2 = _rel_err(out1.unsqueeze(2), ref1), _rel_err(out2, ref2)
     print("rel err one token", e1, "two tokens", e2, flush=True)
     assert e1 <= tol and e2 <= tol, (seed, e1, e2)
+
+
+def _fast_case(seed: int) -> dict:
+    r = random.Random(7000 + seed)
+    uniform = r.random() < 0.4
+    cfg = dict(page_size=128, key_group_size=128, value_group_size=r.choice([16, 32, 64, 128]),
+               sink_tokens=r.choice([0, 32]), hold_partial_pages=r.random() < 0.7, metadata_dtype=torch.float16)
+    if uniform:
+        cfg.update(bits=r.choice([2, 4, 8]), key_bits=r.choice([2, 4, 8]), value_bits=r.choice([2, 4, 8]),
+                   promote_ratio=0.0)
+    else:
+        cfg.update(bits=2, promote_ratio=r.choice([0.125, 0.25, 0.375, 0.5]),
+                   channel_selection=r.choice(["magnitude", "variance"]))
+    B, Hkv = r.choice([(1, 1), (1, 2), (1, 4), (2, 2), (2, 4), (1, 8)])
+    total = r.randint(300, 1000)
+    first = r.randint(1, total)
+    updates = [first] + [1] * min(total - first, 3)
+    updates += [total - sum(updates)] if total > sum(updates) else []
+    return dict(B=B, Hkv=Hkv, G=r.choice([1, 2, 4, 8]), Q=r.choice([1, 1, 2, 3]),
+                dtype=r.choice([torch.bfloat16, torch.float16]), cfg=cfg, updates=updates)
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_page_kernel_caches_vs_oracle(seed):
+    """Caches in the page kernels' layout (head_dim 128, 128-token pages, one key group per page, fp16
+    metadata, 16-bit K/V): random Dart promotion counts or uniform bit widths, value groups, GQA ratios,
+    sinks, held pages, lengths and query token counts; the page kernels must take the page run."""
+    import dartkv_amd as dart
+    from dartkv_amd import _lib, synthetic
+    from dartkv_amd.attention import _multi_token_attention
+    from oracle import dart_oracle as O
+    _lib.load()
+    c = _fast_case(seed)
+    B, Hkv, dtype, cfg, Q = c["B"], c["Hkv"], c["dtype"], c["cfg"], c["Q"]
+    Hq, D = Hkv * c["G"], 128
+    total = sum(c["updates"])
+    print("case", seed, B, Hkv, Hq, Q, dtype, cfg, c["updates"], flush=True)
+    k, v, _ = synthetic.outlier_kv(B, Hkv, total, D, query_heads=Hq, dtype=dtype, seed=2000 + seed)
+    q = torch.randn(B, Hq, Q, D, generator=torch.Generator().manual_seed(seed)).to(dtype)
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    cache = dart.DartKVCache(dart.DartKVCacheConfig(**cfg))
+    kd, vd = k.to(DEV), v.to(DEV)
+    start = 0
+    for n in c["updates"]:
+        oc.append(k[..., start:start + n, :], v[..., start:start + n, :])
+        cache.append(kd[..., start:start + n, :], vd[..., start:start + n, :])
+        start += n
+    torch.cuda.synchronize()
+    segs, osegs = cache.iter_segments(), oc.segments()
+    assert len(segs) == len(osegs)
+    for i, ((ks, vs), (oks, ovs)) in enumerate(zip(segs, osegs)):
+        for side, a, b in (("key", ks, oks), ("value", vs, ovs)):
+            for x, y in zip(_fields(a), _fields(b)):
+                assert bits_equal(x.cpu(), y), (seed, i, side)
+    plan = cache.decode_plan(torch.device(DEV))
+    full_pages = sum(1 for s, _ in osegs if not isinstance(s, torch.Tensor) and O.seg_tokens(s) == 128)
+    # the page kernels take the longest run of full pages (partial pages of unheld appends split runs)
+    assert 0 < plan.fast_count <= full_pages if full_pages else plan.fast_count == 0, (plan.fast_count, full_pages)
+    ref = O.streamed_attention(q, oc, return_fp32=True)[1]
+    out = torch.empty(B, Hq, Q, D, dtype=torch.float32, device=DEV)
+    if Q == 1:
+        o1 = torch.empty(B, Hq, D, dtype=torch.float32, device=DEV)
+        dart.decode_attention(q.to(DEV), cache, out_f32=o1)
+        out = o1.unsqueeze(2)
+    else:
+        _multi_token_attention(q.to(DEV), cache, out_f32=out)
+    torch.cuda.synchronize()
+    err = _rel_err(out, ref)
+    print("rel err", err, "fast pages", plan.fast_count, flush=True)
+    assert err <= 2e-3, (seed, err)
