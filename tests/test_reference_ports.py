@@ -466,16 +466,16 @@ def test_fused_attention_page_run_matches_per_page_kernel():
 @pytest.mark.parametrize("side,bad,promote", [("key", float("nan"), 0.25), ("key", float("inf"), 0.0),
                                               ("value", float("-inf"), 0.25), ("value", float("nan"), 0.0),
                                               ("key", float("nan"), 0.0)])
-@pytest.mark.parametrize("head_dim", [128, 12])
-def test_non_finite_page_inputs_raise_like_the_reference(side, bad, promote, head_dim):
+@pytest.mark.parametrize("head_dim,dtype", [(128, torch.bfloat16), (12, torch.bfloat16), (32, torch.float64)])
+def test_non_finite_page_inputs_raise_like_the_reference(side, bad, promote, head_dim, dtype):
     """A NaN or an infinity in a token that is quantized raises the reference's ValueError
     (mixed keys: mixed.py:187-188; uniform keys and values: quantization.py:159-160); the cache
     is left as it was, and a finite append afterwards works.  Head dims 128 and 12 reach the
-    single-pass and the general key kernels."""
+    single-pass and the general key kernels; float64 caches the double-precision kernels."""
     cfg = DartKVCacheConfig(bits=2, page_size=16, key_group_size=16, value_group_size=4, promote_ratio=promote,
                             sink_tokens=2, hold_partial_pages=True, metadata_dtype=torch.float16)
     torch.manual_seed(9)
-    keys = torch.randn(2, 2, 40, head_dim, device=DEV, dtype=torch.bfloat16)
+    keys = torch.randn(2, 2, 40, head_dim, device=DEV, dtype=dtype)
     values = torch.randn_like(keys)
     cache = DartKVCache(cfg)
     cache.update(keys[..., :20, :], values[..., :20, :])
