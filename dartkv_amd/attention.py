@@ -12,6 +12,7 @@
 
 from __future__ import annotations
 
+import collections
 import ctypes
 import math
 import os
@@ -71,20 +72,31 @@ def _fast_enabled() -> bool:
     return os.environ.get("DKV_FORCE_GENERAL", "0") in ("", "0")
 
 
-_workspaces: dict = {}
+_workspaces: "collections.OrderedDict[tuple, torch.Tensor]" = collections.OrderedDict()
+_MAX_WORKSPACES = 8  # (device, stream) pairs whose workspace is kept; the least recently used goes first
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """A decode workspace for the split records: one per device and stream, kept and grown as needed (calls
-    on one stream run in order, so they can share it).  Under graph capture a fresh one, which the graph
-    keeps."""
+    on one stream run in order, so they can share it).  At most ``_MAX_WORKSPACES`` are kept (least recently
+    used dropped first; the caching allocator reuses a dropped one once the stream's work has run) and
+    ``release_workspaces`` drops them all.  Under graph capture a fresh one, which the graph keeps."""
     if torch.cuda.is_current_stream_capturing():
         return torch.empty(nbytes, dtype=torch.uint8, device=device)
     key = (device.index, _lib.stream_ptr(device))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = _workspaces[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        while len(_workspaces) > _MAX_WORKSPACES:
+            _workspaces.popitem(last=False)
+    _workspaces.move_to_end(key)
     return ws
+
+
+def release_workspaces() -> None:
+    """Drop the kept decode workspaces (their memory returns to torch's caching allocator, so
+    ``torch.cuda.empty_cache`` can free it)."""
+    _workspaces.clear()
 
 
 def _call_layout(plan, cache: DartKVCache, q3: torch.Tensor, kv_heads: int, head_dim: int, tail, use_fast: bool,

@@ -143,8 +143,17 @@ def _nonfinite_flags(device: torch.device) -> torch.Tensor:
         flags = _flag_store.flags = {}
     t = flags.get(device)
     if t is None:
-        t = flags[device] = torch.zeros(2, dtype=torch.int32, pin_memory=True)
+        with torch.inference_mode(False):  # updated in place whatever mode a later append runs in
+            t = flags[device] = torch.zeros(2, dtype=torch.int32, pin_memory=True)
     return t
+
+
+def _storage(shape, dtype: torch.dtype, device) -> torch.Tensor:
+    """Uninitialized storage a cache keeps and updates in place across calls.  It is allocated as a
+    normal tensor even inside ``torch.inference_mode()`` (an inference tensor could not be updated in
+    place by a later call made outside that mode)."""
+    with torch.inference_mode(False):
+        return torch.empty(shape, dtype=dtype, device=device)
 
 
 class _FiniteScope:
@@ -313,8 +322,8 @@ class DartKVCache:
                     # the dense sink tokens precede this append's pages (every earlier token is a sink
                     # token too); they are copied after the quantize launches, which then start sooner
                     ks, vs = key_states[..., :sink, :], value_states[..., :sink, :]
-                    kd = torch.empty(ks.shape, dtype=ks.dtype, device=ks.device)
-                    vd = torch.empty(vs.shape, dtype=vs.dtype, device=vs.device)
+                    kd = _storage(ks.shape, ks.dtype, ks.device)
+                    vd = _storage(vs.shape, vs.dtype, vs.device)
                     self._copy_tokens((kd, ks), (vd, vs))
                     self._keys.insert(at_keys, kd)
                     self._values.insert(at_values, vd)
@@ -561,8 +570,9 @@ class DartKVCache:
                 self._tail_key.copy_(self._tail_key.index_select(0, index))
                 self._tail_value.copy_(self._tail_value.index_select(0, index))
             else:
-                self._tail_key = self._tail_key.index_select(0, index)
-                self._tail_value = self._tail_value.index_select(0, index)
+                with torch.inference_mode(False):  # kept and updated in place by later calls
+                    self._tail_key = self._tail_key.index_select(0, index)
+                    self._tail_value = self._tail_value.index_select(0, index)
                 self._tail_job = None
         if in_tail:
             n = self._pending_key.shape[-2]
@@ -624,8 +634,8 @@ class DartKVCache:
         if self._tail_key is None or self._tail_key.device != keys.device:
             B, H, _, D = keys.shape
             cap = self._tail_capacity()
-            self._tail_key = torch.empty(B, H, cap, D, dtype=keys.dtype, device=keys.device)
-            self._tail_value = torch.empty(B, H, cap, D, dtype=values.dtype, device=values.device)
+            self._tail_key = _storage((B, H, cap, D), keys.dtype, keys.device)
+            self._tail_value = _storage((B, H, cap, D), values.dtype, values.device)
         self._copy_tokens((self._tail_key[..., :n, :], keys), (self._tail_value[..., :n, :], values))
         self._pending_key = self._tail_key[..., :n, :]
         self._pending_value = self._tail_value[..., :n, :]
@@ -748,6 +758,13 @@ class DartKVCache:
             pool = getattr(last, "_pool", None)
             if pool is not None and pool is self._key_pool and last._at == pool.used - 1:
                 pool.used -= 1  # the page is packed again into the same slot
+                if self._finite_scope is not None:
+                    # a failed check later in this append puts the slot's first packing back (packing
+                    # dequantized values again is not idempotent in 16-bit dtypes)
+                    at = last._at
+                    saved = {name: pool.field(name, at).clone() for name in pool.tensors}
+                    self._finite_scope.undo.append(
+                        lambda: [pool.field(name, at).copy_(t) for name, t in saved.items()])
             self._seal_keys(dense)
         if self._pending_key is not None:
             keys = torch.cat((self._pending_key, keys), dim=-2)
@@ -981,13 +998,14 @@ class DartKVCache:
         if self._tail_key is None:
             B, H, D = self._shape
             cap = self._tail_capacity()
-            self._tail_key = torch.empty(B, H, cap, D, dtype=self._dtype, device=self._device)
-            self._tail_value = torch.empty(B, H, cap, D, dtype=self._dtype, device=self._device)
+            self._tail_key = _storage((B, H, cap, D), self._dtype, self._device)
+            self._tail_value = _storage((B, H, cap, D), self._dtype, self._device)
         if self._pending_key is not None and not self._pending_in_tail():
             self._store_pending(self._pending_key, self._pending_value)
             if not self._pending_in_tail():
                 raise RuntimeError("the held tail does not fit the tail buffer")
-        self._tail_count_dev = torch.zeros(1, dtype=torch.int64, device=self._device)
+        self._tail_count_dev = _storage((1,), torch.int64, self._device)
+        self._tail_count_dev.zero_()
         self._sync_device_tail()
         self._sealed_version += 1
 

@@ -62,7 +62,8 @@ class PagePool:
         for name, shape in self.shapes.items():
             full = list(shape)
             full[self.axis] = capacity
-            t = torch.empty(full, dtype=self.dtypes[name], device=self.device)
+            with torch.inference_mode(False):  # kept and updated in place across calls in any mode
+                t = torch.empty(full, dtype=self.dtypes[name], device=self.device)
             old = self.tensors.get(name)
             if old is not None and self.used:
                 t.narrow(self.axis, 0, self.used).copy_(old.narrow(self.axis, 0, self.used))
@@ -88,12 +89,13 @@ class PagePool:
         With the batch size unchanged the gather lands in the same tensors, so descriptors stay valid."""
         index = index.to(self.device)
         same = index.numel() == self.batch
-        for name, t in self.tensors.items():
-            picked = t.index_select(self.batch_axis, index)
-            if same:
-                t.copy_(picked)
-            else:
-                self.tensors[name] = picked
+        with torch.inference_mode(False):  # new pool tensors are kept and updated in place in any mode
+            for name, t in self.tensors.items():
+                picked = t.index_select(self.batch_axis, index)
+                if same:
+                    t.copy_(picked)
+                else:
+                    self.tensors[name] = picked
         if not same:
             for name, shape in self.shapes.items():
                 s = list(shape)
@@ -102,7 +104,8 @@ class PagePool:
             self.generation += 1
 
     def to(self, device: torch.device) -> None:
-        self.tensors = {name: t.to(device) for name, t in self.tensors.items()}
+        with torch.inference_mode(False):
+            self.tensors = {name: t.to(device) for name, t in self.tensors.items()}
         self.device = device
         self.generation += 1
 

@@ -18,6 +18,7 @@ Python control flow, which ends a compiled region anyway.
 
 from __future__ import annotations
 
+import itertools
 import weakref
 from typing import Optional, Tuple
 
@@ -31,14 +32,20 @@ from .cache import DartKVCache
 Tensor = torch.Tensor
 
 _caches: "weakref.WeakValueDictionary[int, DartKVCache]" = weakref.WeakValueDictionary()
+_handles: "weakref.WeakKeyDictionary[DartKVCache, int]" = weakref.WeakKeyDictionary()
+_next_handle = itertools.count(1)
 
 
 def cache_handle(cache: DartKVCache) -> int:
-    """Integer naming ``cache`` for ``torch.ops.dartkv.decode_attention`` (valid while it lives)."""
+    """Integer naming ``cache`` for ``torch.ops.dartkv.decode_attention`` (valid while it lives).  Handles
+    come from a counter and are never reused, so a graph that keeps the handle of a cache that has since
+    been freed gets 'unknown handle' rather than another cache."""
     if not isinstance(cache, DartKVCache):
         raise TypeError("cache_handle expects a DartKVCache")
-    handle = id(cache)
-    _caches[handle] = cache
+    handle = _handles.get(cache)
+    if handle is None:
+        handle = _handles[cache] = next(_next_handle)
+        _caches[handle] = cache
     return handle
 
 

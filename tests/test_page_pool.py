@@ -65,10 +65,20 @@ def test_reorder_batch_gathers_packed_bytes(index, over):
     expected = out_before.index_select(0, idx).cpu()
     if len(index) == 3:  # same batch size, same split counts: the same arithmetic
         assert bits_equal(out_after.cpu(), expected)
-    else:  # another batch size may choose other split counts (fp16 rounding of the weights differs)
-        err = float(((out_after.float().cpu() - expected.float()).abs().amax(-1) /
-                     expected.float().abs().amax(-1)).max())
-        assert err <= 1e-2, err
+    else:  # another batch size may choose other split counts: held to the parity bar against the oracle
+        from oracle import dart_oracle as O
+        cfg = dict(bits=2, page_size=128, key_group_size=128, value_group_size=64, promote_ratio=0.25,
+                   sink_tokens=32, hold_partial_pages=True, metadata_dtype=torch.float16)
+        cfg.update(over)
+        qi = q.index_select(0, idx)
+        out32 = torch.empty(len(index), qi.shape[1], 128, dtype=torch.float32, device=DEV)
+        dart.decode_attention(qi, cache, out_f32=out32)
+        oc = O.OracleCache(O.OracleConfig(**cfg))
+        oc.append(k.index_select(0, idx).cpu(), v.index_select(0, idx).cpu())
+        _, ref32 = O.streamed_attention(qi.cpu(), oc, return_fp32=True)
+        a, b = out32.cpu(), ref32.reshape(out32.shape)
+        err = float(((a - b).abs().amax(-1) / b.abs().amax(-1)).max())
+        assert err <= 2e-3, err
     assert cache.shape[0] == len(index)
     # appends after a reorder keep working: one token, then enough to seal a page
     nk, nv = k[:1, :, :200].expand(len(index), -1, -1, -1).contiguous(), v[:1, :, :200].expand(len(index), -1, -1, -1).contiguous()

@@ -537,6 +537,80 @@ def test_failed_append_leaves_sink_tail_and_device_count_as_they_were(first):
 
 
 @gpu
+def test_failed_kitty_append_restores_the_key_page_packed_again_in_its_slot():
+    """Kitty key window (local_tokens 1) after a prefill that ends on a page boundary: the next one-token
+    append packs the last key page again, from its dequantized values, into the same pool slot.  When a
+    value packed later in that append is non-finite (a NaN in the value window), the append raises and
+    the slot must hold its first packing again: packing dequantized 16-bit values twice is not
+    idempotent, so a retry from the second packing would drift from the reference."""
+    cfg = DartKVCacheConfig(bits=2, page_size=16, key_group_size=16, value_group_size=4, promote_ratio=0.25,
+                            local_tokens=1, value_local_tokens=4, metadata_dtype=torch.float16)
+    torch.manual_seed(11)
+    keys = torch.randn(2, 2, 33, 32, device=DEV, dtype=torch.bfloat16) * 3.1
+    values = torch.randn_like(keys)
+    values[1, 0, 28, 7] = float("nan")  # token 28: in the value window after the prefill, packed next
+    cache, clean = DartKVCache(cfg), DartKVCache(cfg)
+    for c in (cache, clean):
+        c.update(keys[..., :32, :], values[..., :32, :])
+    with pytest.raises(ValueError, match="finite"):
+        cache.update(keys[..., 32:33, :], values[..., 32:33, :])
+    assert cache.get_seq_length() == clean.get_seq_length() == 32
+
+    def packed(c):
+        out = []
+        for seg in c._keys:
+            if isinstance(seg, torch.Tensor):
+                out.append(seg)
+            else:
+                names = ("low_values", "high_values", "channel_indices", "scale", "zero_point", "values")
+                out += [getattr(seg, f) for f in names if isinstance(getattr(seg, f, None), torch.Tensor)]
+        return out
+
+    from tests.golden_util import bits_equal
+    # the premise: packing the last page again from its dequantized values changes its bytes, so a
+    # slot left holding the second packing would show below
+    last = clean._keys[-1]
+    again = dart.quantize_key_mixed(last.dequantize(), group_size=16, promote_ratio=0.25,
+                                    metadata_dtype=torch.float16)
+    assert not all(torch.equal(x, y) for x, y in zip(
+        (again.low_values, again.high_values, again.channel_indices, again.scale, again.zero_point),
+        (last.low_values, last.high_values, last.channel_indices, last.scale, last.zero_point)))
+    a, b = packed(cache), packed(clean)
+    assert len(a) == len(b) and len(a) > 0
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+    # the NaN token is still in both value windows: compare bits
+    assert all(bits_equal(x.cpu(), y.cpu()) for x, y in zip(cache.get(), clean.get()))
+
+
+@gpu
+def test_cache_filled_under_inference_mode_takes_later_calls_outside_it():
+    """A cache whose storage (pools, held tail, device tail count, dense sink) was created by appends
+    under ``torch.inference_mode()`` (a model's prefill) takes later appends, a failed append's restore,
+    device tail counts and batch reordering outside that mode: its storage is made of normal tensors."""
+    cfg = DartKVCacheConfig(bits=2, page_size=16, key_group_size=16, value_group_size=4, promote_ratio=0.25,
+                            sink_tokens=3, hold_partial_pages=True, metadata_dtype=torch.float16)
+    torch.manual_seed(21)
+    keys = torch.randn(2, 2, 90, 32, device=DEV, dtype=torch.bfloat16)
+    values = torch.randn_like(keys)
+    cache, clean = DartKVCache(cfg), DartKVCache(cfg)
+    with torch.inference_mode():
+        cache.update(keys[..., :40, :], values[..., :40, :])
+    clean.update(keys[..., :40, :], values[..., :40, :])
+    bad = keys[..., 40:70, :].clone()
+    bad[1, 0, 3, 9] = float("inf")
+    with pytest.raises(ValueError, match="finite"):
+        cache.update(bad, values[..., 40:70, :])
+    for c in (cache, clean):
+        c.update(keys[..., 40:70, :], values[..., 40:70, :])
+        c.enable_device_tail()
+        c.update(keys[..., 70:71, :], values[..., 70:71, :])
+        c.reorder_batch(torch.tensor([1, 0], device=DEV))
+        c.update(keys[..., 71:, :].flip(0).contiguous(), values[..., 71:, :].flip(0).contiguous())
+    assert cache.get_seq_length() == clean.get_seq_length() == 90
+    assert all(torch.equal(a, b) for a, b in zip(cache.get(), clean.get()))
+
+
+@gpu
 def test_non_finite_token_in_the_held_tail_is_kept_like_the_reference():
     """The reference checks only tokens it quantizes: a NaN that stays in the dense held tail raises
     nothing until a later append seals its page."""
