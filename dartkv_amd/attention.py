@@ -111,7 +111,9 @@ def _call_layout(plan, cache: DartKVCache, q3: torch.Tensor, kv_heads: int, head
     # the dense kernel takes the non-page segments (sink, tail) when they are
     # all dense: one record per 32-token chunk of each
     dense_tokens = 0
-    if use_fast and rest and group <= 8 and plan.rest_dense >= 0 and dense_ok:
+    # (more than 8 heads per KV head only as waves of the Dart page kernel's launch)
+    if (use_fast and rest and (group <= 8 or (fast_count and plan.fast_promoted)) and plan.rest_dense >= 0
+            and dense_ok):
         dense_tokens = max(plan.rest_dense, tail.tokens)
     if fast_count:
         # the uniform page kernel splits over half pages
@@ -263,8 +265,8 @@ def segment_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optiona
 
 
 def _fast_rows(plan) -> Tuple[int, ...]:
-    """Query rows per KV head the MFMA page kernels take (Dart and uniform pages alike)."""
-    return (1, 2, 4, 8)
+    """Query rows per KV head the MFMA page kernels take: up to 16 on Dart pages, 8 on uniform pages."""
+    return (1, 2, 4, 8, 16) if plan.fast_promoted else (1, 2, 4, 8)
 
 
 def _multi_token_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional[float] = None,
@@ -276,7 +278,7 @@ def _multi_token_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Op
     row of h's KV group.  A [B, Hq, c, D] slice of the query read as a
     [B, Hq * c, D] query keeps that grouping (row h * c + i belongs to KV head
     h // G), and the single-token HIP decode path runs it unchanged: the MFMA
-    page kernel while G * c fits its rows per KV head (4, or 8 on Dart pages:
+    page kernel while G * c fits its rows per KV head (8, or 16 on Dart pages:
     the dequantized pages serve all rows of a launch), the general kernel up to
     16.  ``out_f32`` ([B, Hq, Q, D] float32) receives the result before the cast.
     """
@@ -284,20 +286,23 @@ def _multi_token_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Op
     Hq, Q = query.shape[1], query.shape[-2]
     groups = Hq // kv_heads
     plan = cache.decode_plan(query.device)
-    rows = max(_fast_rows(plan)) if plan.fast_count > 0 and _fast_enabled() else 4
-    chunk = max(1, rows // groups) if groups <= rows else max(1, 16 // groups)
+    rows = _fast_rows(plan) if plan.fast_count > 0 and _fast_enabled() else (1, 2, 4)
+    fits = [c for c in range(1, Q + 1) if groups * c in rows]  # token counts a page-kernel launch takes
     if out_f32 is not None and (out_f32.shape != (batch, Hq, Q, head_dim) or out_f32.dtype != torch.float32):
         raise ValueError("out_f32 must be a float32 [B, Hq, Q, D] tensor")
     out = torch.empty(batch, Hq, Q, head_dim, dtype=query.dtype, device=query.device)
-    for start in range(0, Q, chunk):
-        c = min(chunk, Q - start)
-        rows = query[:, :, start:start + c].reshape(batch, Hq * c, head_dim)
+    start = 0
+    while start < Q:
+        left = [c for c in fits if c <= Q - start]
+        c = max(left) if left else min(Q - start, max(1, 16 // groups))
+        q_rows = query[:, :, start:start + c].reshape(batch, Hq * c, head_dim)
         o32 = None if out_f32 is None else torch.empty(batch, Hq * c, head_dim, dtype=torch.float32,
                                                        device=query.device)
-        o = decode_attention(rows, cache, scale=scale, out_f32=o32)
+        o = decode_attention(q_rows, cache, scale=scale, out_f32=o32)
         out[:, :, start:start + c] = o.reshape(batch, Hq, c, head_dim)
         if out_f32 is not None:
             out_f32[:, :, start:start + c] = o32.reshape(batch, Hq, c, head_dim)
+        start += c
     return out
 
 

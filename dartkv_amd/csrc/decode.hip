@@ -494,8 +494,8 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
               "fast page range outside the descriptor table");
     DKV_CHECK(a.D == 128, DKV_ERR_UNSUPPORTED, "fast page path needs head_dim 128");
     const int64_t gq = a.Hq / a.Hkv;
-    DKV_CHECK(gq == 1 || gq == 2 || gq == 4 || gq == 8, DKV_ERR_UNSUPPORTED,
-              "fast page path needs 1, 2, 4 or 8 query rows per KV head");
+    DKV_CHECK(gq == 1 || gq == 2 || gq == 4 || gq == 8 || (gq == 16 && a.fast_promoted > 0), DKV_ERR_UNSUPPORTED,
+              "fast page path needs 1, 2, 4 or 8 query rows per KV head (16 on Dart pages)");
     DKV_CHECK(a.cache_dtype == dkv::kBF16 || a.cache_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED,
               "fast page path needs a bf16 or fp16 cache");
     DKV_CHECK(a.meta_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED, "fast page path needs fp16 metadata");
@@ -549,8 +549,11 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
               "rest_dense_tokens needs n_splits == non-page segments * ceil(rest_dense_tokens / %d)", kDenseChunk);
     DKV_CHECK(a.cache_dtype == dkv::kBF16 || a.cache_dtype == dkv::kF16, DKV_ERR_UNSUPPORTED,
               "rest_dense_tokens needs a bf16 or fp16 cache");
-    DKV_CHECK(a.D == kDenseDim && p.group <= kDenseMaxGroup, DKV_ERR_UNSUPPORTED,
-              "rest_dense_tokens needs head_dim %d and at most %d query heads per KV head", kDenseDim, kDenseMaxGroup);
+    // up to kDenseMaxGroup heads per KV head in the dense kernels of their own; 16 only as waves of the
+    // Dart page kernel's launch
+    const int max_group = fast_count > 0 && a.fast_promoted > 0 ? kDenseFusedMaxGroup : kDenseMaxGroup;
+    DKV_CHECK(a.D == kDenseDim && p.group <= max_group, DKV_ERR_UNSUPPORTED,
+              "rest_dense_tokens needs head_dim %d and at most %d query heads per KV head", kDenseDim, max_group);
   }
   if (fast_count > 0) {
     // With a dense rest, the page kernel's launch also runs the dense chunks
@@ -561,6 +564,9 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
     // release writes back its L2.
     const bool fuse = dense_rest && B_Hkv_rest_chunks_ok(a, rest, chunks) &&
                       (size_t)2 * stride * sizeof(float) <= 64 * 1024;
+    DKV_CHECK(!dense_rest || fuse || p.group <= kDenseMaxGroup, DKV_ERR_UNSUPPORTED,
+              "rest_dense_tokens with more than %d query heads per KV head needs the dense chunks in the page "
+              "kernel's launch (too many splits)", kDenseMaxGroup);
     dkv::FusedRest fr{&p, (int)chunks};
     int rc = record_event(a.fast_events[0], s);
     if (rc) return rc;

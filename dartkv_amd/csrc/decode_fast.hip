@@ -3,10 +3,10 @@
 // Scope: head_dim 128, 128-token pages, keys with Dart promotion (2-bit codes
 // for every channel plus the upper 2 bits of NP promoted channels, one key
 // group per page), 2-bit values with groups of vg (16 | vg, vg | 128)
-// channels, fp16 metadata, bf16 or fp16 cache, 1, 2, 4 or 8 query rows per KV
-// head (8 rows: two row groups of 4, each with its own Q K MFMAs on the same
-// dequantized B operands; the multi-token path maps two tokens of a
-// 4-head group here).  Everything else goes through the general kernel
+// channels, fp16 metadata, bf16 or fp16 cache, 1, 2, 4, 8 or 16 query rows per
+// KV head (8 or 16 rows: two or four row groups of 4, each with its own Q K
+// MFMAs on the same dequantized B operands; the multi-token path maps two or
+// four tokens of a 4-head group here).  Everything else goes through the general kernel
 // (decode.hip).
 //
 // One wave owns one split: a contiguous range of pages of one (batch, kv
@@ -60,10 +60,10 @@ struct LdsMap {
   int kl, vc, kh, ki, ks, kz, vs, vz, klut, klut16, vlut, pidx, q16, qp, pt, zero, bytes;
 };
 
-// rg: row groups of 4 query rows (1, or 2 for 8 rows per KV head).  With two,
-// the promoted channels' query rows live in the softmax-weight region (which
-// is free from the weights' last read in P V until the softmax writes them)
-// and the query takes 8 rows.
+// rg: row groups of 4 query rows (1, or 2 / 4 for 8 / 16 rows per KV head).
+// With several, the promoted channels' query rows live in the softmax-weight
+// region (which is free from the weights' last read in P V until the softmax
+// writes them) and the query takes 4 rg rows.
 __host__ __device__ inline LdsMap lds_map(int np, int gv, int rg) {
   LdsMap m;
   int o = 0;
@@ -88,7 +88,7 @@ __host__ __device__ inline LdsMap lds_map(int np, int gv, int rg) {
     o = (o + 127) / 128 * 128;
   }
   m.pt = o; o += 4 * rg * kPtStride;       // softmax weights [4 rg][128 tok] fp16
-  if (rg != 1) m.qp = m.pt;                // [8][NP] fits: 8 kQpStride <= 8 kPtStride
+  if (rg != 1) m.qp = m.pt;                // [4 rg][NP] fits: kQpStride <= kPtStride
   o = (o + 127) / 128 * 128 + 64;
   m.zero = o; o += 256;                    // zeros read by A-operand lanes without data
   o = (o + 15) / 16 * 16;
@@ -243,27 +243,34 @@ __device__ __forceinline__ void lut_block_operands(const uint32_t x[4], const ui
 }
 
 
-// GQ: query rows per KV head (1, 2, 4 or 8); NP: promoted channels (16, 32,
-// 48 or 64); BF16: cache dtype bf16 (else fp16).  All compile-time, so every
-// block loop unrolls with immediate offsets and the table builds carry no
-// dtype tests.  Rows come in RG groups of GH: each group has its own Q K
-// MFMAs (the slot layout holds 4 rows), with 8 rows the groups' A operands are
-// formed per MFMA from one 2-byte LDS read each (two register sets would not
-// fit; four reads per operand, three of zeros, stalled on LDS issue), as are
-// the promoted pass's for any row count, and P V takes all rows in one MFMA
-// (rows 4g + i: lane group kq = g holds group g's outputs).
+// Row groups of 4 query rows for GQ rows per KV head, and waves per workgroup:
+// one-wave workgroups for 16 rows, whose LDS region (about 24 KB) leaves room
+// for six waves per CU but not for two four-wave workgroups.
+__host__ __device__ constexpr int fast_row_groups(int gq) { return gq > 4 ? gq / 4 : 1; }
+__host__ __device__ constexpr int fast_waves_per_block(int gq) { return gq > 8 ? 1 : kWaves; }
+
+// GQ: query rows per KV head (1, 2, 4, 8 or 16); NP: promoted channels (16,
+// 32, 48 or 64); BF16: cache dtype bf16 (else fp16).  All compile-time, so
+// every block loop unrolls with immediate offsets and the table builds carry
+// no dtype tests.  Rows come in RG groups of GH: each group has its own Q K
+// MFMAs (the slot layout holds 4 rows), with 8 or 16 rows the groups' A
+// operands are formed per MFMA from one 2-byte LDS read each (several register
+// sets would not fit; four reads per operand, three of zeros, stalled on LDS
+// issue), as are the promoted pass's for any row count, and P V takes all rows
+// in one MFMA (rows 4g + i: lane group kq = g holds group g's outputs).
 template <int GQ, int NP, bool BF16>
-__global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
+__global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
+    decode_pages_fast(FastParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, kq = lane >> 4;
-  const int worker = blockIdx.x * kWaves + wave;
+  const int worker = blockIdx.x * fast_waves_per_block(GQ) + wave;
   const int total_workers = p.B * p.Hkv * p.splits;
   constexpr int np = NP;
   constexpr bool bf16 = BF16;
-  constexpr int RG = GQ > 4 ? 2 : 1, GH = GQ > 4 ? 4 : GQ;
-  static_assert(GQ == 1 || GQ == 2 || GQ == 4 || GQ == 8, "1, 2, 4 or 8 query rows per KV head");
+  constexpr int RG = fast_row_groups(GQ), GH = GQ > 4 ? 4 : GQ;
+  static_assert(GQ == 1 || GQ == 2 || GQ == 4 || GQ == 8 || GQ == 16, "1, 2, 4, 8 or 16 query rows per KV head");
   const int gv = p.gv;
   const LdsMap M = lds_map(np, gv, RG);
   uint8_t* lds = smem + wave * M.bytes;
@@ -524,7 +531,9 @@ __global__ void __launch_bounds__(256, 2) decode_pages_fast(FastParams p) {
 #pragma unroll
         for (int i = 0; i < GH; ++i) {
           // O row 4g + i sits in lane group kq = g (rows past GQ are zero)
-          const float al = RG == 1 ? alpha[0][i] : (kq == 1 ? alpha[RG - 1][i] : alpha[0][i]);
+          float al = alpha[0][i];
+#pragma unroll
+          for (int g = 1; g < RG; ++g) al = kq == g ? alpha[g][i] : al;
 #pragma unroll
           for (int j = 0; j < 8; ++j) O[j][i] *= al;
         }
@@ -613,7 +622,7 @@ namespace dkv {
 int fast_decode_max_loads(int np, int gv) { return n_small_loads(np, gv) + n_key_loads(np); }
 
 size_t fast_decode_lds_bytes(int np, int gv, int gq) {
-  return (size_t)kWaves * lds_map(np, gv, gq > 4 ? 2 : 1).bytes;
+  return (size_t)fast_waves_per_block(gq) * lds_map(np, gv, fast_row_groups(gq)).bytes;
 }
 
 int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, int vg, int splits, int split_stride,
@@ -640,9 +649,10 @@ int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, i
   p.ws = (float*)a.workspace;
   set_fused(p, fused);
   const int64_t workers = (int64_t)p.B * p.Hkv * splits + p.dense_workers;
-  const unsigned blocks = (unsigned)((workers + kWaves - 1) / kWaves);
+  const int wpb = fast_waves_per_block(p.GQ);
+  const unsigned blocks = (unsigned)((workers + wpb - 1) / wpb);
   const size_t lds = fast_decode_lds_bytes(np, p.gv, p.GQ);
-  const dim3 grid(blocks), block(256);
+  const dim3 grid(blocks), block(64 * wpb);
 #define DKV_FAST_LAUNCH(G, N)                                                                  \
   do {                                                                                         \
     if (p.bf16) hipLaunchKernelGGL((decode_pages_fast<G, N, true>), grid, block, lds, stream, p);  \
@@ -664,8 +674,9 @@ int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, i
     case 2: DKV_FAST_NP(2); break;
     case 4: DKV_FAST_NP(4); break;
     case 8: DKV_FAST_NP(8); break;
+    case 16: DKV_FAST_NP(16); break;
     default:
-      set_error("fast decode supports 1, 2, 4 or 8 query rows per KV head");
+      set_error("fast decode supports 1, 2, 4, 8 or 16 query rows per KV head");
       return DKV_ERR_UNSUPPORTED;
   }
 #undef DKV_FAST_NP

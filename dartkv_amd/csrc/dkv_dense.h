@@ -41,7 +41,8 @@ __device__ __forceinline__ dkv_segment general_segment(const DecodeParams& p, in
 constexpr int kDenseWaves = 4;
 constexpr int kDenseChunk = 32;
 constexpr int kDenseDim = 128;
-constexpr int kDenseMaxGroup = 8;
+constexpr int kDenseMaxGroup = 8;        // the dense kernels of their own (decode.hip)
+constexpr int kDenseFusedMaxGroup = 16;  // dense chunk waves inside the Dart page kernel's launch
 
 // Every head slot of the dense kernel computes (the query of slots >= G is
 // zero), so the unrolled loops carry no per-head branches; only the record

@@ -114,8 +114,12 @@ def _seg_fields(seg):
 
 
 @pytest.mark.parametrize("Hkv,Hq,Q,dtype,uniform", [
-    (8, 32, 3, torch.bfloat16, False),   # G 4: two tokens per launch, then one (MFMA page kernel, 8 and 4 rows)
+    (8, 32, 3, torch.bfloat16, False),   # G 4: two tokens (8 rows), then one (4 rows)
+    (8, 32, 4, torch.bfloat16, False),   # G 4: four tokens in one launch (16 rows)
+    (8, 32, 8, torch.float16, False),    # G 4: two launches of four tokens
     (4, 16, 3, torch.bfloat16, True),    # G 4 on uniform 4-bit pages: two tokens, then one
+    (4, 16, 4, torch.bfloat16, True),    # G 4 on uniform pages: two launches of two tokens
+    (4, 16, 8, torch.float16, True),     # G 4 on uniform pages: four launches of two tokens
     (2, 4, 5, torch.float16, True),      # G 2 on uniform pages: four tokens, then one
 ])
 def test_multi_token_attention_vs_oracle_by_page_kind(Hkv, Hq, Q, dtype, uniform):
@@ -145,11 +149,13 @@ def test_multi_token_attention_vs_oracle_by_page_kind(Hkv, Hq, Q, dtype, uniform
 
 
 @pytest.mark.parametrize("Hkv,Hq,Q,dtype", [
-    (8, 32, 3, torch.bfloat16),   # G 4: two tokens per launch, then one (MFMA page kernel, 8 and 4 rows)
-    (8, 32, 4, torch.float16),    # G 4: two launches of two tokens
-    (4, 8, 5, torch.bfloat16),    # G 2: four tokens per launch, then one
+    (8, 32, 3, torch.bfloat16),   # G 4: two tokens (8 rows), then one (4 rows)
+    (8, 32, 4, torch.float16),    # G 4: four tokens in one launch (16 rows)
+    (8, 32, 5, torch.bfloat16),   # G 4: four tokens, then one (16 and 4 rows)
+    (4, 8, 5, torch.bfloat16),    # G 2: four tokens (8 rows), then one
     (4, 4, 4, torch.float16),     # G 1: four tokens in one launch
-    (2, 16, 3, torch.bfloat16),   # G 8: one token per launch (8 rows)
+    (2, 16, 3, torch.bfloat16),   # G 8: two tokens per launch (16 rows), then one (8 rows)
+    (2, 32, 1, torch.bfloat16),   # G 16: one token, the 16-row page kernel
     (2, 6, 2, torch.bfloat16),    # G 3: general kernel
 ])
 def test_multi_token_attention_vs_oracle(Hkv, Hq, Q, dtype):
