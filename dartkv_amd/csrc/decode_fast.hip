@@ -109,26 +109,6 @@ __host__ __device__ inline int key_slot(int c) { return (c & ~7) | ((c & 3) << 1
 // lane's four tokens t, t + 4, t + 8, t + 12 are adjacent.
 __host__ __device__ inline int kpos(int t) { return (t & ~15) | ((t & 3) << 2) | ((t >> 2) & 3); }
 
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-
-// fp16 scale or zero point (bits in the low half of x) in both halves; as an
-// operand of a packed op this is an op_sel broadcast, not an instruction.
-__device__ __forceinline__ half2v splat_h(uint32_t x) {
-  const _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)x);
-  return half2v{h, h};
-}
-
-// Exact dequantized values for codes (c0, c1) of one (scale, zero) pair, as
-// an fp16 pair: fp16(fp16(code*s) + z), then bf16 precision if BF16.
-template <bool BF16>
-__device__ __forceinline__ uint32_t lut_pair(uint32_t codes_h2, half2v s, half2v z) {
-  const half2v c = __builtin_bit_cast(half2v, codes_h2);
-  const half2v prod = c * s;  // -ffp-contract=off keeps the multiply and the add separate
-  const half2v sum = prod + z;
-  uint32_t r = __builtin_bit_cast(uint32_t, sum);
-  return BF16 ? round_pair_to_bf16_precision(r) : r;
-}
-
 // Byte-plane table of the 4 values for codes 0..3: x = low bytes, y = high bytes.
 // For codes 0 and 1 the products 0 * s and 1 * s are exact, so one fused
 // multiply-add rounds once, exactly as fp16(fp16(code * s) + z) does; codes 2

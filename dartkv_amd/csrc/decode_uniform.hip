@@ -19,14 +19,21 @@
 //   * O += P V in the same slot layout (a lane's four B values are four
 //     channels of one token; A carries the weight at the lane's slot), two
 //     tiles of 64 channels.
-// Codes are dequantized arithmetically, exactly as the reference rounds: the
-// code exactly in fp16, then fp16(code * scale), fp16(+ zero) and, for bf16
-// caches, bf16 precision.  Codes below 16 become fp16 through the fp8
-// converter: the e4m3 pattern of a code c < 16 is c * 2^-9 (subnormals and
-// the first binade are evenly spaced), and the converter's power-of-two scale
-// 2^9 restores c.  8-bit codes use byte permutes under the fp16 exponent of
-// 1024 (0x64xx = 1024 + code) and subtract 1024.  Scales and zero points are
-// duplicated into (s, s, z, z) tables once per page (keys) or half (values).
+// 2- and 4-bit codes are dequantized by exact-value tables (with 1, 2 or 4
+// query rows; for values, with value groups of 64 or 128 channels): every key
+// channel's table (its 2^B values under the reference's rounding chain,
+// fp16(fp16(code * scale) + zero) and, for bf16 caches, bf16 precision) is
+// built once per page and every (token, value group)'s once per quarter page;
+// a B operand is then four 2-byte LDS gathers.  Each lane group of 16 reads
+// one 32-byte table (8 banks) and the four groups' tables sit in distinct
+// banks, so the gathers do not conflict.  Otherwise codes are dequantized
+// arithmetically with the same rounding chain: codes below 16 become fp16
+// through the fp8 converter (the e4m3 pattern of a code c < 16 is c * 2^-9:
+// subnormals and the first binade are evenly spaced, and the converter's
+// power-of-two scale 2^9 restores c), 8-bit codes through byte permutes
+// under the fp16 exponent of 1024 (0x64xx = 1024 + code) less 1024, with
+// scales and zero points duplicated into (s, s, z, z) tables once per page
+// (keys) or half (values).
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -46,13 +53,25 @@ struct UMap {
   int kc, vc, ks, kz, vs, vz, kt, vt, q16, pt, zero, bytes;
 };
 
+// Exact-value tables (32 bytes each, 2^B fp16 entries) for B-bit keys with
+// 1, 2 or 4 query rows, and for B-bit values as well when their groups are
+// 64 or 128 channels wide (at most two per token, so a quarter page's tables
+// fit beside the rest of the wave's LDS).
+__host__ __device__ constexpr bool key_tables(int kb, int gq) { return kb <= 4 && gq <= 4; }
+__host__ __device__ constexpr bool value_tables_ok(int vb, int gq) { return vb <= 4 && gq <= 4; }
+constexpr int kTable = 32;      // bytes per table
+constexpr int kQuarterTok = 32; // tokens whose value tables are built at a time
+
 // Key rows staged per page (2: both halves of every channel's 16 KB-byte row)
 // or per half page (1).  A half row is half a 128-byte line for 2- and 4-bit
 // keys; staging it per half would fetch the line again once L2 has dropped it.
 __host__ __device__ constexpr int key_rows_per_stage(int kb) { return kb <= 4 ? 2 : 1; }
 
-// rg: row groups of 4 query rows (the query and the softmax weights take 4 rg rows).
-__host__ __device__ inline UMap umap(int kb, int vb, int gv, int rg) {
+// rg: row groups of 4 query rows (the query and the softmax weights take 4 rg
+// rows); kt / vt: key / value tables (else (s, s, z, z) entries).  Tables
+// start on a 256-byte boundary (gather4 forms addresses by byte permutes) and
+// so does every wave's region when there are any.
+__host__ __device__ inline UMap umap(int kb, int vb, int gv, int rg, bool kt, bool vt) {
   UMap m;
   int o = 0;
   const int kf = key_rows_per_stage(kb);
@@ -62,14 +81,28 @@ __host__ __device__ inline UMap umap(int kb, int vb, int gv, int rg) {
   m.kz = o; o += 256;                  // key zero  [128] fp16
   m.vs = o; o += 128 * gv;             // value scale of the half [64 tok][Gv] fp16
   m.vz = o; o += 128 * gv;             // value zero  of the half [64 tok][Gv] fp16
-  m.kt = o; o += kD * 8;               // key (s, s, z, z) per channel [128] (fp16 pairs)
-  m.vt = o; o += kHalfTok * 8 * gv;    // value (s, s, z, z) of the half [64 tok][Gv]
-  m.q16 = o; o += 1024 * rg;           // query [4 rg][128 ch] fp16 (split start only, and per MFMA with 2 groups)
+  if (kt) {
+    o = (o + 255) / 256 * 256;
+    m.kt = o; o += kD * kTable;        // key tables [128 ch][2^KB] fp16
+  } else {
+    m.kt = o; o += kD * 8;             // key (s, s, z, z) per channel [128] (fp16 pairs)
+  }
+  if (vt) {
+    o = (o + 255) / 256 * 256;
+    m.vt = o; o += gv * kQuarterTok * kTable;  // value tables of a quarter page [Gv][32 tok][2^VB] fp16
+  } else {
+    m.vt = o; o += kHalfTok * 8 * gv;  // value (s, s, z, z) of the half [64 tok][Gv]
+  }
+  if (vt && rg == 1 && gv * kQuarterTok * kTable >= 1024) {
+    m.q16 = m.vt;                      // the query is read once, before any value table is built
+  } else {
+    m.q16 = o; o += 1024 * rg;         // query [4 rg][128 ch] fp16 (split start only, and per MFMA with 2 groups)
+  }
   o = (o + 127) / 128 * 128;
   m.pt = o; o += 4 * rg * kPtRow;      // softmax weights [4 rg][64 tok] fp16
   o = (o + 127) / 128 * 128 + 64;
   m.zero = o; o += 256;                // zeros read by A-operand lanes without data
-  m.bytes = (o + 15) / 16 * 16;
+  m.bytes = (kt || vt) ? (o + 255) / 256 * 256 : (o + 15) / 16 * 16;
   return m;
 }
 
@@ -150,7 +183,51 @@ __device__ __forceinline__ void build_sz_table(uint8_t* lds, int dst, int src_s,
     *(uint2*)(lds + dst + 8 * i) = make_uint2((uint32_t)s[i] * 0x10001u, (uint32_t)z[i] * 0x10001u);
 }
 
-template <int GQ, int KB, int VB, bool BF16>
+// Half h of the exact-value table of one (scale, zero) pair: codes
+// h 2^(B-1) .. (h + 1) 2^(B-1) - 1 (B = 2 or 4), written at dst.
+template <int B, bool BF16>
+__device__ __forceinline__ void build_table_half(uint8_t* lds, int dst, uint16_t s, uint16_t z, int h) {
+  const half2v s2 = splat_h(s), z2 = splat_h(z);
+  if constexpr (B == 4) {
+    uint32_t v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = lut_pair<BF16>(code_pair(q, h), s2, z2);
+    *(uint4*)(lds + dst + 16 * h) = make_uint4(v[0], v[1], v[2], v[3]);
+  } else {
+    *(uint32_t*)(lds + dst + 4 * h) = lut_pair<BF16>(code_pair(h, 0), s2, z2);  // codes (2h, 2h + 1)
+  }
+}
+
+// Key tables of a page: channel c's at kt + 32 c; item i is half i & 1 of channel i >> 1.
+template <int B, bool BF16>
+__device__ __forceinline__ void build_key_tables(const UMap& M, uint8_t* lds, int lane) {
+  const uint16_t* ks = (const uint16_t*)(lds + M.ks);
+  const uint16_t* kz = (const uint16_t*)(lds + M.kz);
+#pragma unroll
+  for (int i = lane; i < 2 * kD; i += 64) build_table_half<B, BF16>(lds, M.kt + kTable * (i >> 1), ks[i >> 1], kz[i >> 1], i & 1);
+}
+
+// Value tables of quarter page qr of the half: (token 32 qr + t, group g)'s
+// at vt + 1024 g + 32 t; item i is half i & 1 of table i >> 1 = 32 g + t.
+template <int B, bool BF16>
+__device__ __forceinline__ void build_value_tables(const UMap& M, uint8_t* lds, int gv, int qr, int lane) {
+  const uint16_t* vs = (const uint16_t*)(lds + M.vs);
+  const uint16_t* vz = (const uint16_t*)(lds + M.vz);
+  for (int i = lane; i < 2 * kQuarterTok * gv; i += 64) {
+    const int g = i >> 6, t = (i >> 1) & 31, src = (kQuarterTok * qr + t) * gv + g;
+    build_table_half<B, BF16>(lds, M.vt + kQuarterTok * kTable * g + kTable * t, vs[src], vz[src], i & 1);
+  }
+}
+
+// Byte j of the result = 2 x the B-bit code at bits [shift + 8 j, shift + 8 j + B)
+// of w, plus add (rot = (shift - 1) mod 32).
+template <int B>
+__device__ __forceinline__ uint32_t twice_code_bytes(uint32_t w, uint32_t rot, uint32_t add) {
+  const uint32_t mask = B == 4 ? 0x1e1e1e1eu : 0x06060606u;
+  return (__builtin_amdgcn_alignbit(w, w, rot) & mask) | add;
+}
+
+template <int GQ, int KB, int VB, bool BF16, bool VTAB>
 __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
   constexpr int RG = GQ > 4 ? 2 : 1, GH = GQ > 4 ? 4 : GQ;  // row groups of GH query rows
   static_assert(GQ == 1 || GQ == 2 || GQ == 4 || GQ == 8, "1, 2, 4 or 8 query rows per KV head");
@@ -159,8 +236,10 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, kq = lane >> 4;
   const int worker = blockIdx.x * kWaves + wave;
+  constexpr bool KT = key_tables(KB, GQ), VT = VTAB;  // exact-value tables for keys / values
+  static_assert(!VT || value_tables_ok(VB, GQ), "value tables need 2- or 4-bit values and at most 4 query rows");
   const int gv = p.gv;
-  const UMap M = umap(KB, VB, gv, RG);
+  const UMap M = umap(KB, VB, gv, RG, KT, VT);
   uint8_t* lds = smem + wave * M.bytes;
   if (worker >= p.B * p.Hkv * p.splits) {  // a dense-rest worker, or none
     dense_worker<GQ, BF16>(p, worker - p.B * p.Hkv * p.splits, lane, (float*)lds);
@@ -241,6 +320,15 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
   }
   const float c2 = ldexpf(p.scale * kLog2e, qexp);
   const uint32_t kmask = code_mask<KB>(), vmask = code_mask<VB>();
+  // table addressing: block cb's key tables at kt + 128 cb (the lane's channel
+  // 4 cb + kq at + 32 kq), token group tg's value tables of tile t at
+  // vt + 1024 vg_t + 128 (tg mod 8) (the lane's token at + 32 kq); the bases'
+  // low bytes are zero, byte j of a selector is 2 code_j + 32 kq
+  const uint32_t kq32 = 0x20202020u * (uint32_t)kq;
+  const uint32_t krot = (uint32_t)(kshift - 1) & 31u, vrot = (uint32_t)(vshift - 1) & 31u;
+  const uint32_t kt_base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.kt));
+  const uint32_t vt_base0 = (uint32_t)(uintptr_t)(lds_void*)(lds + M.vt + kQuarterTok * kTable * vg0);
+  const uint32_t vt_base1 = (uint32_t)(uintptr_t)(lds_void*)(lds + M.vt + kQuarterTok * kTable * vg1);
 
 #pragma unroll 1
   for (int hq = hp0; hq < hp1; ++hq) {
@@ -253,7 +341,8 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
     // outstanding, oldest first: key scales + codes (if staged for this half), values (this half)
     vm_wait(n_value_loads_u(VB));
     if (hq == hp0 || kf == 1 || (hq & 1) == 0) {  // keys staged for this half: their (s, s, z, z) table
-      build_sz_table(lds, M.kt, M.ks, M.kz, kD, lane);
+      if constexpr (KT) build_key_tables<KB, BF16>(M, lds, lane);
+      else build_sz_table(lds, M.kt, M.ks, M.kz, kD, lane);
       lds_sync();
     }
 
@@ -262,22 +351,33 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
 #pragma unroll
     for (int g = 0; g < RG; ++g) S[g] = float4v{0.f, 0.f, 0.f, 0.f};
     {
-      constexpr int kAhead = 2;
+      constexpr int kAhead = KT ? 3 : 2;  // code words read ahead (with tables: gathered two ahead)
       uint32_t w[kD / 4];
       uint2 sz[kD / 4];
+      half4 bk[kD / 4];  // with key tables: block cb's B operand, gathered one block ahead
       const int kh = krow + (kf == 2 ? 8 * KB * (hq & 1) : 0);
       auto load_cb = [&](int c) {
         w[c] = lds_u32(lds, kh + 32 * KB * kf * c);
-        sz[c] = *(const uint2*)(lds + M.kt + 8 * (4 * c + kq));
+        if constexpr (!KT) sz[c] = *(const uint2*)(lds + M.kt + 8 * (4 * c + kq));
       };
+      auto gather_cb = [&](int c) { bk[c] = gather4(kt_base, twice_code_bytes<KB>(w[c], krot, kq32), 4 * kTable * c); };
 #pragma unroll
       for (int c = 0; c < kAhead; ++c) load_cb(c);
+      if constexpr (KT) {
+        gather_cb(0);
+        gather_cb(1);
+      }
       half4 pend;  // even block's B operand, waiting for the odd one
 #pragma unroll
       for (int cb = 0; cb < kD / 4; ++cb) {
         if (cb + kAhead < kD / 4) load_cb(cb + kAhead);
-        const uint32_t e = (w[cb] >> kshift) & kmask;
-        const half4 b = dequant4<KB, BF16>(e, sz[cb]);
+        half4 b;
+        if constexpr (KT) {
+          if (cb + 2 < kD / 4) gather_cb(cb + 2);
+          b = bk[cb];
+        } else {
+          b = dequant4<KB, BF16>((w[cb] >> kshift) & kmask, sz[cb]);
+        }
         if (cb & 1) {  // blocks cb - 1, cb in one K = 32 MFMA
           if constexpr (RG == 1) {
             S[0] = mma2(qa[cb - 1], qa[cb], pend, b, S[0]);
@@ -296,7 +396,7 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
     if (keys_next) issue_keys_u(M, lds, nxt, KB, nh, lane);
     // this half's values are older than the next half's key loads issued since
     vm_wait(keys_next ? n_key_loads_u(KB) : 0);
-    build_sz_table(lds, M.vt, M.vs, M.vz, kHalfTok * gv, lane);
+    if constexpr (!VT) build_sz_table(lds, M.vt, M.vs, M.vz, kHalfTok * gv, lane);
 
     // ---- online softmax in base 2 ----
     {
@@ -339,13 +439,20 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
     lds_sync();
 
     // ---- O += P V: token group tg = tokens 4 tg .. 4 tg + 3, lane's token 4 tg + kq ----
+    // (with value tables: per quarter page, the quarter's tables first; a
+    // group's codes are read three groups ahead, its B operands gathered two
+    // ahead, and its A operand formed from the one non-zero weight, slot_a)
     {
+      constexpr int kQuarters = VT ? kHalfTok / kQuarterTok : 1;
+      constexpr int kGroups = kHalfTok / 4 / kQuarters;  // token groups per table build
+      constexpr int kLoadAhead = VT ? 3 : 1;
       half4 a[RG][kHalfTok / 4];
       uint32_t w0[kHalfTok / 4], w1[kHalfTok / 4];
       uint2 sz0[kHalfTok / 4], sz1[kHalfTok / 4];
+      half4 bv0[kHalfTok / 4], bv1[kHalfTok / 4];
       auto load_tg = [&](int tg) {
         const int t = 4 * tg + kq;
-        if constexpr (RG == 1) {
+        if constexpr (RG == 1 && !VT) {
           a[0][tg] = load_a(lds, aq, 8 * tg);
         } else {
 #pragma unroll
@@ -353,25 +460,54 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
         }
         w0[tg] = lds_u32(lds, M.vc + 16 * VB * t + vdw);
         w1[tg] = lds_u32(lds, M.vc + 16 * VB * t + 8 * VB + vdw);
-        sz0[tg] = *(const uint2*)(lds + M.vt + 8 * (t * gv + vg0));
-        sz1[tg] = *(const uint2*)(lds + M.vt + 8 * (t * gv + vg1));
+        if constexpr (!VT) {
+          sz0[tg] = *(const uint2*)(lds + M.vt + 8 * (t * gv + vg0));
+          sz1[tg] = *(const uint2*)(lds + M.vt + 8 * (t * gv + vg1));
+        }
       };
-      load_tg(0);
+      auto gather_tg = [&](int tg) {
+        const int off = 4 * kTable * (tg % (kQuarterTok / 4));
+        bv0[tg] = gather4(vt_base0, twice_code_bytes<VB>(w0[tg], vrot, kq32), off);
+        bv1[tg] = gather4(vt_base1, twice_code_bytes<VB>(w1[tg], vrot, kq32), off);
+      };
       half4 p0, p1;  // even group's B operands, waiting for the odd one
 #pragma unroll
-      for (int tg = 0; tg < kHalfTok / 4; ++tg) {
-        if (tg + 1 < kHalfTok / 4) load_tg(tg + 1);
-        const half4 b0 = dequant4<VB, BF16>((w0[tg] >> vshift) & vmask, sz0[tg]);
-        const half4 b1 = dequant4<VB, BF16>((w1[tg] >> vshift) & vmask, sz1[tg]);
-        if (tg & 1) {  // token groups tg - 1, tg in one K = 32 MFMA per tile
+      for (int qr = 0; qr < kQuarters; ++qr) {
+        if constexpr (VT) {
+          if (qr > 0) lds_sync();  // the previous quarter's gathers are done
+          build_value_tables<VB, BF16>(M, lds, gv, qr, lane);
+          lds_sync();
+        }
+        const int tg0 = kGroups * qr;
 #pragma unroll
-          for (int g = 0; g < RG; ++g) {
-            O[g][0] = mma2(a[g][tg - 1], a[g][tg], p0, b0, O[g][0]);
-            O[g][1] = mma2(a[g][tg - 1], a[g][tg], p1, b1, O[g][1]);
+        for (int i = 0; i < kLoadAhead; ++i) load_tg(tg0 + i);
+        if constexpr (VT) {
+          gather_tg(tg0);
+          gather_tg(tg0 + 1);
+        }
+#pragma unroll
+        for (int i = 0; i < kGroups; ++i) {
+          const int tg = tg0 + i;
+          if (i + kLoadAhead < kGroups) load_tg(tg + kLoadAhead);
+          half4 b0, b1;
+          if constexpr (VT) {
+            if (i + 2 < kGroups) gather_tg(tg + 2);
+            b0 = bv0[tg];
+            b1 = bv1[tg];
+          } else {
+            b0 = dequant4<VB, BF16>((w0[tg] >> vshift) & vmask, sz0[tg]);
+            b1 = dequant4<VB, BF16>((w1[tg] >> vshift) & vmask, sz1[tg]);
           }
-        } else {
-          p0 = b0;
-          p1 = b1;
+          if (tg & 1) {  // token groups tg - 1, tg in one K = 32 MFMA per tile
+#pragma unroll
+            for (int g = 0; g < RG; ++g) {
+              O[g][0] = mma2(a[g][tg - 1], a[g][tg], p0, b0, O[g][0]);
+              O[g][1] = mma2(a[g][tg - 1], a[g][tg], p1, b1, O[g][1]);
+            }
+          } else {
+            p0 = b0;
+            p1 = b1;
+          }
         }
       }
     }
@@ -404,10 +540,30 @@ namespace dkv {
 
 // The kernel waits until at most one half page's key or value loads are in
 // flight; vm_wait takes counts below 16.
-size_t uniform_decode_wave_lds_bytes(int kb, int vb, int gv) { return (size_t)umap(kb, vb, gv, 1).bytes; }
+// Value tables when the values are 2- or 4-bit, there are at most 4 query
+// rows and at most two value groups per token.
+static bool use_value_tables(int vb, int gq, int gv) { return value_tables_ok(vb, gq) && gv <= 2; }
+
+size_t uniform_decode_wave_lds_bytes(int kb, int vb, int gv) {
+  return (size_t)umap(kb, vb, gv, 1, key_tables(kb, 1), use_value_tables(vb, 1, gv)).bytes;
+}
 
 int uniform_decode_max_loads(int kb, int vb) {
   return n_key_loads_u(kb) > n_value_loads_u(vb) ? n_key_loads_u(kb) : n_value_loads_u(vb);
+}
+
+template <int G, int K, int V>
+static void launch_uniform_kernel(bool vtab, bool bf16, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                                  const FastParams& p) {
+  if constexpr (value_tables_ok(V, G)) {
+    if (vtab) {
+      if (bf16) hipLaunchKernelGGL((decode_pages_uniform<G, K, V, true, true>), grid, block, lds, stream, p);
+      else hipLaunchKernelGGL((decode_pages_uniform<G, K, V, false, true>), grid, block, lds, stream, p);
+      return;
+    }
+  }
+  if (bf16) hipLaunchKernelGGL((decode_pages_uniform<G, K, V, true, false>), grid, block, lds, stream, p);
+  else hipLaunchKernelGGL((decode_pages_uniform<G, K, V, false, false>), grid, block, lds, stream, p);
 }
 
 int launch_uniform_decode(const dkv_decode_args& a, int first, int count, int kb, int vb, int vg, int splits,
@@ -435,7 +591,9 @@ int launch_uniform_decode(const dkv_decode_args& a, int first, int count, int kb
   set_fused(p, fused);
   const int64_t workers = (int64_t)p.B * p.Hkv * splits + p.dense_workers;
   const dim3 grid((unsigned)((workers + kWaves - 1) / kWaves)), block(256);
-  const size_t lds = (size_t)kWaves * umap(kb, vb, p.gv, p.GQ > 4 ? 2 : 1).bytes;
+  const bool vtab = use_value_tables(vb, p.GQ, p.gv);
+  const size_t lds =
+      (size_t)kWaves * umap(kb, vb, p.gv, p.GQ > 4 ? 2 : 1, key_tables(kb, p.GQ), vtab).bytes;
   if ((kb != 2 && kb != 4 && kb != 8) || (vb != 2 && vb != 4 && vb != 8)) {
     set_error("uniform page decode supports 2, 4 and 8-bit codes");
     return DKV_ERR_UNSUPPORTED;
@@ -444,11 +602,7 @@ int launch_uniform_decode(const dkv_decode_args& a, int first, int count, int kb
     set_error("uniform page decode supports 1, 2, 4 or 8 query rows per KV head");
     return DKV_ERR_UNSUPPORTED;
   }
-#define DKV_U_LAUNCH(G, K, V)                                                                            \
-  do {                                                                                                   \
-    if (p.bf16) hipLaunchKernelGGL((decode_pages_uniform<G, K, V, true>), grid, block, lds, stream, p);  \
-    else hipLaunchKernelGGL((decode_pages_uniform<G, K, V, false>), grid, block, lds, stream, p);        \
-  } while (0)
+#define DKV_U_LAUNCH(G, K, V) launch_uniform_kernel<G, K, V>(vtab, p.bf16 != 0, grid, block, lds, stream, p)
 #define DKV_U_V(G, K)                                   \
   switch (vb) {                                         \
     case 2: DKV_U_LAUNCH(G, K, 2); break;               \

@@ -50,6 +50,44 @@ __device__ __forceinline__ uint32_t round_pair_to_bf16_precision(uint32_t x) {
   return (x + 0x00030003u + lsb) & 0xfff8fff8u;
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// fp16 scale or zero point (bits in the low half of x) in both halves; as an
+// operand of a packed op this is an op_sel broadcast, not an instruction.
+__device__ __forceinline__ half2v splat_h(uint32_t x) {
+  const _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)x);
+  return half2v{h, h};
+}
+
+// Exact dequantized values for codes (c0, c1) of one (scale, zero) pair, as
+// an fp16 pair: fp16(fp16(code*s) + z), then bf16 precision if BF16.
+template <bool BF16>
+__device__ __forceinline__ uint32_t lut_pair(uint32_t codes_h2, half2v s, half2v z) {
+  const half2v c = __builtin_bit_cast(half2v, codes_h2);
+  const half2v prod = c * s;  // -ffp-contract=off keeps the multiply and the add separate
+  const half2v sum = prod + z;
+  uint32_t r = __builtin_bit_cast(uint32_t, sum);
+  return BF16 ? round_pair_to_bf16_precision(r) : r;
+}
+
+// Codes (2q + 8h, 2q + 1 + 8h) as an fp16 pair (h = 0, 1: entries 0..7 or 8..15).
+__device__ __forceinline__ uint32_t code_pair(int q, int h) {
+  const uint32_t lo[4] = {0x3c000000u, 0x42004000u, 0x45004400u, 0x47004600u};  // (0, 1) .. (6, 7)
+  const uint32_t hi[4] = {0x48804800u, 0x49804900u, 0x4a804a00u, 0x4b804b00u};  // (8, 9) .. (14, 15)
+  return h ? hi[q] : lo[q];
+}
+
+// Four entries (fp16) of LDS tables, at byte offsets off + byte j of sel from
+// base (whose low byte is zero, so a byte permute forms each address), as a
+// B operand.
+__device__ __forceinline__ half4 gather4(uint32_t base, uint32_t sel, int off) {
+  typedef __attribute__((address_space(3))) const _Float16 lds_half;
+  half4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r[j] = ((lds_half*)(uintptr_t)perm(base, sel, 0x07060500u | j))[off / 2];
+  return r;
+}
+
 struct FastParams {
   const dkv_segment* segs;   // descriptor table; pages are entries [first, first + count)
   int first, count;
