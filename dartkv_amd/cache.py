@@ -148,6 +148,21 @@ def _nonfinite_flags(device: torch.device) -> torch.Tensor:
     return t
 
 
+def _drain(device: torch.device) -> None:
+    """Wait until the device's current stream has run everything enqueued so far, by polling an event
+    recorded on it: the wait ends within a few microseconds of the GPU finishing, where a blocking
+    stream synchronization returns about 10-15 µs later (measured on MI355X)."""
+    events = getattr(_flag_store, "events", None)
+    if events is None:
+        events = _flag_store.events = {}
+    ev = events.get(device)
+    if ev is None:
+        ev = events[device] = torch.cuda.Event()
+    ev.record(torch.cuda.current_stream(device))
+    while not ev.query():
+        pass
+
+
 def _storage(shape, dtype: torch.dtype, device) -> torch.Tensor:
     """Uninitialized storage a cache keeps and updates in place across calls.  It is allocated as a
     normal tensor even inside ``torch.inference_mode()`` (an inference tensor could not be updated in
@@ -812,7 +827,7 @@ class DartKVCache:
                 scope.flags.zero_()
         if scope.flags is None:
             return
-        torch.cuda.current_stream(self._device).synchronize()
+        _drain(self._device)
         bad_keys, bad_values = scope.flags.tolist()
         if bad_keys or bad_values:
             scope.flags.zero_()
@@ -942,7 +957,7 @@ class DartKVCache:
         fresh = groups != -(-c.page_size // kg)
         pool = self._key_pool_for(src, groups, fresh)
         slot = pool.reserve(n_pages, headroom=0 if fresh else (max(2, n_pages // 16) if pool.used == 0 else None))
-        t = pool.tensors  # page-major: the launch writes pages [slot, slot + n_pages)
+        t = {name: pool.ref(name) for name in pool.shapes}  # page-major: the launch writes pages [slot, slot + n_pages)
         values = None if job is None else job[0]
         flag = self._flag_ptr(0)
         if c.promote_ratio > 0.0:
@@ -1216,7 +1231,7 @@ def _value_rows_job(src: torch.Tensor, bits: int, group: int, meta: torch.dtype,
         values, scale, zero = out
         out_rows, row0 = T, 0
     else:
-        values, scale, zero = pool.tensors["values"], pool.tensors["scale"], pool.tensors["zero_point"]
+        values, scale, zero = pool.ref("values"), pool.ref("scale"), pool.ref("zero_point")
         out_rows = pool.capacity
     job = _lib.ValueRowsArgs(src=src.data_ptr(), src_dtype=_lib.dtype_code(src.dtype), blocks=blocks,
                              block_stride=block_stride, block_rows=T, n=D, row_stride=D, bits=bits, group=group,

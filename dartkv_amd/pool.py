@@ -27,9 +27,39 @@ from .mixed import MixedQuantizedKey
 from .quantization import QuantizedTensor
 
 
+class FieldRef:
+    """A contiguous pool field known by its address, shape and dtype before its tensor view exists:
+    enough for a launch (``data_ptr``, ``stride``, ``element_size``), built without any torch call."""
+
+    __slots__ = ("_ptr", "_strides", "_size", "shape")
+
+    def __init__(self, ptr: int, shape: Tuple[int, ...], element_size: int) -> None:
+        self._ptr, self.shape, self._size = ptr, shape, element_size
+        strides, acc = [], 1
+        for n in reversed(shape):
+            strides.append(acc)
+            acc *= n
+        self._strides = tuple(reversed(strides))
+
+    def data_ptr(self) -> int:
+        return self._ptr
+
+    def stride(self, dim: int) -> int:
+        return self._strides[dim]
+
+    def element_size(self) -> int:
+        return self._size
+
+
 class PagePool:
     """Growable packed storage.  ``fields`` maps a field name to (shape, dtype) with the slot axis
-    ``axis`` sized 0; ``batch_axis`` is the batch dimension.  Slots [0, used) hold data."""
+    ``axis`` sized 0; ``batch_axis`` is the batch dimension.  Slots [0, used) hold data.
+
+    A pool's fields share one allocation (each at a 256-byte aligned offset).  Right after it is made,
+    only their addresses are known (``ref``): a launch can write them before any tensor view exists,
+    and the views (``tensors``) are made on first use, usually while that launch runs."""
+
+    _ALIGN = 256
 
     def __init__(self, fields: Dict[str, Tuple[Tuple[int, ...], torch.dtype]], axis: int, batch_axis: int,
                  device: torch.device, align: int = 1) -> None:
@@ -39,8 +69,32 @@ class PagePool:
         self.device = device
         self.capacity = 0
         self.used = 0
-        self.tensors: Dict[str, torch.Tensor] = {}
+        self._tensors: Optional[Dict[str, torch.Tensor]] = {}
+        self._buffer: Optional[torch.Tensor] = None
+        self._layout: Dict[str, Tuple[int, Tuple[int, ...]]] = {}  # name -> (byte offset, full shape)
         self.generation = 0  # bumps whenever the tensors are replaced (field addresses change)
+
+    @property
+    def tensors(self) -> Dict[str, torch.Tensor]:
+        """The fields as tensors (views of the pool's allocation, made on first use after a resize)."""
+        if self._tensors is None:
+            views = {}
+            with torch.inference_mode(False):  # views updated in place by later calls in any mode
+                for name, (offset, full) in self._layout.items():
+                    dtype = self.dtypes[name]
+                    nbytes = dtype.itemsize
+                    for n in full:
+                        nbytes *= n
+                    views[name] = self._buffer.narrow(0, offset, nbytes).view(dtype).view(full)
+            self._tensors = views
+        return self._tensors
+
+    def ref(self, name: str):
+        """Field ``name`` (all slots) as a tensor, or as a FieldRef while its view is not made yet."""
+        if self._tensors is not None:
+            return self._tensors[name]
+        offset, full = self._layout[name]
+        return FieldRef(self._buffer.data_ptr() + offset, full, self.dtypes[name].itemsize)
 
     @property
     def batch(self) -> int:
@@ -58,17 +112,22 @@ class PagePool:
         return start
 
     def _resize(self, capacity: int) -> None:
-        fresh = {}
+        old = self.tensors if self.used else None
+        layout, total = {}, 0
         for name, shape in self.shapes.items():
             full = list(shape)
             full[self.axis] = capacity
-            with torch.inference_mode(False):  # kept and updated in place across calls in any mode
-                t = torch.empty(full, dtype=self.dtypes[name], device=self.device)
-            old = self.tensors.get(name)
-            if old is not None and self.used:
-                t.narrow(self.axis, 0, self.used).copy_(old.narrow(self.axis, 0, self.used))
-            fresh[name] = t
-        self.tensors, self.capacity = fresh, capacity
+            nbytes = self.dtypes[name].itemsize
+            for n in full:
+                nbytes *= n
+            layout[name] = (total, tuple(full))
+            total += -(-nbytes // self._ALIGN) * self._ALIGN
+        with torch.inference_mode(False):  # kept and updated in place across calls in any mode
+            self._buffer = torch.empty(max(total, 1), dtype=torch.uint8, device=self.device)
+        self._layout, self._tensors, self.capacity = layout, None, capacity
+        if old is not None:
+            for name, t in self.tensors.items():
+                t.narrow(self.axis, 0, self.used).copy_(old[name].narrow(self.axis, 0, self.used))
         self.generation += 1
 
     def field(self, name: str, at: int, n: Optional[int] = None) -> torch.Tensor:
@@ -89,13 +148,14 @@ class PagePool:
         With the batch size unchanged the gather lands in the same tensors, so descriptors stay valid."""
         index = index.to(self.device)
         same = index.numel() == self.batch
+        tensors = self.tensors
         with torch.inference_mode(False):  # new pool tensors are kept and updated in place in any mode
-            for name, t in self.tensors.items():
+            for name, t in list(tensors.items()):
                 picked = t.index_select(self.batch_axis, index)
                 if same:
                     t.copy_(picked)
                 else:
-                    self.tensors[name] = picked
+                    tensors[name] = picked
         if not same:
             for name, shape in self.shapes.items():
                 s = list(shape)
@@ -105,7 +165,7 @@ class PagePool:
 
     def to(self, device: torch.device) -> None:
         with torch.inference_mode(False):
-            self.tensors = {name: t.to(device) for name, t in self.tensors.items()}
+            self._tensors = {name: t.to(device) for name, t in self.tensors.items()}
         self.device = device
         self.generation += 1
 
