@@ -26,7 +26,7 @@ KEY_DENSE, KEY_UNIFORM, KEY_MIXED = 0, 1, 2
 VALUE_DENSE, VALUE_UNIFORM = 0, 1
 SELECT_MAGNITUDE, SELECT_VARIANCE, SELECT_GIVEN = 0, 1, 2
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 # element types the kernels read and write (sources, outputs, metadata)
@@ -68,6 +68,7 @@ class KeyPagesArgs(ctypes.Structure):
         ("zero", ctypes.c_void_p), ("zero_page_stride", ctypes.c_int64),
         ("values", ctypes.c_void_p),  # const dkv_value_rows_args* (optional)
         ("nonfinite", ctypes.c_void_p),  # uint32_t* (optional)
+        ("copies", ctypes.c_void_p), ("n_copies", ctypes.c_int64),  # const dkv_copy_block* (optional)
     ]
 
 

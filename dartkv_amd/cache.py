@@ -23,8 +23,9 @@ boundaries.  How it is stored is this build's own:
 from __future__ import annotations
 
 import contextlib
+import ctypes
 import threading
-from dataclasses import dataclass
+from dataclasses import dataclass, fields as dataclass_fields
 from itertools import accumulate
 from typing import TYPE_CHECKING, List, Optional, Tuple, Union
 
@@ -111,6 +112,8 @@ class DartKVCacheConfig:
             raise ValueError("channel_selection must be 'magnitude', 'random', or 'variance'")
         if self.metadata_dtype not in (torch.float16, torch.bfloat16, torch.float32, torch.float64):
             raise TypeError("metadata_dtype must be a floating-point torch dtype")
+        # the field values as one tuple: a cheap dictionary key for plans made per configuration
+        object.__setattr__(self, "_key", tuple(getattr(self, f.name) for f in dataclass_fields(self)))
 
     @property
     def resolved_key_bits(self) -> int:
@@ -206,6 +209,140 @@ class _FiniteScope:
     def _trimmed(track: list, n: int, last) -> list:
         kept = track[:max(0, n - 1)]
         return kept + [last] if n else kept
+
+
+class _PrefillPlan:
+    """What the first append of an empty cache (``DartKVCache._prefill``) needs that depends only on
+    the configuration and the inputs' shape, strides, dtype and device: the token split (dense sink,
+    full pages, held tail), the pools' fields, capacities and layouts, and the library arguments with
+    every address left to fill in (offsets into the sources, pools and dense buffer instead).  The
+    capacities are those the general path's reserve calls make, so later appends grow the pools at the
+    same points."""
+
+    __slots__ = ("B", "H", "T", "D", "sink", "sealable", "pending", "n_pages", "mixed", "key_group",
+                 "key_groups", "key_bits", "key_packed", "value_group", "value_bits", "value_padded",
+                 "value_packed", "key_fields", "value_fields", "key_layout", "key_bytes", "key_capacity",
+                 "value_layout", "value_bytes", "value_capacity", "key_offsets", "value_offsets", "row",
+                 "sink_bytes", "tail_capacity", "tail_bytes", "dense_bytes", "key_src", "value_src", "key_args",
+                 "value_args", "copies", "copy_type", "copy_blocks")
+
+    @staticmethod
+    def build(c: DartKVCacheConfig, key_states: torch.Tensor, value_states: torch.Tensor):
+        """The plan, or False where the general path must run: a Kitty value window, a random channel
+        choice, nothing to seal, a short last page, inputs whose last dim is not contiguous, or a value
+        layout the rows kernel cannot read in place."""
+        if c.value_local_tokens or key_states.stride(-1) != 1 or value_states.stride(-1) != 1:
+            return False
+        B, H, T, D = key_states.shape
+        P = c.page_size
+        sink = min(c.sink_tokens, T)
+        rest = T - sink
+        held = c.hold_partial_pages or c.local_tokens
+        sealable = (max(0, rest - c.local_tokens) // P) * P if held else rest
+        pending = rest - sealable
+        if sealable == 0 or sealable % P or pending > P + c.local_tokens:
+            return False
+        mixed = c.promote_ratio > 0.0
+        K = promoted_count(D, c.promote_ratio) if mixed else 0
+        if mixed and c.channel_selection == "random" and 0 < K < D:
+            return False
+        vsb, vsh, vst, _ = value_states.stride()
+        if sealable > 1 and vst != D:
+            return False
+        if H == 1:
+            vblocks, vblock_stride = B, vsb
+        elif B == 1 or vsb == H * vsh:
+            vblocks, vblock_stride = B * H, vsh
+        else:
+            return False
+        self = _PrefillPlan()
+        self.B, self.H, self.T, self.D = B, H, T, D
+        self.sink, self.sealable, self.pending, self.n_pages = sink, sealable, pending, sealable // P
+        kg, vg, meta = c.resolved_key_group_size, c.resolved_value_group_size, c.metadata_dtype
+        kb, vb = c.resolved_key_bits, c.resolved_value_bits
+        groups = -(-P // kg)
+        self.mixed, self.key_group, self.key_groups, self.key_bits = mixed, kg, groups, kb
+        self.value_group, self.value_bits = vg, vb
+        # the pools _key_pool_for / _value_pool_for make, at the capacities their first reserve gives
+        if mixed:
+            nb = (kg + 3) // 4
+            self.key_fields = {"low_values": ((0, B, H, D, groups, nb), torch.uint8),
+                               "high_values": ((0, B, H, K, groups, nb if K else nb * 4), torch.uint8),
+                               "channel_indices": ((0, B, H, K), torch.int32),
+                               "scale": ((0, B, H, D, groups), meta), "zero_point": ((0, B, H, D, groups), meta)}
+            names = ("low_values", "high_values", "channel_indices", "scale", "zero_point")
+        else:
+            kpacked = -(-groups * kg // (8 // kb))
+            self.key_fields = {"values": ((0, B, H, D, kpacked), torch.uint8),
+                               "scale": ((0, B, H, D, groups), meta), "zero_point": ((0, B, H, D, groups), meta)}
+            names = ("values", None, None, "scale", "zero_point")
+            self.key_packed = kpacked * (8 // kb)
+        vgroups = -(-D // vg)
+        vpacked = -(-vgroups * vg // (8 // vb))
+        self.value_fields = {"values": ((B, H, 0, vpacked), torch.uint8), "scale": ((B, H, 0, vgroups), meta),
+                             "zero_point": ((B, H, 0, vgroups), meta)}
+        self.value_padded, self.value_packed = vgroups * vg, vpacked * (8 // vb)
+        kpool = PagePool(self.key_fields, axis=0, batch_axis=1, device=key_states.device)
+        vpool = PagePool(self.value_fields, axis=2, batch_axis=0, device=key_states.device, align=64)
+        self.key_capacity = kpool.capacity_for(self.n_pages, max(2, self.n_pages // 16))
+        self.value_capacity = vpool.capacity_for(sealable, max(vpool.align, sealable // 16))
+        self.key_layout, self.key_bytes = kpool.plan(self.key_capacity)
+        self.value_layout, self.value_bytes = vpool.plan(self.value_capacity)
+        self.key_offsets = tuple(0 if n is None else self.key_layout[n][0] for n in names)
+        self.value_offsets = tuple(self.value_layout[n][0] for n in ("values", "scale", "zero_point"))
+        # the dense buffer: sink keys, sink values, tail keys, tail values (each 256-byte aligned)
+        e = key_states.element_size()
+        row = self.row = D * e
+        self.sink_bytes = -(-B * H * sink * row // 256) * 256
+        self.tail_capacity = P + c.local_tokens if pending else 0
+        self.tail_bytes = -(-B * H * self.tail_capacity * row // 256) * 256
+        self.dense_bytes = 2 * (self.sink_bytes + self.tail_bytes)
+        ksb, ksh, kst, ksd = key_states.stride()
+        self.key_src, self.value_src = sink * kst * e, sink * vst * e
+        v = _lib.ValueRowsArgs(src_dtype=_lib.dtype_code(value_states.dtype), blocks=vblocks,
+                               block_stride=vblock_stride, block_rows=sealable, n=D, row_stride=D, bits=vb, group=vg,
+                               meta_dtype=_lib.dtype_code(meta), out_block_rows=self.value_capacity, out_row0=0)
+        self.value_args = bytes(v)
+        a = _lib.KeyPagesArgs()
+        a.src_dtype = _lib.dtype_code(key_states.dtype)
+        a.B, a.H, a.D, a.page_tokens, a.n_pages = B, H, D, P, self.n_pages
+        a.sb, a.sh, a.st, a.sd = ksb, ksh, kst, ksd
+        a.group, a.meta_dtype = kg, _lib.dtype_code(meta)
+        if mixed:
+            a.key_mode, a.bits, a.promoted = _lib.KEY_MIXED, 2, K
+            a.selection = _lib.SELECT_VARIANCE if c.channel_selection == "variance" else _lib.SELECT_MAGNITUDE
+        else:
+            a.key_mode, a.bits = _lib.KEY_UNIFORM, kb
+        if self.n_pages > 1:
+            for attr, name in zip(("low", "high", "idx", "scale", "zero"), names):
+                if name is not None:
+                    _, full = self.key_layout[name]
+                    stride = self.key_fields[name][1].itemsize
+                    for n in full[1:]:
+                        stride *= n
+                    setattr(a, attr + "_page_stride", stride)
+        self.key_args = bytes(a)
+        # the copies: (source byte offset, dense byte offset, from the values) and their fixed fields
+        runs = ([(0, sink, sink, 0, self.sink_bytes)] if sink else []) + \
+            ([(sink + sealable, pending, self.tail_capacity, 2 * self.sink_bytes,
+               2 * self.sink_bytes + self.tail_bytes)] if pending else [])
+        self.copy_type = _lib.CopyBlock * max(1, 2 * len(runs))
+        blocks = self.copy_type()
+        self.copies = []
+        for t0, count, cap, koff, voff in runs:
+            for from_values, (sb, sh, st), off in ((False, (ksb, ksh, kst), koff), (True, (vsb, vsh, vst), voff)):
+                blk = blocks[len(self.copies)]
+                blk.B, blk.H, blk.T, blk.row_bytes = B, H, count, row
+                blk.src_sb, blk.src_sh, blk.src_st = sb * e, sh * e, st * e
+                blk.dst_sb, blk.dst_sh, blk.dst_st = H * cap * row, cap * row, row
+                self.copies.append((t0 * st * e, off, from_values))
+        self.copies = tuple(self.copies)
+        self.copy_blocks = bytes(blocks)
+        return self
+
+
+# prefill plans by (config fields, key shape, key strides, value strides, dtype, device)
+_PREFILL_PLANS: dict = {}
 
 
 class _DecodePlan:
@@ -314,6 +451,8 @@ class DartKVCache:
             return
         _lib.require_device(key_states, value_states)
         self._validate_inputs(key_states, value_states)
+        if self._seen_tokens == 0 and self._prefill(key_states, value_states):
+            return
         key_states = key_states.detach()
         value_states = value_states.detach()
         if key_states.stride(-1) != 1:
@@ -351,6 +490,94 @@ class DartKVCache:
         self._seen_tokens += chunk
         self._layout_version += 1
         self._invalidate_page_descriptors()
+
+    def _prefill(self, key_states: torch.Tensor, value_states: torch.Tensor) -> bool:
+        """The first append of an empty cache (a prefill) in few host steps: the dense sink, full pages
+        and held tail of the general path from one library call that quantizes the pages' keys and values
+        and copies the sink and tail tokens, with every output allocated and described before it (from a
+        plan kept per configuration and input layout) and the segment objects made while it runs.  Same
+        result as the general path; False (nothing done) when the plan does not apply, and the general
+        path then runs.  Inputs are validated."""
+        if (self._keys or self._values or self._key_pool is not None or self._value_pool is not None
+                or self._tail_key is not None or self._tail_count_dev is not None or self._pending_key is not None
+                or self._pending_value is not None):
+            return False
+        device = key_states.device
+        key = (self.config._key, key_states.shape, key_states.stride(), value_states.stride(), key_states.dtype,
+               device)
+        plan = _PREFILL_PLANS.get(key)
+        if plan is None:
+            plan = _PrefillPlan.build(self.config, key_states, value_states)
+            if len(_PREFILL_PLANS) >= 32:
+                _PREFILL_PLANS.clear()
+            _PREFILL_PLANS[key] = plan
+        if plan is False:
+            return False
+        c = self.config
+        with self._finite_inputs():  # (a failed check finds the pools made here and empties them)
+            kpool = self._key_pool = PagePool(plan.key_fields, axis=0, batch_axis=1, device=device)
+            vpool = self._value_pool = PagePool(plan.value_fields, axis=2, batch_axis=0, device=device, align=64)
+            normal = torch.is_inference_mode_enabled()
+            with torch.inference_mode(False) if normal else contextlib.nullcontext():
+                # kept and updated in place by later calls in any mode
+                kbuf = torch.empty(plan.key_bytes, dtype=torch.uint8, device=device)
+                vbuf = torch.empty(plan.value_bytes, dtype=torch.uint8, device=device)
+                dense = torch.empty(plan.dense_bytes, dtype=torch.uint8, device=device) if plan.dense_bytes else None
+            kpool.place(kbuf, plan.key_layout, plan.key_capacity)
+            vpool.place(vbuf, plan.value_layout, plan.value_capacity)
+            kpool.used, vpool.used = plan.n_pages, plan.sealable
+            a = _lib.KeyPagesArgs.from_buffer_copy(plan.key_args)
+            v = _lib.ValueRowsArgs.from_buffer_copy(plan.value_args)
+            kptr, vptr = key_states.data_ptr(), value_states.data_ptr()
+            a.src, v.src = kptr + plan.key_src, vptr + plan.value_src
+            kbase, vbase = kbuf.data_ptr(), vbuf.data_ptr()
+            a.low = kbase + plan.key_offsets[0]
+            if plan.mixed:
+                a.high, a.idx = kbase + plan.key_offsets[1], kbase + plan.key_offsets[2]
+            a.scale, a.zero = kbase + plan.key_offsets[3], kbase + plan.key_offsets[4]
+            v.values = vbase + plan.value_offsets[0]
+            v.scale, v.zero = vbase + plan.value_offsets[1], vbase + plan.value_offsets[2]
+            v.nonfinite = self._flag_ptr(1)
+            a.nonfinite = self._flag_ptr(0)
+            a.values = ctypes.addressof(v)
+            if plan.copies:
+                copies = plan.copy_type.from_buffer_copy(plan.copy_blocks)
+                dptr = dense.data_ptr()
+                for blk, (src_off, dst_off, from_values) in zip(copies, plan.copies):
+                    blk.src, blk.dst = (vptr if from_values else kptr) + src_off, dptr + dst_off
+                a.copies, a.n_copies = ctypes.addressof(copies), len(plan.copies)
+            _lib.check(_lib.load().dkv_quantize_key_pages(a, _lib.stream_ptr(device)), "dkv_quantize_key_pages")
+            # the segments, while the launches run
+            P, D, dtype, kg, vg = c.page_size, plan.D, key_states.dtype, plan.key_group, plan.value_group
+            padded = plan.key_groups * kg
+            if plan.mixed:
+                keys = [PoolMixedKey(kpool, p, P, D, padded, kg, c.promote_bits, dtype) for p in range(plan.n_pages)]
+            else:
+                kb = plan.key_bits
+                keys = [PoolKeys(kpool, p, P, D, padded, plan.key_packed, kg, kb, dtype) for p in range(plan.n_pages)]
+            vb, vpadded, vpacked = plan.value_bits, plan.value_padded, plan.value_packed
+            values = [PoolValues(vpool, i * P, P, D, vpadded, vpacked, vg, vb, dtype) for i in range(plan.n_pages)]
+            self._sealed_version += 1
+            if dense is not None:
+                B, H = plan.B, plan.H
+                with torch.inference_mode(False) if normal else contextlib.nullcontext():
+                    if plan.sink:
+                        n = B * H * plan.sink * plan.row
+                        keys.insert(0, dense.narrow(0, 0, n).view(dtype).view(B, H, plan.sink, D))
+                        values.insert(0, dense.narrow(0, plan.sink_bytes, n).view(dtype).view(B, H, plan.sink, D))
+                        self._sealed_version += 1
+                    if plan.pending:
+                        at, cap = 2 * plan.sink_bytes, plan.tail_capacity
+                        n = B * H * cap * plan.row
+                        self._tail_key = dense.narrow(0, at, n).view(dtype).view(B, H, cap, D)
+                        self._tail_value = dense.narrow(0, at + plan.tail_bytes, n).view(dtype).view(B, H, cap, D)
+                        self._pending_key = self._tail_key.narrow(2, 0, plan.pending)
+                        self._pending_value = self._tail_value.narrow(2, 0, plan.pending)
+            self._keys, self._values = keys, values
+        self._seen_tokens += plan.T
+        self._layout_version += 1
+        self._invalidate_page_descriptors()
+        return True
 
     def get(self) -> Tuple[torch.Tensor, torch.Tensor]:
         if self._seen_tokens == 0:

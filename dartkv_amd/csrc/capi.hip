@@ -19,4 +19,4 @@ void set_error(const char* fmt, ...) {
 
 extern "C" const char* dkv_last_error(void) { return dkv::g_last_error; }
 
-extern "C" int dkv_abi_version(void) { return 12; }
+extern "C" int dkv_abi_version(void) { return 13; }

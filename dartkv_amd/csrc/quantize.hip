@@ -13,6 +13,7 @@
 #include <algorithm>
 
 #include "dkv_capi_util.h"
+#include "dkv_copy.h"
 #include "dkv_device.h"
 #include "dkv_select.h"
 #include "dkv_select_wave.h"
@@ -1236,12 +1237,25 @@ __global__ void __launch_bounds__(64) key_select_pages(KeyParams k, int row_byte
 
 // The key path's channel selection and a value-row job in one launch.
 // Workgroups [0, sel_blocks) select (one wave per page, as key_select_pages);
-// the others quantize value rows (workgroup b - sel_blocks of the gx x gy grid
-// of quantize_rows_vec).  A selection wave mostly waits on its LDS steps;
-// the value rows use each SIMD meanwhile.  (Spreading the selection
-// workgroups among the value rows' was slower: a selection wave's chain of
-// dependent steps stretches when VALU-bound row waves share its SIMD.)
+// the next gx * gy quantize value rows (workgroup b - sel_blocks of the
+// gx x gy grid of quantize_rows_vec); the last ones make the call's dense
+// token copies, kCopyUnitsPerThread 16-byte units per thread.  A selection
+// wave mostly waits on its LDS steps; the value rows use each SIMD meanwhile.
+// (Spreading the selection workgroups among the value rows' was slower: a
+// selection wave's chain of dependent steps stretches when VALU-bound row
+// waves share its SIMD.)
 constexpr int kSelectWaves = kThreads / 64;
+constexpr int kCopyUnitsPerThread = 4;
+
+__global__ void __launch_bounds__(kThreads) copy_token_blocks_kernel(dkv::CopyParams cp) {
+  const int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (u < cp.first[cp.n]) dkv::copy_token_unit(cp, u);
+}
+
+__host__ inline int64_t copy_blocks_for(const dkv::CopyParams& cp) {
+  const int64_t per_block = (int64_t)kThreads * kCopyUnitsPerThread;
+  return (cp.first[cp.n] + per_block - 1) / per_block;
+}
 // Shared launches pay off while every selection wave is resident at once (one
 // wave per page, 256 CUs x 32 waves); past that the selections queue in rounds
 // and the value rows wait behind them, so the two run as separate launches.
@@ -1250,7 +1264,8 @@ constexpr int64_t kSelectFuseMaxPages = 8192;
 template <int BITS, int SRC, int E>
 __global__ void __launch_bounds__(kThreads) select_pages_and_rows(KeyParams k, int row_bytes, int64_t items,
                                                                   int64_t sel_blocks, RowsParams p, int lpg,
-                                                                  int row_shift, int64_t gx, int64_t gy) {
+                                                                  int row_shift, int64_t gx, int64_t gy,
+                                                                  dkv::CopyParams cp) {
   __shared__ SelectLds l[kSelectWaves];
   if ((int64_t)blockIdx.x < sel_blocks) {
     const int wave = threadIdx.x >> 6;
@@ -1259,7 +1274,17 @@ __global__ void __launch_bounds__(kThreads) select_pages_and_rows(KeyParams k, i
     return;
   }
   const int64_t b = (int64_t)blockIdx.x - sel_blocks;
-  rows_vec_body<BITS, SRC, E>(p, lpg, row_shift, b % gx, b / gx, gx, gy);
+  if (b < gx * gy) {
+    rows_vec_body<BITS, SRC, E>(p, lpg, row_shift, b % gx, b / gx, gx, gy);
+    return;
+  }
+  const int64_t u0 = (b - gx * gy) * kThreads * kCopyUnitsPerThread + threadIdx.x;
+  const int64_t units = cp.first[cp.n];
+#pragma unroll
+  for (int i = 0; i < kCopyUnitsPerThread; ++i) {
+    const int64_t u = u0 + (int64_t)i * kThreads;
+    if (u < units) dkv::copy_token_unit(cp, u);
+  }
 }
 
 __host__ inline size_t key_tiled_smem(int D, int T, int G, int K, int row_bytes) {
@@ -1512,11 +1537,25 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
                                 v.out_block_rows, v.out_row0, VL);
     if (rc != DKV_OK) return rc;
   }
-  hipStream_t s = (hipStream_t)stream;
-  if (a.n_pages == 0) {
-    if (with_values) launch_rows(VL, s);
-    return dkv_check_launch("dkv_quantize_key_pages");
+  // the optional dense copies: validated before anything launches; they ride in the
+  // selection + value-row launch when it runs, else they get a launch of their own last
+  dkv::CopyParams CP;
+  {
+    const int rc = dkv::prepare_copies(a.copies, a.n_copies, CP, "dkv_quantize_key_pages copies");
+    if (rc != DKV_OK) return rc;
   }
+  bool copies_done = CP.first[CP.n] == 0;
+  hipStream_t s = (hipStream_t)stream;
+  auto finish = [&]() {
+    if (with_values && !values_done) launch_rows(VL, s);
+    if (!copies_done) {
+      const int64_t units = CP.first[CP.n];
+      hipLaunchKernelGGL(copy_token_blocks_kernel, dim3((unsigned)((units + kThreads - 1) / kThreads)),
+                         dim3(kThreads), 0, s, CP);
+    }
+    return dkv_check_launch("dkv_quantize_key_pages");
+  };
+  if (a.n_pages == 0) return finish();
   KeyParams k;
   k.a = a;
   k.G = (a.page_tokens + a.group - 1) / a.group;
@@ -1567,18 +1606,18 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
       const int64_t items = a.B * a.H * a.n_pages;
       DKV_KEYF_RUN(kKeyScores);
       if (with_values && VL.vec && VL.rows > 0 && items <= kSelectFuseMaxPages &&
-          (items + kSelectWaves - 1) / kSelectWaves + VL.gx * VL.gy <= 0x7fffffffLL) {
-        // the selection and the value rows share one launch
+          (items + kSelectWaves - 1) / kSelectWaves + VL.gx * VL.gy + copy_blocks_for(CP) <= 0x7fffffffLL) {
+        // the selection, the value rows and the copies share one launch
         const int64_t sel_blocks = (items + kSelectWaves - 1) / kSelectWaves;
-        const dim3 sgrid((unsigned)(sel_blocks + VL.gx * VL.gy));
+        const dim3 sgrid((unsigned)(sel_blocks + VL.gx * VL.gy + copy_blocks_for(CP)));
 #define DKV_SV(B, T)                                                                                           \
   do {                                                                                                        \
     if (VL.epl == 16)                                                                                         \
       hipLaunchKernelGGL((select_pages_and_rows<B, T, 16>), sgrid, dim3(kThreads), 0, s, k, row_bytes, items,  \
-                         sel_blocks, VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy);                               \
+                         sel_blocks, VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy, CP);                           \
     else                                                                                                      \
       hipLaunchKernelGGL((select_pages_and_rows<B, T, 8>), sgrid, dim3(kThreads), 0, s, k, row_bytes, items,   \
-                         sel_blocks, VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy);                               \
+                         sel_blocks, VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy, CP);                           \
   } while (0)
 #define DKV_SV_BITS(T)                    \
   do {                                    \
@@ -1592,6 +1631,7 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
 #undef DKV_SV_BITS
 #undef DKV_SV
         values_done = true;
+        copies_done = true;
       } else {
         hipLaunchKernelGGL(key_select_pages, dim3((unsigned)items), dim3(64), 0, s, k, row_bytes);
       }
@@ -1602,8 +1642,7 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
 #undef DKV_KEYF_RUN
 #undef DKV_KEYF_BITS
 #undef DKV_KEYF
-    if (with_values && !values_done) launch_rows(VL, s);
-    return dkv_check_launch("dkv_quantize_key_pages");
+    return finish();
   }
   if (use_tiled) {
     const dim3 grid((unsigned)(a.B * a.H), (unsigned)a.n_pages);
@@ -1617,8 +1656,7 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
     } else {
       hipLaunchKernelGGL(quantize_key_pages_tiled, grid, dim3(kThreads), tiled, s, k, kKeyAll);
     }
-    if (with_values) launch_rows(VL, s);
-    return dkv_check_launch("dkv_quantize_key_pages");
+    return finish();
   }
   const bool f64 = a.src_dtype == kF64;
   const size_t shmem = f64 ? key_generic_smem<double>(a.D) : key_generic_smem<float>(a.D);
@@ -1629,8 +1667,7 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
   } else {
     hipLaunchKernelGGL(quantize_key_pages_kernel<float>, grid, dim3(kThreads), shmem, s, k);
   }
-  if (with_values) launch_rows(VL, s);
-  return dkv_check_launch("dkv_quantize_key_pages");
+  return finish();
 }
 
 extern "C" int dkv_dequantize_rows(const uint8_t* values, const void* scale, const void* zero, int meta_dtype,

@@ -100,19 +100,22 @@ class PagePool:
     def batch(self) -> int:
         return next(iter(self.shapes.values()))[self.batch_axis]
 
+    def capacity_for(self, n: int, headroom: Optional[int] = None) -> int:
+        """The capacity ``reserve(n, headroom)`` grows to when the n slots do not fit."""
+        extra = max(self.align, (self.used + n) // 8) if headroom is None else headroom
+        cap = self.used + n + extra
+        return -(-cap // self.align) * self.align
+
     def reserve(self, n: int, headroom: Optional[int] = None) -> int:
         """Slots [start, start + n) for new data; grows (copying the used slots) when they do not fit."""
         if self.used + n > self.capacity:
-            extra = max(self.align, (self.used + n) // 8) if headroom is None else headroom
-            cap = self.used + n + extra
-            cap = -(-cap // self.align) * self.align
-            self._resize(cap)
+            self._resize(self.capacity_for(n, headroom))
         start = self.used
         self.used += n
         return start
 
-    def _resize(self, capacity: int) -> None:
-        old = self.tensors if self.used else None
+    def plan(self, capacity: int) -> Tuple[Dict[str, Tuple[int, Tuple[int, ...]]], int]:
+        """(name -> (byte offset, full shape), bytes) of the fields at ``capacity`` slots."""
         layout, total = {}, 0
         for name, shape in self.shapes.items():
             full = list(shape)
@@ -122,8 +125,21 @@ class PagePool:
                 nbytes *= n
             layout[name] = (total, tuple(full))
             total += -(-nbytes // self._ALIGN) * self._ALIGN
+        return layout, max(total, 1)
+
+    def place(self, buffer: torch.Tensor, layout: Dict[str, Tuple[int, Tuple[int, ...]]], capacity: int) -> None:
+        """Take ``buffer`` (uint8, on the pool's device, ``plan(capacity)``'s bytes) as the storage of a
+        pool that holds no data yet."""
+        if self.used:
+            raise RuntimeError("PagePool.place needs an empty pool")
+        self._buffer, self._layout, self._tensors, self.capacity = buffer, layout, None, capacity
+        self.generation += 1
+
+    def _resize(self, capacity: int) -> None:
+        old = self.tensors if self.used else None
+        layout, total = self.plan(capacity)
         with torch.inference_mode(False):  # kept and updated in place across calls in any mode
-            self._buffer = torch.empty(max(total, 1), dtype=torch.uint8, device=self.device)
+            self._buffer = torch.empty(total, dtype=torch.uint8, device=self.device)
         self._layout, self._tensors, self.capacity = layout, None, capacity
         if old is not None:
             for name, t in self.tensors.items():

@@ -52,7 +52,7 @@ extern "C" {
 /* Thread-local description of the last error on this thread. */
 const char* dkv_last_error(void);
 
-/* ABI version (12); bumps when a struct or an entry point below changes. */
+/* ABI version (13); bumps when a struct or an entry point below changes. */
 int dkv_abi_version(void);
 
 /*
@@ -149,6 +149,8 @@ int dkv_quantize_value_rows(const dkv_value_rows_args* args, void* stream);
  * Page p's fields start at field + p * field_page_stride (strides in bytes).
  * Replaces reference src/dart/cache.py:481-503 (`_quantize_key_pages`).
  */
+struct dkv_copy_block; /* defined with dkv_copy_token_blocks below */
+
 typedef struct dkv_key_pages_args {
   const void* src;
   int64_t src_dtype;
@@ -177,6 +179,14 @@ typedef struct dkv_key_pages_args {
    * infinity (reference src/dart/mixed.py:187-188 and
    * src/dart/quantization.py:159-160 raise ValueError); never cleared. */
   uint32_t* nonfinite;
+  /* Optional (n_copies 0: none): up to DKV_COPY_MAX_BLOCKS dense token-row
+   * copies, with the meaning dkv_copy_token_blocks gives them, made by this
+   * call too.  An append keeps its sink tokens and its held tail dense next
+   * to the pages it quantizes (reference src/dart/cache.py:183-185 and
+   * :417-418, :451-467); given here, the library runs them inside a quantize
+   * launch where one has room for them. */
+  const struct dkv_copy_block* copies;
+  int64_t n_copies;
 } dkv_key_pages_args;
 
 int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stream);
