@@ -1236,11 +1236,11 @@ __global__ void __launch_bounds__(64) key_select_pages(KeyParams k, int row_byte
 }
 
 // The key path's channel selection and a value-row job in one launch.
-// Workgroups [0, sel_blocks) select (one wave per page, as key_select_pages);
-// the next gx * gy quantize value rows (workgroup b - sel_blocks of the
-// gx x gy grid of quantize_rows_vec); the last ones make the call's dense
-// token copies, kCopyUnitsPerThread 16-byte units per thread.  A selection
-// wave mostly waits on its LDS steps; the value rows use each SIMD meanwhile.
+// The first workgroups make the call's dense token copies
+// (kCopyUnitsPerThread units per thread), the next sel_blocks select (one
+// wave per page, as key_select_pages) and the last gx * gy quantize value rows
+// (the gx x gy grid of quantize_rows_vec).  A selection wave mostly waits on
+// its LDS steps; the copies and the value rows use each SIMD meanwhile.
 // (Spreading the selection workgroups among the value rows' was slower: a
 // selection wave's chain of dependent steps stretches when VALU-bound row
 // waves share its SIMD.)
@@ -1265,26 +1265,27 @@ template <int BITS, int SRC, int E>
 __global__ void __launch_bounds__(kThreads) select_pages_and_rows(KeyParams k, int row_bytes, int64_t items,
                                                                   int64_t sel_blocks, RowsParams p, int lpg,
                                                                   int row_shift, int64_t gx, int64_t gy,
-                                                                  dkv::CopyParams cp) {
+                                                                  dkv::CopyParams cp, int64_t copy_blocks) {
   __shared__ SelectLds l[kSelectWaves];
-  if ((int64_t)blockIdx.x < sel_blocks) {
+  if ((int64_t)blockIdx.x < copy_blocks) {
+    const int64_t u0 = (int64_t)blockIdx.x * kThreads * kCopyUnitsPerThread + threadIdx.x;
+    const int64_t units = cp.first[cp.n];
+#pragma unroll
+    for (int i = 0; i < kCopyUnitsPerThread; ++i) {
+      const int64_t u = u0 + (int64_t)i * kThreads;
+      if (u < units) dkv::copy_token_unit(cp, u);
+    }
+    return;
+  }
+  const int64_t sb = (int64_t)blockIdx.x - copy_blocks;
+  if (sb < sel_blocks) {
     const int wave = threadIdx.x >> 6;
-    const int64_t item = (int64_t)blockIdx.x * kSelectWaves + wave;
+    const int64_t item = sb * kSelectWaves + wave;
     if (item < items) select_page(k, row_bytes, item, threadIdx.x & 63, l[wave]);
     return;
   }
-  const int64_t b = (int64_t)blockIdx.x - sel_blocks;
-  if (b < gx * gy) {
-    rows_vec_body<BITS, SRC, E>(p, lpg, row_shift, b % gx, b / gx, gx, gy);
-    return;
-  }
-  const int64_t u0 = (b - gx * gy) * kThreads * kCopyUnitsPerThread + threadIdx.x;
-  const int64_t units = cp.first[cp.n];
-#pragma unroll
-  for (int i = 0; i < kCopyUnitsPerThread; ++i) {
-    const int64_t u = u0 + (int64_t)i * kThreads;
-    if (u < units) dkv::copy_token_unit(cp, u);
-  }
+  const int64_t b = sb - sel_blocks;
+  rows_vec_body<BITS, SRC, E>(p, lpg, row_shift, b % gx, b / gx, gx, gy);
 }
 
 __host__ inline size_t key_tiled_smem(int D, int T, int G, int K, int row_bytes) {
@@ -1614,10 +1615,10 @@ extern "C" int dkv_quantize_key_pages(const dkv_key_pages_args* args, void* stre
   do {                                                                                                        \
     if (VL.epl == 16)                                                                                         \
       hipLaunchKernelGGL((select_pages_and_rows<B, T, 16>), sgrid, dim3(kThreads), 0, s, k, row_bytes, items,  \
-                         sel_blocks, VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy, CP);                           \
+                         sel_blocks, VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy, CP, copy_blocks_for(CP));    \
     else                                                                                                      \
       hipLaunchKernelGGL((select_pages_and_rows<B, T, 8>), sgrid, dim3(kThreads), 0, s, k, row_bytes, items,   \
-                         sel_blocks, VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy, CP);                           \
+                         sel_blocks, VL.p, VL.lpg, VL.row_shift, VL.gx, VL.gy, CP, copy_blocks_for(CP));    \
   } while (0)
 #define DKV_SV_BITS(T)                    \
   do {                                    \
