@@ -42,9 +42,10 @@ class DartCacheLayer(CacheLayerMixin):
     is_sliding = False
     is_compileable = False
 
-    def __init__(self, config: DartKVCacheConfig) -> None:
+    def __init__(self, config: DartKVCacheConfig, requantize_on_reorder: bool = False) -> None:
         super().__init__()
         self.dart_config = config
+        self.requantize_on_reorder = requantize_on_reorder
         self.cache = DartKVCache(config)
         self.last_update_prefill = False
 
@@ -84,21 +85,36 @@ class DartCacheLayer(CacheLayerMixin):
         self.is_initialized = False
         self.last_update_prefill = False
 
-    # Batch reordering gathers the packed bytes along the batch axis (DartKVCache.reorder_batch); the
-    # reference re-packs the selected rows from their dequantized contents instead
-    # (huggingface.py:117-127), which changes the codes of a second quantization.
+    # Batch reordering gathers the packed bytes along the batch axis (DartKVCache.reorder_batch).  With
+    # requantize_on_reorder the layer is rebuilt as the reference rebuilds it (huggingface.py:117-127): a
+    # fresh cache appends the selected rows of the materialized contents, so they are quantized again and
+    # the page lifecycle restarts from one prefill.
+    def _reorder(self, rows: torch.Tensor) -> None:
+        if not self.requantize_on_reorder:
+            self.cache.reorder_batch(rows)
+            return
+        if self.cache.shape is None:
+            return
+        keys, values = self.cache.get()
+        index = rows.to(keys.device)
+        if index.dtype == torch.bool:
+            index = index.nonzero().flatten()
+        rebuilt = DartKVCache(self.dart_config)
+        rebuilt.append(keys.index_select(0, index), values.index_select(0, index))
+        self.cache = rebuilt
+
     def reorder_cache(self, beam_idx: torch.LongTensor) -> None:
-        self.cache.reorder_batch(beam_idx)
+        self._reorder(torch.as_tensor(beam_idx))
 
     def batch_repeat_interleave(self, repeats: int) -> None:
         if self.cache.shape is not None:
             rows = torch.arange(self.cache.shape[0], device=self.cache.device)
-            self.cache.reorder_batch(rows.repeat_interleave(repeats))
+            self._reorder(rows.repeat_interleave(repeats))
 
     def batch_select_indices(self, indices: torch.Tensor) -> None:
         if self.cache.shape is not None:
             rows = torch.arange(self.cache.shape[0], device=self.cache.device)
-            self.cache.reorder_batch(rows[indices.to(rows.device) if isinstance(indices, torch.Tensor) else indices])
+            self._reorder(rows[indices.to(rows.device) if isinstance(indices, torch.Tensor) else indices])
 
     def crop(self, tokens_to_remove: int) -> None:
         raise NotImplementedError("DartHFCache pages are append-only; crop is not supported")
@@ -114,16 +130,20 @@ class DartHFCache(Cache):
 
     is_compileable = False
 
-    def __init__(self, config: Optional[DartKVCacheConfig] = None) -> None:
+    def __init__(self, config: Optional[DartKVCacheConfig] = None, *, requantize_on_reorder: bool = False) -> None:
+        """``requantize_on_reorder``: beam reordering and batch selection rebuild each layer from its
+        materialized rows, quantized again, exactly as the reference does (huggingface.py:117-127);
+        by default they gather the packed bytes instead (no second quantization, no pass over the cache)."""
         super().__init__(layers=[])
         self.dart_config = config or DartKVCacheConfig()
+        self.requantize_on_reorder = requantize_on_reorder
         self._seen_tokens = 0
         self.graph_epoch = 0  # bumps when batch rows move: captured decode graphs must be captured again
 
     # ---- lifecycle ----
     def _layer(self, layer_idx: int) -> DartCacheLayer:
         while len(self.layers) <= layer_idx:
-            self.layers.append(DartCacheLayer(self.dart_config))
+            self.layers.append(DartCacheLayer(self.dart_config, self.requantize_on_reorder))
         return self.layers[layer_idx]
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int,
@@ -220,7 +240,8 @@ class DartHFCache(Cache):
         return layer.page_runs(device=device, rebuild=rebuild) if layer is not None else None
 
     def reorder_cache(self, beam_idx: torch.LongTensor) -> "DartHFCache":
-        """Reorder the beams of every layer; packed pages keep their bytes (no re-quantization)."""
+        """Reorder the beams of every layer: packed pages keep their bytes, or, with
+        ``requantize_on_reorder``, every layer is rebuilt from its selected materialized rows."""
         for layer in self.layers:
             layer.reorder_cache(beam_idx)
             layer.last_update_prefill = False

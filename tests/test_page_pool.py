@@ -3,8 +3,9 @@ page tables as views of the page directory, and attention for shapes beyond the 
 
 Reordering is checked against the cache's own bytes (every packed field of every segment, row by row)
 and against the oracle on the reordered inputs; the reference re-quantizes reordered rows
-(integrations/huggingface.py:117-127), which this build deliberately does not, so the oracle comparison
-is of decode outputs, not of codes.
+(integrations/huggingface.py:117-127), which this build does not by default, so that oracle comparison
+is of decode outputs, not of codes.  The adapter's opt-in ``requantize_on_reorder`` mode rebuilds the
+layer as the reference does, and is checked bit for bit against the oracle doing the same.
 """
 
 from __future__ import annotations
@@ -211,3 +212,48 @@ def test_one_token_appends_reach_decode_after_a_decode_at_any_tail_length(start)
         cache.append(k[:, :, t:t + 1].to(DEV), v[:, :, t:t + 1].to(DEV))
         oc.append(k[:, :, t:t + 1], v[:, :, t:t + 1])
     assert cache.get_seq_length() == start + 6
+
+
+def test_hf_requantize_on_reorder_rebuilds_like_the_reference():
+    """Reference huggingface.py:117-127: each layer is rebuilt from index_select of its materialized rows,
+    so the selected rows are quantized again from one prefill; every packed field and the materialized
+    contents match an oracle cache rebuilt the same way, bit for bit."""
+    import dartkv_amd as dart
+    from dartkv_amd.integrations import DartHFCache
+    from dartkv_amd import synthetic
+    from oracle import dart_oracle as O
+    cfg = dict(bits=2, page_size=16, key_group_size=16, value_group_size=16, promote_ratio=0.25, sink_tokens=3,
+               hold_partial_pages=True, metadata_dtype=torch.float16)
+    k, v, _ = synthetic.outlier_kv(4, 2, 53, 32, dtype=torch.bfloat16, seed=11)
+    hf = DartHFCache(dart.DartKVCacheConfig(**cfg), requantize_on_reorder=True)
+    oc = O.OracleCache(O.OracleConfig(**cfg))
+    hf.update(k[:, :, :50].to(DEV), v[:, :, :50].to(DEV), 0)
+    oc.append(k[:, :, :50], v[:, :, :50])
+    for t in range(50, 53):  # one-token updates that leave a held tail
+        hf.update(k[:, :, t:t + 1].to(DEV), v[:, :, t:t + 1].to(DEV), 0)
+        oc.append(k[:, :, t:t + 1], v[:, :, t:t + 1])
+    epoch = hf.graph_epoch
+    for rows in ([3, 1, 1, 0], [2, 0]):
+        if len(rows) == 4:
+            hf.reorder_cache(torch.tensor(rows))
+        else:
+            hf.batch_select_indices(torch.tensor(rows))
+        ok, ov = oc.get()
+        idx = torch.tensor(rows)
+        oc = O.OracleCache(O.OracleConfig(**cfg))
+        oc.append(ok.index_select(0, idx), ov.index_select(0, idx))
+        cache = hf.layer_for_attention(0)
+        torch.cuda.synchronize()
+        segs, osegs = cache.iter_segments(), oc.segments()
+        assert len(segs) == len(osegs)
+        for (ks, vs), (oks, ovs) in zip(segs, osegs):
+            for a, b in ((ks, oks), (vs, ovs)):
+                fa, fb = _fields(a), _fields(b)
+                assert len(fa) == len(fb)
+                for x, y in zip(fa, fb):
+                    assert bits_equal(x.cpu(), y)
+        kk, vv = cache.get()
+        ek, ev = oc.get()
+        assert bits_equal(kk.cpu(), ek) and bits_equal(vv.cpu(), ev)
+        assert hf.get_seq_length() == 53
+    assert hf.graph_epoch == epoch + 2
