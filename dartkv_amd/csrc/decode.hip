@@ -516,7 +516,8 @@ extern "C" int dkv_decode_attention(const dkv_decode_args* args, void* stream) {
                     (a.fast_value_bits == 2 || a.fast_value_bits == 4 || a.fast_value_bits == 8),
                 DKV_ERR_UNSUPPORTED, "fast uniform pages need 2, 4 or 8-bit keys and values");
       DKV_CHECK(a.fast_splits >= 1 && a.fast_splits <= 2 * fast_count, DKV_ERR_INVALID, "fast_splits out of range");
-      DKV_CHECK(dkv::uniform_decode_max_loads((int)a.fast_key_bits, (int)a.fast_value_bits) < 16,
+      DKV_CHECK(dkv::uniform_decode_max_loads((int)a.fast_key_bits, (int)a.fast_value_bits,
+                                              (int)(128 / a.fast_value_group)) < 16,
                 DKV_ERR_UNSUPPORTED, "fast uniform pages: too many loads in flight");
     }
   }

@@ -151,13 +151,28 @@ __device__ __forceinline__ half4 gather16(uint32_t wl, uint32_t wh, uint32_t rl,
 
 // Page data in three groups, each issued as soon as the previous page no
 // longer reads that LDS region.
+//
+// The small fields take as few copies as their bytes allow: each lane of a
+// copy reads its own 16 bytes and lands them at M0 + 16 lane, so one copy
+// gathers several fields into adjacent LDS regions (promoted-channel indices,
+// key scales and key zero points in one; value scales and zero points in
+// 512 gv / 1024 more).  A wave pays for every copy it issues, partial or not,
+// whatever their bytes, so five partial copies cost more than two.
 __device__ __forceinline__ void issue_small(const LdsMap& M, uint8_t* lds, const PageAddr& a, int np, int gv,
                                             int lane) {
-  copy_to_lds(lds + M.ki, (const uint8_t*)a.ki, (np * 4 + 15) / 16 * 16, lane);
-  copy_to_lds(lds + M.ks, (const uint8_t*)a.ks, 256, lane);
-  copy_to_lds(lds + M.kz, (const uint8_t*)a.kz, 256, lane);
-  copy_to_lds(lds + M.vs, (const uint8_t*)a.vs, 256 * gv, lane);
-  copy_to_lds(lds + M.vz, (const uint8_t*)a.vz, 256 * gv, lane);
+  const int ni = (np * 4 + 15) / 16;  // 16-byte lanes of the indices: M.ks = M.ki + 16 ni, M.kz = M.ks + 256
+  {
+    const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.ki));
+    const uint8_t* src = lane < ni        ? (const uint8_t*)a.ki + 16 * lane
+                         : lane < ni + 16 ? (const uint8_t*)a.ks + 16 * (lane - ni)
+                                          : (const uint8_t*)a.kz + 16 * (lane - ni - 16);
+    if (lane < ni + 32) dma16(src, dst);
+  }
+  const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.vs));  // M.vz = M.vs + 256 gv
+  for (int off = 0; off < 512 * gv; off += 1024) {
+    const int i = (off >> 4) + lane;
+    if (i < 32 * gv) dma16(i < 16 * gv ? (const uint8_t*)a.vs + 16 * i : (const uint8_t*)a.vz + 16 * (i - 16 * gv), dst + off);
+  }
 }
 __device__ __forceinline__ void issue_keys(const LdsMap& M, uint8_t* lds, const PageAddr& a, int np, int lane) {
   copy_to_lds(lds + M.kl, a.kl, 4096, lane);
@@ -168,9 +183,7 @@ __device__ __forceinline__ void issue_values(const LdsMap& M, uint8_t* lds, cons
 }
 
 // Number of copy_to_lds instructions in each staging group.
-__host__ __device__ inline int n_small_loads(int np, int gv) {
-  return ((np * 4 + 15) / 16 * 16 + 1023) / 1024 + 2 + 2 * ((256 * gv + 1023) / 1024);
-}
+__host__ __device__ inline int n_small_loads(int np, int gv) { return 1 + (512 * gv + 1023) / 1024; }
 __host__ __device__ inline int n_key_loads(int np) { return 4 + (np * 32 + 1023) / 1024; }
 
 // 4-bit key tables of the NP promoted slots: lanes (2j, 2j+1) build entries

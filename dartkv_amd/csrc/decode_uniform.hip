@@ -109,13 +109,18 @@ __host__ __device__ inline UMap umap(int kb, int vb, int gv, int rg, bool kt, bo
 // Staging: key scales and codes of a page (or half page, see above), issued
 // after the Q K of the half before it, then value codes and value scales of a
 // half page (issued after the P V of the half before it).
-__host__ __device__ inline int n_key_loads_u(int kb) { return kb * key_rows_per_stage(kb) + 2; }
-__host__ __device__ inline int n_value_loads_u(int vb) { return vb + 2; }
+// The scales and zero points of a stage share copies: each lane of a copy
+// reads its own 16 bytes, so one copy fills the adjacent scale and zero
+// regions (M.kz = M.ks + 256, M.vz = M.vs + 128 gv).
+__host__ __device__ inline int n_key_loads_u(int kb) { return kb * key_rows_per_stage(kb) + 1; }
+__host__ __device__ inline int n_value_loads_u(int vb, int gv) { return vb + (16 * gv + 63) / 64; }
 
 __device__ __forceinline__ void issue_keys_u(const UMap& M, uint8_t* lds, const PageAddr& a, int kb, int h,
                                              int lane) {
-  copy_to_lds(lds + M.ks, (const uint8_t*)a.ks, 256, lane);
-  copy_to_lds(lds + M.kz, (const uint8_t*)a.kz, 256, lane);
+  {
+    const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.ks));
+    if (lane < 32) dma16(lane < 16 ? (const uint8_t*)a.ks + 16 * lane : (const uint8_t*)a.kz + 16 * (lane - 16), dst);
+  }
   const int kf = key_rows_per_stage(kb);
   if (kf == 2) {  // whole rows: one contiguous block
     copy_to_lds(lds + M.kc, a.kl, kD * 16 * kb, lane);
@@ -132,8 +137,13 @@ __device__ __forceinline__ void issue_keys_u(const UMap& M, uint8_t* lds, const 
 __device__ __forceinline__ void issue_values_u(const UMap& M, uint8_t* lds, const PageAddr& a, int vb, int gv, int h,
                                                int lane) {
   copy_to_lds(lds + M.vc, a.vc + 16 * vb * kHalfTok * h, 16 * vb * kHalfTok, lane);
-  copy_to_lds(lds + M.vs, (const uint8_t*)a.vs + 128 * gv * h, 128 * gv, lane);
-  copy_to_lds(lds + M.vz, (const uint8_t*)a.vz + 128 * gv * h, 128 * gv, lane);
+  const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.vs));
+  const uint8_t* vs = (const uint8_t*)a.vs + 128 * gv * h;
+  const uint8_t* vz = (const uint8_t*)a.vz + 128 * gv * h;
+  for (int off = 0; off < 256 * gv; off += 1024) {
+    const int i = (off >> 4) + lane;
+    if (i < 16 * gv) dma16(i < 8 * gv ? vs + 16 * i : vz + 16 * (i - 8 * gv), dst + off);
+  }
 }
 
 // Four codes (one per byte of e, values 0..2^B - 1) -> their dequantized
@@ -339,7 +349,7 @@ __global__ void __launch_bounds__(256) decode_pages_uniform(FastParams p) {
     // the next half needs new key rows unless it is the second half of a page staged whole
     const bool keys_next = has_next && (kf == 1 || nh == 0);
     // outstanding, oldest first: key scales + codes (if staged for this half), values (this half)
-    vm_wait(n_value_loads_u(VB));
+    vm_wait(n_value_loads_u(VB, gv));
     if (hq == hp0 || kf == 1 || (hq & 1) == 0) {  // keys staged for this half: their (s, s, z, z) table
       if constexpr (KT) build_key_tables<KB, BF16>(M, lds, lane);
       else build_sz_table(lds, M.kt, M.ks, M.kz, kD, lane);
@@ -548,8 +558,8 @@ size_t uniform_decode_wave_lds_bytes(int kb, int vb, int gv) {
   return (size_t)umap(kb, vb, gv, 1, key_tables(kb, 1), use_value_tables(vb, 1, gv)).bytes;
 }
 
-int uniform_decode_max_loads(int kb, int vb) {
-  return n_key_loads_u(kb) > n_value_loads_u(vb) ? n_key_loads_u(kb) : n_value_loads_u(vb);
+int uniform_decode_max_loads(int kb, int vb, int gv) {
+  return n_key_loads_u(kb) > n_value_loads_u(vb, gv) ? n_key_loads_u(kb) : n_value_loads_u(vb, gv);
 }
 
 template <int G, int K, int V>

@@ -31,7 +31,7 @@ int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, i
 // Uniform pages (KB-bit keys along tokens, VB-bit values along channels):
 // the largest load count one wait must cover, and the launch (splits over
 // half pages).
-int uniform_decode_max_loads(int kb, int vb);
+int uniform_decode_max_loads(int kb, int vb, int gv);
 int launch_uniform_decode(const dkv_decode_args& a, int first, int count, int kb, int vb, int vg, int splits,
                           int split_stride, hipStream_t stream, const FusedRest* fused = nullptr);
 // LDS bytes of one wave of the uniform page kernel.
