@@ -74,3 +74,19 @@ def test_ctypes_structs_match_the_header(tmp_path):
         assert got[(cname, "size")] == ctypes.sizeof(cls), cname
         for field, _ in cls._fields_:
             assert got[(cname, field)] == getattr(cls, field).offset, (cname, field)
+
+
+def test_build_rejects_page_kernels_that_use_scratch():
+    """The build reads hipcc's kernel-resource-usage remarks for the page-kernel sources and fails when a
+    kernel spills to scratch memory (private memory in HBM), which would add traffic to the page loops."""
+    from dartkv_amd import build as B
+    remarks = "\n".join([
+        "a.hip:1:1: remark: Function Name: _Z6spillsv [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:1:1: remark:     VGPRs: 168 [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:1:1: remark:     ScratchSize [bytes/lane]: 8 [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:1:1: remark: Function Name: _Z5cleanv [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:1:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert B.scratch_kernels(remarks) == ["_Z6spillsv"]
+    assert B.scratch_kernels("") == []
+    assert {"decode_fast.hip", "decode_uniform.hip"} <= B.NO_SCRATCH <= set(B.SOURCES)
