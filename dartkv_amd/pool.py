@@ -177,11 +177,13 @@ class PagePool:
                 s = list(shape)
                 s[self.batch_axis] = index.numel()
                 self.shapes[name] = tuple(s)
+            self._buffer = None  # the fields are now tensors of their own: the old allocation can go
             self.generation += 1
 
     def to(self, device: torch.device) -> None:
         with torch.inference_mode(False):
             self._tensors = {name: t.to(device) for name, t in self.tensors.items()}
+        self._buffer = None  # the views keep what they still use; a copied-out allocation can go
         self.device = device
         self.generation += 1
 

@@ -257,3 +257,22 @@ def test_hf_requantize_on_reorder_rebuilds_like_the_reference():
         assert bits_equal(kk.cpu(), ek) and bits_equal(vv.cpu(), ev)
         assert hf.get_seq_length() == 53
     assert hf.graph_epoch == epoch + 2
+
+
+def test_shrinking_batch_selection_frees_the_old_pool_allocation():
+    """Selecting fewer batch rows gathers every pool field into tensors of their own; the pool's old
+    allocation (all fields of every row) is then released, not kept until the pool next grows."""
+    cache, k, v, q = _cache(4, 700)
+    kpool, vpool = cache._key_pool, cache._value_pool
+    old_bytes = sum(p._buffer.numel() for p in (kpool, vpool) if p._buffer is not None)
+    assert old_bytes > 0
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    cache.reorder_batch([2])
+    torch.cuda.synchronize()
+    after = torch.cuda.memory_allocated()
+    assert kpool._buffer is None and vpool._buffer is None
+    assert before - after >= old_bytes // 2, (before, after, old_bytes)
+    import dartkv_amd as dart
+    out = dart.decode_attention(q[[2]], cache)  # the selected row still decodes
+    assert torch.isfinite(out.float()).all()
