@@ -25,6 +25,7 @@ from __future__ import annotations
 import contextlib
 import ctypes
 import threading
+import time
 from dataclasses import dataclass, fields as dataclass_fields
 from itertools import accumulate
 from typing import TYPE_CHECKING, List, Optional, Tuple, Union
@@ -151,10 +152,14 @@ def _nonfinite_flags(device: torch.device) -> torch.Tensor:
     return t
 
 
+_DRAIN_SPIN_S = 1e-3  # poll this long, then block (a long append does not keep a CPU core busy)
+
+
 def _drain(device: torch.device) -> None:
     """Wait until the device's current stream has run everything enqueued so far, by polling an event
     recorded on it: the wait ends within a few microseconds of the GPU finishing, where a blocking
-    stream synchronization returns about 10-15 µs later (measured on MI355X)."""
+    stream synchronization returns about 10-15 µs later (measured on MI355X).  Work still running
+    after ``_DRAIN_SPIN_S`` of polling is waited for with a blocking synchronization."""
     events = getattr(_flag_store, "events", None)
     if events is None:
         events = _flag_store.events = {}
@@ -162,8 +167,11 @@ def _drain(device: torch.device) -> None:
     if ev is None:
         ev = events[device] = torch.cuda.Event()
     ev.record(torch.cuda.current_stream(device))
+    t0 = time.perf_counter()
     while not ev.query():
-        pass
+        if time.perf_counter() - t0 > _DRAIN_SPIN_S:
+            ev.synchronize()
+            return
 
 
 def _storage(shape, dtype: torch.dtype, device) -> torch.Tensor:
