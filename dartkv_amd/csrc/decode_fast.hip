@@ -163,18 +163,18 @@ __device__ __forceinline__ void issue_small(const LdsMap& M, uint8_t* lds, const
   const int ni = (np * 4 + 15) / 16;  // 16-byte lanes of the indices: M.ks = M.ki + 16 ni, M.kz = M.ks + 256
   {
     // lane -> its field's base plus 16 (lane - first lane of the field), as
-    // wave-uniform pointer differences (a select chain became a table in scratch)
+    // wave-uniform byte distances (a select chain became a table in scratch)
     const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.ki));
-    const int64_t to_ks = (const uint8_t*)a.ks - ((const uint8_t*)a.ki + 16 * ni);
-    const int64_t to_kz = (const uint8_t*)a.kz - ((const uint8_t*)a.ks + 256);
-    const uint8_t* src = (const uint8_t*)a.ki + 16 * lane + (lane >= ni ? to_ks : 0) + (lane >= ni + 16 ? to_kz : 0);
+    const int64_t to_ks = byte_gap(a.ks, a.ki) - 16 * ni;
+    const int64_t to_kz = byte_gap(a.kz, a.ks) - 256;
+    const uint8_t* src = byte_at(a.ki, 16 * lane + (lane >= ni ? to_ks : 0) + (lane >= ni + 16 ? to_kz : 0));
     if (lane < ni + 32) dma16(src, dst);
   }
   const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.vs));  // M.vz = M.vs + 256 gv
   for (int off = 0; off < 512 * gv; off += 1024) {
     const int i = (off >> 4) + lane;
-    const int64_t to_vz = (const uint8_t*)a.vz - ((const uint8_t*)a.vs + 256 * gv);
-    if (i < 32 * gv) dma16((const uint8_t*)a.vs + 16 * i + (i >= 16 * gv ? to_vz : 0), dst + off);
+    const int64_t to_vz = byte_gap(a.vz, a.vs) - 256 * gv;
+    if (i < 32 * gv) dma16(byte_at(a.vs, 16 * i + (i >= 16 * gv ? to_vz : 0)), dst + off);
   }
 }
 __device__ __forceinline__ void issue_keys(const LdsMap& M, uint8_t* lds, const PageAddr& a, int np, int lane) {

@@ -119,8 +119,8 @@ __device__ __forceinline__ void issue_keys_u(const UMap& M, uint8_t* lds, const 
                                              int lane) {
   {
     const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.ks));
-    const int64_t to_kz = (const uint8_t*)a.kz - ((const uint8_t*)a.ks + 256);
-    if (lane < 32) dma16((const uint8_t*)a.ks + 16 * lane + (lane >= 16 ? to_kz : 0), dst);
+    const int64_t to_kz = byte_gap(a.kz, a.ks) - 256;
+    if (lane < 32) dma16(byte_at(a.ks, 16 * lane + (lane >= 16 ? to_kz : 0)), dst);
   }
   const int kf = key_rows_per_stage(kb);
   if (kf == 2) {  // whole rows: one contiguous block
@@ -139,11 +139,10 @@ __device__ __forceinline__ void issue_values_u(const UMap& M, uint8_t* lds, cons
                                                int lane) {
   copy_to_lds(lds + M.vc, a.vc + 16 * vb * kHalfTok * h, 16 * vb * kHalfTok, lane);
   const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds + M.vs));
-  const uint8_t* vs = (const uint8_t*)a.vs + 128 * gv * h;
-  const uint8_t* vz = (const uint8_t*)a.vz + 128 * gv * h;
+  const int64_t to_vz = byte_gap(a.vz, a.vs) - 128 * gv;  // the half's zero points follow its scales
   for (int off = 0; off < 256 * gv; off += 1024) {
     const int i = (off >> 4) + lane;
-    if (i < 16 * gv) dma16(vs + 16 * i + (i >= 8 * gv ? vz - (vs + 128 * gv) : 0), dst + off);
+    if (i < 16 * gv) dma16(byte_at(a.vs, 128 * gv * h + 16 * i + (i >= 8 * gv ? to_vz : 0)), dst + off);
   }
 }
 

@@ -129,6 +129,16 @@ __device__ __forceinline__ void dense_worker(const FastParams& p, int dw, int la
                       lds + kDenseDim * MG);
 }
 
+// A gathered copy's lanes move from one page field to another (possibly in
+// another allocation) by wave-uniform byte distances; the addresses are
+// formed as integers, which pointer arithmetic across objects does not express.
+__device__ __forceinline__ int64_t byte_gap(const void* to, const void* from) {
+  return (int64_t)((uintptr_t)to - (uintptr_t)from);
+}
+__device__ __forceinline__ const uint8_t* byte_at(const void* base, int64_t off) {
+  return (const uint8_t*)((uintptr_t)base + (uint64_t)off);
+}
+
 struct PageAddr {
   const uint8_t *kl, *kh, *vc;
   const int32_t* ki;
