@@ -40,6 +40,7 @@
 // The partial state goes to the workspace and the shared merge pass finishes.
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <stdlib.h>
 
 #include "dkv_capi_util.h"
 #include "dkv_decode.h"
@@ -222,22 +223,41 @@ __device__ __forceinline__ void build_lut16_tables(const LdsMap& M, uint8_t* lds
 // scalar register, sel2 = 0x04000400 in a vector register.  All eight B
 // operands are formed before the MFMAs issue, so no MFMA waits on the VALU
 // result it reads.
-// wk[j]: the B operand of channel tile j (j < 8).
+// wk[j]: the B operand of channel tile j (j < 8).  With W = 4 (a channel-split
+// wave) only tiles k0 and k0 + 4, as wk[0] and wk[1].
+template <int W>
 __device__ __forceinline__ void lut_block_operands(const uint32_t x[4], const uint32_t lo[4], const uint32_t hi[4],
-                                                   uint2 wk[8], uint32_t m3, uint32_t sel2) {
+                                                   uint2 wk[8 / W], uint32_t m3, uint32_t sel2, int k0) {
   const uint32_t y0 = perm(x[1], x[0], 0x05010400u);
   const uint32_t y1 = perm(x[3], x[2], 0x05010400u);
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int kk = 0; kk < 4 / W; ++kk) {
+    const int k = W > 1 ? k0 : kk;
     const uint32_t e0 = ((y0 >> (2 * k)) & m3) | sel2;
     const uint32_t e1 = ((y1 >> (2 * k)) & m3) | sel2;
     const uint32_t lp0 = perm(lo[1], lo[0], e0), hp0 = perm(hi[1], hi[0], e0);
     const uint32_t lp1 = perm(lo[3], lo[2], e1), hp1 = perm(hi[3], hi[2], e1);
-    wk[k] = make_uint2(perm(hp0, lp0, 0x05010400u), perm(hp1, lp1, 0x05010400u));
-    wk[k + 4] = make_uint2(perm(hp0, lp0, 0x07030602u), perm(hp1, lp1, 0x07030602u));
+    wk[kk] = make_uint2(perm(hp0, lp0, 0x05010400u), perm(hp1, lp1, 0x05010400u));
+    wk[kk + 4 / W] = make_uint2(perm(hp0, lp0, 0x07030602u), perm(hp1, lp1, 0x07030602u));
   }
 }
 
+
+// Channel-split pages (W = 4, for launches that leave most of the GPU idle):
+// the four waves of a workgroup take one split together.  Each stages the
+// whole page and builds every table, but takes a quarter of the work that
+// scales with channels: Q K channel blocks 8 w .. 8 w + 7, the promoted pairs
+// w, w + 4, ... and the P V outputs of channels 8 n + w and 8 n + w + 4.  The
+// partial logits meet in LDS (summed in wave order, so all four waves hold the
+// same S and run the same softmax), and each wave writes its channels of the
+// split's record.  A page then takes about half the time of one wave's.
+constexpr int kSplitWaves = 4;
+// Bytes of one logit-exchange buffer: every wave's S for RG row groups.
+__host__ __device__ constexpr int xchg_bytes(int rg) { return kSplitWaves * rg * 2 * 4 * 64 * 4; }
+
+// Every wave of the workgroup: this wave's LDS traffic done, then s_barrier.
+// Outstanding page copies stay in flight.
+__device__ __forceinline__ void block_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Row groups of 4 query rows for GQ rows per KV head, and waves per workgroup:
 // one-wave workgroups for 16 rows, whose LDS region (about 24 KB) leaves room
@@ -254,15 +274,20 @@ __host__ __device__ constexpr int fast_waves_per_block(int gq) { return gq > 8 ?
 // sets would not fit; four reads per operand, three of zeros, stalled on LDS
 // issue), as are the promoted pass's for any row count, and P V takes all rows
 // in one MFMA (rows 4g + i: lane group kq = g holds group g's outputs).
-template <int GQ, int NP, bool BF16>
+//
+// W: waves per split, 1 or kSplitWaves (channel-split pages, GQ <= 8).
+template <int GQ, int NP, bool BF16, int W>
 __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
     decode_pages_fast(FastParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, kq = lane >> 4;
-  const int worker = blockIdx.x * fast_waves_per_block(GQ) + wave;
+  static_assert(W == 1 || (W == kSplitWaves && fast_waves_per_block(GQ) == W), "one split per workgroup");
+  const int mw = W > 1 ? wave : 0;  // this wave's quarter of a channel-split page
   const int total_workers = p.B * p.Hkv * p.splits;
+  // page workers first (W waves each), then the dense-rest workers (one wave each)
+  const int worker = W > 1 ? (int)blockIdx.x : (int)blockIdx.x * fast_waves_per_block(GQ) + wave;
   constexpr int np = NP;
   constexpr bool bf16 = BF16;
   constexpr int RG = fast_row_groups(GQ), GH = GQ > 4 ? 4 : GQ;
@@ -271,7 +296,8 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
   const LdsMap M = lds_map(np, gv, RG);
   uint8_t* lds = smem + wave * M.bytes;
   if (worker >= total_workers) {  // a dense-rest worker, or none
-    dense_worker<GQ, BF16>(p, worker - total_workers, lane, (float*)lds);
+    const int dw = W > 1 ? (worker - total_workers) * W + wave : worker - total_workers;
+    dense_worker<GQ, BF16>(p, dw, lane, (float*)lds);
     return;
   }
   // wave-uniform indices (kept in scalar registers)
@@ -307,7 +333,7 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
   // S (slot layout): lane (n, kq) holds rows 4g + 0..3 of tokens 32(n/4) + 16t + 4kq + n%4 in S[g][t].
   // O (rows in rows): lanes kq = g hold rows 4g + 0..3 of channels 8n + j in O[j].
   float m_run[RG][4], l_part[RG][4];
-  float4v O[8];
+  float4v O[8 / W];  // channel-split waves: channels 8n + mw (O[0]) and 8n + mw + 4 (O[1])
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
 #pragma unroll
@@ -317,7 +343,7 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
     }
   }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) O[j] = float4v{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < 8 / W; ++j) O[j] = float4v{0.f, 0.f, 0.f, 0.f};
 
   int qexp;  // the query's power-of-two scale (query_exponent)
   {
@@ -337,12 +363,14 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
   // Q K A operands for channel blocks cb = 0..31 (natural channel order), kept
   // in registers for the whole split: q[head][4cb + kq] at half `slot` (with
   // one row group; with two they are read from q16 per MFMA, qsrc).
-  half4 qa[RG == 1 ? kD / 4 : 1];
+  // (a channel-split wave keeps its own blocks cb0 .. cb0 + kD / 4 / W - 1)
+  const int cb0 = kD / 4 / W * mw;
+  half4 qa[RG == 1 ? kD / 4 / W : 1];
   if constexpr (RG == 1) {
     const uint16_t* q16 = (const uint16_t*)(lds + M.q16);
 #pragma unroll
-    for (int cb = 0; cb < kD / 4; ++cb) {
-      const _Float16 v = __builtin_bit_cast(_Float16, q16[head * kD + 4 * cb + kq]);
+    for (int cb = 0; cb < kD / 4 / W; ++cb) {
+      const _Float16 v = __builtin_bit_cast(_Float16, q16[head * kD + 4 * (cb0 + cb) + kq]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) qa[cb][i] = i == slot ? v : (_Float16)0.f;
     }
@@ -398,12 +426,32 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
     // passes need (value tables, 4-bit key tables, the promoted channels'
     // query) are built in between, so their LDS latency overlaps the lookups.
     {
-      const int row = M.kl + 32 * kq + qd;
-      const int tab = M.klut + 16 * kq;
+      // a channel-split wave takes pairs u0 .. u0 + NU - 1 (its qa blocks)
+      constexpr int NU = kD / 8 / W;
+      const int u0 = NU * mw;
+      const int row = M.kl + 32 * kq + qd + 256 * u0;
+      const int tab = M.klut + 16 * kq + 64 * u0;
       const uint16_t* vs = (const uint16_t*)(lds + M.vs);
       const uint16_t* vz = (const uint16_t*)(lds + M.vz);
-      uint2 wc[kD / 4];
-      uint4 t[kD / 8];
+      if constexpr (W > 1) {
+        // every table, before this wave's share of the lookups
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int tt = lane + 64 * (k & 1), g = (k >> 1) % gv;
+          *(uint2*)(lds + M.vlut + kVlutStride * g + 8 * kpos(tt)) = build_lut4<bf16>(vs[tt * gv + g], vz[tt * gv + g]);
+        }
+        build_lut16_tables<bf16, np>(M, lds, ks, kz, lane);
+        const uint16_t* q16 = (const uint16_t*)(lds + M.q16);
+        const uint8_t* pidx = lds + M.pidx;
+        uint16_t* qp = (uint16_t*)(lds + M.qp);
+#pragma unroll
+        for (int i = lane; i < GQ * np; i += 64) {
+          const int h = i / np, j = i % np;
+          qp[h * (kQpStride / 2) + j] = q16[h * kD + pidx[j]];
+        }
+      }
+      uint2 wc[2 * NU];
+      uint4 t[NU];
       auto load_pair = [&](int u) {
         wc[2 * u] = *(const uint2*)(lds + row + 256 * u);
         wc[2 * u + 1] = *(const uint2*)(lds + row + 256 * u + 128);
@@ -411,8 +459,8 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
       };
       load_pair(0);
 #pragma unroll
-      for (int u = 0; u < kD / 8; ++u) {
-        if (u + 1 < kD / 8) load_pair(u + 1);
+      for (int u = 0; u < NU; ++u) {
+        if (u + 1 < NU) load_pair(u + 1);
         const half4 b0e = lookup4((wc[2 * u].x >> sh) & 0x03030303u, t[u].x, t[u].y);
         const half4 b1e = lookup4((wc[2 * u].y >> sh) & 0x03030303u, t[u].x, t[u].y);
         const half4 b0o = lookup4((wc[2 * u + 1].x >> sh) & 0x03030303u, t[u].z, t[u].w);
@@ -423,21 +471,21 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
         } else {
 #pragma unroll
           for (int g = 0; g < RG; ++g) {
-            const half4 a0 = slot_a(*(const uint16_t*)(lds + qsrc[g] + 16 * u), asel);
-            const half4 a1 = slot_a(*(const uint16_t*)(lds + qsrc[g] + 16 * u + 8), asel);
+            const half4 a0 = slot_a(*(const uint16_t*)(lds + qsrc[g] + 16 * (u0 + u)), asel);
+            const half4 a1 = slot_a(*(const uint16_t*)(lds + qsrc[g] + 16 * (u0 + u) + 8), asel);
             S[g][0] = mma2(a0, a1, b0e, b0o, S[g][0]);
             S[g][1] = mma2(a0, a1, b1e, b1o, S[g][1]);
           }
         }
-        if (u % 2 == 0 && u / 2 < 4) {
+        if (W == 1 && u % 2 == 0 && u / 2 < 4) {
           // value table k = u / 2 of this lane: token lane + 64 (k & 1), group k >> 1
           // (groups beyond gv rebuild an existing table with identical contents)
           const int k = u / 2;
           const int tt = lane + 64 * (k & 1), g = (k >> 1) % gv;
           *(uint2*)(lds + M.vlut + kVlutStride * g + 8 * kpos(tt)) = build_lut4<bf16>(vs[tt * gv + g], vz[tt * gv + g]);
         }
-        if (u == 9) build_lut16_tables<bf16, np>(M, lds, ks, kz, lane);
-        if (u == 13) {
+        if (W == 1 && u == 9) build_lut16_tables<bf16, np>(M, lds, ks, kz, lane);
+        if (W == 1 && u == 13) {
           const uint16_t* q16 = (const uint16_t*)(lds + M.q16);
           const uint8_t* pidx = lds + M.pidx;
           uint16_t* qp = (uint16_t*)(lds + M.qp);
@@ -463,6 +511,38 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
       const uint32_t rl = (uint32_t)(sh - 1) & 31u, rh = (uint32_t)(sh - 3) & 31u;
       const uint32_t kq32 = 0x20202020u * (uint32_t)kq;
       const uint32_t m6 = in_sgpr(0x06060606u), m18 = in_sgpr(0x18181818u);
+      if constexpr (W > 1) {
+        // block pairs (2 pp, 2 pp + 1) for pp = mw, mw + W, ...: the pair's
+        // tables start at tab16 + 256 pp (low byte still zero), the odd
+        // block's 128 bytes on
+        constexpr int NPP = np / 8;
+#pragma unroll
+        for (int i = 0; i < (NPP + W - 1) / W; ++i) {
+          const int pp = mw + W * i;
+          if (pp < NPP) {
+            uint2 wlp[2], whp[2];
+            half4 ap[2][RG];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const int j = 4 * (2 * pp + e) + kq;
+              wlp[e] = *(const uint2*)(lds + M.kl + 32 * pidx[j] + qd);
+              whp[e] = *(const uint2*)(lds + M.kh + 32 * j + qd);
+#pragma unroll
+              for (int g = 0; g < RG; ++g) ap[e][g] = slot_a(*(const uint16_t*)(lds + psrc[g] + 8 * (2 * pp + e)), asel);
+            }
+            const uint32_t tabp = tab16 + 256u * (uint32_t)pp;
+            const half4 b00 = gather16(wlp[0].x, whp[0].x, rl, rh, kq32, tabp, 0, m6, m18);
+            const half4 b01 = gather16(wlp[0].y, whp[0].y, rl, rh, kq32, tabp, 0, m6, m18);
+            const half4 b10 = gather16(wlp[1].x, whp[1].x, rl, rh, kq32, tabp, 128, m6, m18);
+            const half4 b11 = gather16(wlp[1].y, whp[1].y, rl, rh, kq32, tabp, 128, m6, m18);
+#pragma unroll
+            for (int g = 0; g < RG; ++g) {
+              S[g][0] = mma2(ap[0][g], ap[1][g], b00, b10, S[g][0]);
+              S[g][1] = mma2(ap[0][g], ap[1][g], b01, b11, S[g][1]);
+            }
+          }
+        }
+      } else {
       uint2 wl[np / 4], wh[np / 4];  // .x: tile 0, .y: tile 1
       auto load_pb = [&](int pb) {
         const int j = 4 * pb + kq;
@@ -492,8 +572,32 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
           pend1 = b1;
         }
       }
+      }
     }
     lds_sync();
+    if constexpr (W > 1) {
+      // the waves' partial logits, summed in wave order (two buffers by page
+      // parity: a wave one page ahead writes the other one)
+      float* xs = (float*)(smem + kSplitWaves * M.bytes + xchg_bytes(RG) * (pg & 1));
+#pragma unroll
+      for (int g = 0; g < RG; ++g)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xs[(((mw * RG + g) * 2 + t) * 4 + i) * 64 + lane] = S[g][t][i];
+      block_lds_barrier();
+#pragma unroll
+      for (int g = 0; g < RG; ++g)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float acc = xs[((g * 2 + t) * 4 + i) * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < W; ++w) acc += xs[(((w * RG + g) * 2 + t) * 4 + i) * 64 + lane];
+            S[g][t][i] = acc;
+          }
+    }
     if (has_next) {
       issue_small(M, lds, nxt, np, gv, lane);
       issue_keys(M, lds, nxt, np, lane);
@@ -531,7 +635,7 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
 #pragma unroll
           for (int g = 1; g < RG; ++g) al = kq == g ? alpha[g][i] : al;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) O[j][i] *= al;
+          for (int j = 0; j < 8 / W; ++j) O[j][i] *= al;
         }
       }
       uint16_t* pt = (uint16_t*)(lds + M.pt);
@@ -570,20 +674,20 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
         lo[blk][2] = t23.x; hi[blk][2] = t23.y; lo[blk][3] = t23.z; hi[blk][3] = t23.w;
       };
       load_blk(0);
-      uint2 wprev[8];  // even block's B operands, waiting for the odd one
+      uint2 wprev[8 / W];  // even block's B operands, waiting for the odd one
 #pragma unroll
       for (int blk = 0; blk < kPage / 16; ++blk) {
         if (blk + 1 < kPage / 16) load_blk(blk + 1);
-        uint2 wk[8];
-        lut_block_operands(x[blk], lo[blk], hi[blk], wk, m3, sel2);
+        uint2 wk[8 / W];
+        lut_block_operands<W>(x[blk], lo[blk], hi[blk], wk, m3, sel2, mw);
         if (blk & 1) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
+          for (int j = 0; j < 8 / W; ++j)
             O[j] = mma2(a[blk - 1], a[blk], __builtin_bit_cast(half4, wprev[j]), __builtin_bit_cast(half4, wk[j]),
                         O[j]);
         } else {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) wprev[j] = wk[j];
+          for (int j = 0; j < 8 / W; ++j) wprev[j] = wk[j];
         }
       }
     }
@@ -599,13 +703,18 @@ __global__ void __launch_bounds__(64 * fast_waves_per_block(GQ), 2)
       const float l = wave_sum64(l_part[g][i]);
       const int hq = kvh * GQ + 4 * g + i;
       float* rec = p.ws + (((int64_t)b * p.Hq + hq) * p.split_stride + split) * (kD + 2);
-      if (lane == 0) {
+      if (lane == 0 && mw == 0) {
         rec[0] = (tab16 & 255u) == 0 ? m_run[g][i] * kLn2 : NAN;
         rec[1] = l;
       }
       if (kq == g) {
+        if constexpr (W == 1) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) rec[2 + 8 * n + j] = O[j][i];
+          for (int j = 0; j < 8; ++j) rec[2 + 8 * n + j] = O[j][i];
+        } else {
+          rec[2 + 8 * n + mw] = O[0][i];
+          rec[6 + 8 * n + mw] = O[1][i];
+        }
       }
     }
   }
@@ -619,6 +728,20 @@ int fast_decode_max_loads(int np, int gv) { return n_small_loads(np, gv) + n_key
 
 size_t fast_decode_lds_bytes(int np, int gv, int gq) {
   return (size_t)fast_waves_per_block(gq) * lds_map(np, gv, fast_row_groups(gq)).bytes;
+}
+
+// Compute units of the current device (read once per device).
+static int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static int cus[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
 }
 
 int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, int vg, int splits, int split_stride,
@@ -644,15 +767,38 @@ int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, i
   p.q_sh = a.q_sh;
   p.ws = (float*)a.workspace;
   set_fused(p, fused);
-  const int64_t workers = (int64_t)p.B * p.Hkv * splits + p.dense_workers;
+  const int64_t page_workers = (int64_t)p.B * p.Hkv * splits;
   const int wpb = fast_waves_per_block(p.GQ);
-  const unsigned blocks = (unsigned)((workers + wpb - 1) / wpb);
-  const size_t lds = fast_decode_lds_bytes(np, p.gv, p.GQ);
+  // Channel-split pages when every workgroup of that launch (one split each,
+  // then the dense-rest waves four to a workgroup) has a compute unit to
+  // itself: the launch leaves most of the GPU idle, and a page's latency
+  // bounds the call.  DKV_SPLIT_PAGES=0 / 1 in the environment turns them off
+  // / on for every launch that can take them (tests compare the two).
+  const int64_t split_blocks = page_workers + (p.dense_workers + kSplitWaves - 1) / kSplitWaves;
+  const char* force = getenv("DKV_SPLIT_PAGES");
+  bool split_pages = false;
+  if (wpb == kSplitWaves) {
+    if (force != nullptr && force[0] != '\0') {
+      split_pages = force[0] != '0';
+    } else {
+      const int cus = device_cus();
+      split_pages = cus > 0 && split_blocks <= cus;
+    }
+  }
+  const unsigned blocks =
+      (unsigned)(split_pages ? split_blocks : (page_workers + p.dense_workers + wpb - 1) / wpb);
+  const size_t lds = fast_decode_lds_bytes(np, p.gv, p.GQ) +
+                     (split_pages ? (size_t)2 * xchg_bytes(fast_row_groups(p.GQ)) : 0);
   const dim3 grid(blocks), block(64 * wpb);
-#define DKV_FAST_LAUNCH(G, N)                                                                  \
-  do {                                                                                         \
-    if (p.bf16) hipLaunchKernelGGL((decode_pages_fast<G, N, true>), grid, block, lds, stream, p);  \
-    else hipLaunchKernelGGL((decode_pages_fast<G, N, false>), grid, block, lds, stream, p);        \
+#define DKV_FAST_LAUNCH(G, N)                                                                             \
+  do {                                                                                                    \
+    if (split_pages && G <= 8) {                                                                          \
+      if (p.bf16) hipLaunchKernelGGL((decode_pages_fast<G, N, true, G <= 8 ? kSplitWaves : 1>), grid, block, lds, stream, p); \
+      else hipLaunchKernelGGL((decode_pages_fast<G, N, false, G <= 8 ? kSplitWaves : 1>), grid, block, lds, stream, p);      \
+    } else {                                                                                              \
+      if (p.bf16) hipLaunchKernelGGL((decode_pages_fast<G, N, true, 1>), grid, block, lds, stream, p);    \
+      else hipLaunchKernelGGL((decode_pages_fast<G, N, false, 1>), grid, block, lds, stream, p);          \
+    }                                                                                                     \
   } while (0)
 #define DKV_FAST_NP(G)                         \
   switch (np) {                                \

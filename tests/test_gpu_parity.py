@@ -437,6 +437,37 @@ def test_fast_page_kernel_vs_oracle_and_general(B, Hkv, Hq, T, dtype, vg, ratio)
     assert e_fast <= 2e-3
 
 
+@pytest.mark.parametrize("B,Hkv,Hq,T,dtype,vg,ratio", [
+    (1, 8, 32, 1024, torch.bfloat16, 64, 0.25),    # config 2
+    (2, 2, 4, 1500, torch.float16, 32, 0.25),      # GQA 2, fp16 cache, value group 32
+    (2, 4, 4, 700, torch.bfloat16, 128, 0.25),     # GQA 1, value group 128
+    (2, 4, 32, 1300, torch.bfloat16, 64, 0.25),    # GQA 8: two row groups
+    (1, 2, 16, 800, torch.bfloat16, 64, 0.5),      # GQA 8, 64 promoted channels
+    (2, 2, 16, 600, torch.bfloat16, 16, 0.125),    # GQA 8, 16 promoted channels, value group 16
+    (1, 2, 8, 900, torch.float16, 64, 0.375),      # 48 promoted channels
+])
+def test_channel_split_pages_agree_with_whole_pages(monkeypatch, B, Hkv, Hq, T, dtype, vg, ratio):
+    """Pages shared by four waves (each a quarter of the channels, partial logits summed in LDS) give the
+    oracle's answer, and the whole-page kernel's up to the fp16 rounding of the softmax weights."""
+    dart = _dkv()
+    cache, q, ref32 = _oracle_and_cache(B, Hkv, Hq, T, dtype, seed=11 + T, value_group_size=vg, promote_ratio=ratio)
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("DKV_SPLIT_PAGES", mode)
+        for splits in (None, 1, 3):
+            o = torch.empty(B, Hq, 128, dtype=torch.float32, device=DEV)
+            dart.decode_attention(q, cache, out_f32=o, n_splits=splits, fast=True)
+            torch.cuda.synchronize()
+            outs[mode, splits] = o.cpu()
+    for key, o in outs.items():
+        e = rel_err(o.unsqueeze(2), ref32)
+        d = rel_err(o.unsqueeze(2), outs["0", key[1]].unsqueeze(2))
+        print("case", B, Hkv, Hq, T, dtype, vg, ratio, "split pages", key, "rel err", e, "vs whole pages", d,
+              flush=True)
+        assert e <= 2e-3
+        assert d <= 1e-3
+
+
 def test_fast_page_kernel_split_counts_agree():
     """Every split count gives the same answer.
 
