@@ -10,7 +10,9 @@
 // (decode.hip).
 //
 // One wave owns one split: a contiguous range of pages of one (batch, kv
-// head).  Per page the wave
+// head).  (Launches that leave most of the GPU idle give a split four waves,
+// each a quarter of the page's channels: "channel-split pages" below.)  Per
+// page the wave
 //   1. stages the packed page (10,880 bytes at the reference layout) in its
 //      private LDS region with global_load_lds; the next page's parts are
 //      issued as soon as the current page no longer reads their region;
@@ -18,29 +20,29 @@
 //      dequantized value of each code under the reference's rounding chain
 //      (fp16 code*scale, fp16 +zero, then the cache dtype), stored as fp16
 //      (bf16 values are exact in fp16 in its normal range) in byte planes
-//      (low bytes of the entries in one dword, high bytes in another);
-//   3. orders channels so the NP promoted channels come first (the query is
-//      permuted the same way);
-//   4. computes S = Q K and O += P V with f16 MFMAs (16x16, K = 32: two
-//      16-deep blocks per instruction) in a "slot"
-//      layout: the 16 rows of a tile are 4 slots x 4 query heads.  For Q K the
-//      16 K values of one MFMA are 4 channels x 4 slots and a slot picks one
-//      of 4 tokens, so the B values a lane holds are 4 tokens of ONE channel
-//      (one table) and the A operand carries q at the lane's slot and zeros
-//      elsewhere.  For P V a slot picks one of 4 channels of one token (one
-//      table) and A carries p at the lane's slot.  A tile then holds 64
-//      tokens x 4 heads (Q K) or 64 channels x 4 heads (P V), and every lane
-//      holds useful results;
-//   5. B values come from v_perm lookups of the 2-bit codes in the byte-plane
-//      tables (a 16-entry table read as two 8-entry halves plus a blend for
-//      the 4-bit promoted codes), so every K/V element is dequantized once;
-//   6. keeps an online softmax in base 2 whose running max only moves when a
+//      (low bytes of the entries in one dword, high bytes in another), and a
+//      16-entry table per promoted channel;
+//   3. computes S = Q K with f16 MFMAs (16x16, K = 32: two 16-deep blocks per
+//      instruction) in a "slot" layout: the 16 rows of a tile are 4 slots x 4
+//      query heads, the 16 K values of one MFMA are 4 channels x 4 slots and a
+//      slot picks one of 4 tokens, so the B values a lane holds are 4 tokens of
+//      ONE channel (one table, four v_perm lookups of the 2-bit codes) and the
+//      A operand carries q at the lane's slot and zeros elsewhere.  The
+//      promoted channels' 2-bit tables are zero; a second pass adds their
+//      4-bit products, each B element one 2-byte LDS gather from the channel's
+//      16-entry table at an address formed by byte permutes;
+//   4. keeps an online softmax in base 2 whose running max only moves when a
 //      logit exceeds it by more than 8 (so p <= 256 keeps fp16's relative
-//      precision); row sums stay per lane until the end.
+//      precision); row sums stay per lane until the end;
+//   5. computes O += P V with the query heads in the MFMA rows and 16 tokens
+//      per K block, the weights written to LDS in the blocks' K order and the
+//      value B operands looked up in the (token, group) tables.
 // The partial state goes to the workspace and the shared merge pass finishes.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdlib.h>
+
+#include <atomic>
 
 #include "dkv_capi_util.h"
 #include "dkv_decode.h"
@@ -730,18 +732,19 @@ size_t fast_decode_lds_bytes(int np, int gv, int gq) {
   return (size_t)fast_waves_per_block(gq) * lds_map(np, gv, fast_row_groups(gq)).bytes;
 }
 
-// Compute units of the current device (read once per device).
+// Compute units of the current device (read once per device; threads that
+// race on the first read store the same value).
 static int device_cus() {
   constexpr int kMaxDevices = 64;
-  static int cus[kMaxDevices] = {};
+  static std::atomic<int> cus[kMaxDevices] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-  if (cus[dev] == 0) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 int launch_fast_decode(const dkv_decode_args& a, int first, int count, int np, int vg, int splits, int split_stride,
