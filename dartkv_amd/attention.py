@@ -68,22 +68,31 @@ def page_kernel_splits(batch: int, kv_heads: int, pages: int) -> int:
     return max(1, min(pages, max(-(-2048 // bh), min(16, -(-pages // 4)))))
 
 
+_FAST_ENABLED: Optional[bool] = None
+_NO_TAIL = _lib.Segment()  # the descriptor of no held tail (read only)
+
+
 def _fast_enabled() -> bool:
-    return os.environ.get("DKV_FORCE_GENERAL", "0") in ("", "0")
+    """False when the environment sets DKV_FORCE_GENERAL (read on first use: a decode call does not pay
+    for an environment lookup)."""
+    global _FAST_ENABLED
+    if _FAST_ENABLED is None:
+        _FAST_ENABLED = os.environ.get("DKV_FORCE_GENERAL", "0") in ("", "0")
+    return _FAST_ENABLED
 
 
 _workspaces: "collections.OrderedDict[tuple, torch.Tensor]" = collections.OrderedDict()
 _MAX_WORKSPACES = 8  # (device, stream) pairs whose workspace is kept; the least recently used goes first
 
 
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+def _workspace(device: torch.device, nbytes: int, stream: Optional[int] = None) -> torch.Tensor:
     """A decode workspace for the split records: one per device and stream, kept and grown as needed (calls
     on one stream run in order, so they can share it).  At most ``_MAX_WORKSPACES`` are kept (least recently
     used dropped first; the caching allocator reuses a dropped one once the stream's work has run) and
     ``release_workspaces`` drops them all.  Under graph capture a fresh one, which the graph keeps."""
     if torch.cuda.is_current_stream_capturing():
         return torch.empty(nbytes, dtype=torch.uint8, device=device)
-    key = (device.index, _lib.stream_ptr(device))
+    key = (device.index, _lib.stream_ptr(device) if stream is None else stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = _workspaces[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
@@ -167,18 +176,23 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     """
     _lib.require_device(query)
     batch, kv_heads, head_dim = _check_query(query, cache)
-    q3 = query.reshape(query.shape[0], query.shape[1], query.shape[-1]) if query.ndim == 4 else query
+    # q3: the query as [B, Hq, D] (a [B, Hq, 1, D] query is read through its own strides 0, 1 and 3)
+    q3 = query.reshape(query.shape[0], query.shape[1], query.shape[-1]) if query.ndim == 4 and query.shape[2] != 1 \
+        else query
     if q3.stride(-1) != 1:
         q3 = q3.contiguous()
-    if query.device != cache.device:
+    device = query.device
+    if device != cache.device:
         raise ValueError("query and cache must be on the same device")
     factor = scale if scale is not None else 1.0 / math.sqrt(head_dim)
-    plan = cache.decode_plan(query.device)
-    tail = tail_segment(cache) if plan.tail_is_pending else _lib.Segment()
+    plan = cache.decode_plan(device)
+    if plan.tail_is_pending:
+        tail, dense_ok = tail_segment(cache, with_dense_check=True)
+    else:
+        tail, dense_ok = _NO_TAIL, True
     Hq = q3.shape[1]
     use_fast = ((_fast_enabled() if fast is None else fast) and plan.fast_count > 0
                 and Hq // kv_heads in _fast_rows(plan))
-    dense_ok = tail.tokens == 0 or _dense16_ok(tail)
     chunks = -(-max(plan.rest_dense, tail.tokens) // 32)
     key = (Hq, q3.dtype, q3.stride(0), q3.stride(1), use_fast, n_splits, factor, static_scratch, tail.tokens > 0,
            dense_ok, chunks)
@@ -193,7 +207,8 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
             or out.stride(-1) != 1:
         raise ValueError("out must be a [B, Hq, 1, D] tensor of the query's dtype and device, unit stride in D")
     lib = _lib.load()
-    workspace = None if static_scratch else _workspace(query.device, ws_bytes)
+    stream = _lib.stream_ptr(device)
+    workspace = None if static_scratch else _workspace(device, ws_bytes, stream)
     a = _lib.DecodeArgs.from_buffer_copy(template)
     a.query = q3.data_ptr()
     a.out = out.data_ptr()
@@ -209,9 +224,9 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     if fast_events is not None:
         a.fast_events[0], a.fast_events[1] = fast_events[0].cuda_event, fast_events[1].cuda_event
     if static_scratch:
-        _lib.check(lib.dkv_decode_attention_noalloc(a, _lib.stream_ptr(query.device)), "dkv_decode_attention_noalloc")
+        _lib.check(lib.dkv_decode_attention_noalloc(a, stream), "dkv_decode_attention_noalloc")
     else:
-        _lib.check(lib.dkv_decode_attention(a, _lib.stream_ptr(query.device)), "dkv_decode_attention")
+        _lib.check(lib.dkv_decode_attention(a, stream), "dkv_decode_attention")
     return out
 
 

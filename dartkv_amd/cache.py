@@ -410,7 +410,7 @@ class DartKVCache:
         self._finite_scope: Optional[_FiniteScope] = None
         self._copy_queue: Optional[list] = None  # an append's dense token copies, launched once at its end
         self._tail_job: Optional[tuple] = None  # _tail_copy_job of the current tail buffers
-        self._tail_desc = None  # (tail tensors' addresses and strides, their descriptor without a token count)
+        self._tail_desc = None  # [tail tensors' addresses and strides, descriptor, dense check, tokens, with them]
         self._sealed_pairs_cache: Optional[Tuple[int, list]] = None
         self._directory_cache: dict = {}
         self._decode_plan_cache: Optional[_DecodePlan] = None
@@ -1687,35 +1687,42 @@ def _rest_dense(cache: DartKVCache, descs, count: int, fast: Tuple[int, ...]) ->
     return max((d.tokens for d in rest), default=0)
 
 
-def tail_segment(cache: DartKVCache):
+def tail_segment(cache: DartKVCache, with_dense_check: bool = False):
     """Descriptor of the held tail (pending tokens in the tail buffer).
 
     With device-side tail counts the descriptor spans the whole tail buffer
     (its capacity) and the kernels read the live count from the device.  The
     descriptor of a tail is kept while its tensors keep their addresses and
-    strides (one-token appends only change the token count).
+    strides (one-token appends only change the token count), and the same
+    object is returned while the token count stays too: do not modify it.
+    ``with_dense_check`` returns (descriptor, True when it has no tokens or the
+    dense decode kernel can read it: ``_dense16_ok``).
     """
     if cache._tail_count_dev is not None:
         pk, pv = cache._tail_key, cache._tail_value
     elif cache._pending_key is None:
-        return _lib.Segment()
+        desc = _lib.Segment()
+        return (desc, True) if with_dense_check else desc
     else:
         pk, pv = cache._pending_key, cache._pending_value
     key = (pk.data_ptr(), pv.data_ptr(), pk.stride(), pv.stride())
+    tokens = pk.shape[-2]
     held = cache._tail_desc
     if held is None or held[0] != key:
-        desc = _lib.Segment()
-        desc.key_kind = _lib.KEY_DENSE
-        desc.value_kind = _lib.VALUE_DENSE
+        base = _lib.Segment()
+        base.key_kind = _lib.KEY_DENSE
+        base.value_kind = _lib.VALUE_DENSE
         keep: list = []
-        desc.key[0], desc.key_bh[0] = _dense_block(pk, keep)
-        desc.value[0], desc.value_bh[0] = _dense_block(pv, keep)
+        base.key[0], base.key_bh[0] = _dense_block(pk, keep)
+        base.value[0], base.value_bh[0] = _dense_block(pv, keep)
         if keep:
             raise RuntimeError("held tail is not in the tail buffer layout")
-        held = cache._tail_desc = (key, desc)
-    desc = _lib.Segment.from_buffer_copy(held[1])
-    desc.tokens = pk.shape[-2]
-    return desc
+        held = cache._tail_desc = [key, base, _dense16_ok(base), -1, None]
+    if held[3] != tokens:
+        desc = _lib.Segment.from_buffer_copy(held[1])
+        desc.tokens = tokens
+        held[3], held[4] = tokens, desc
+    return (held[4], tokens == 0 or held[2]) if with_dense_check else held[4]
 
 
 __all__ = ["DartKVCache", "DartKVCacheConfig", "DartPageMetadata", "DartSegmentLayout"]
