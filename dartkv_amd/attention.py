@@ -165,7 +165,7 @@ def decode_attention(query: torch.Tensor, cache: DartKVCache, *, scale: Optional
     [B, Hq, 1, D] in ``query.dtype``.  If ``out_f32`` ([B, Hq, D] fp32) is
     given it receives the result before the final cast.  ``fast`` selects
     the MFMA page kernel for the pages it supports (default: on unless the
-    environment sets DKV_FORCE_GENERAL=1); ``n_splits`` overrides the split
+    environment sets DKV_FORCE_GENERAL=1, read at the first call); ``n_splits`` overrides the split
     count of the page kernel (or of the general kernel when it does all work).
     ``fast_events`` (two recorded ``torch.cuda.Event`` objects) are recorded
     again right before and after the page kernel, to time it alone.  ``out``
