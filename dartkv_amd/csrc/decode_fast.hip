@@ -252,7 +252,7 @@ __device__ __forceinline__ void lut_block_operands(const uint32_t x[4], const ui
 // w, w + 4, ... and the P V outputs of channels 8 n + w and 8 n + w + 4.  The
 // partial logits meet in LDS (summed in wave order, so all four waves hold the
 // same S and run the same softmax), and each wave writes its channels of the
-// split's record.  A page then takes about half the time of one wave's.
+// split's record.  At C2 a wave's page then takes about 60 % of the time.
 constexpr int kSplitWaves = 4;
 // Bytes of one logit-exchange buffer: every wave's S for RG row groups.
 __host__ __device__ constexpr int xchg_bytes(int rg) { return kSplitWaves * rg * 2 * 4 * 64 * 4; }
